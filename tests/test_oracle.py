@@ -1,0 +1,234 @@
+"""Pins the CPU oracle before anything is checked against it (runs without a GPU).
+
+Each oracle function is checked against something independent of its own
+formula: a second formula (softmax vs product of sigmoids), explicit loops,
+closed-form known answers, finite differences (gradcheck), the C restatement of
+the reference's CPU kernel, the reference's own compiled kernel (oracle/_ref,
+when built) and golden vectors written by the reference (tests/golden).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle_c, race_cpu_port
+from oracle import race_oracle as orc
+
+F64 = torch.float64
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "soft_hash_golden.npz")
+
+
+def softmax_probs(N, T, L, R, gen):
+    return torch.softmax(torch.randn(N, T, L, R, generator=gen, dtype=F64), -1).reshape(N, T, L * R)
+
+
+# ----------------------------------------------------------------------------- a1
+def test_corners_are_binary_counting():
+    for Kb in (1, 2, 3, 4):
+        _, protos = orc.build_planes_protos(8, Kb, 2)
+        R = 1 << Kb
+        for r in range(R):
+            for k in range(Kb):
+                bit = (r >> (Kb - 1 - k)) & 1
+                assert protos[k, r].item() == (1.0 if bit else -1.0)
+
+
+def test_planes_match_reference_golden():
+    z = np.load(GOLDEN)
+    for i in range(6):
+        B, H, T, D, L, Kb, seed, _ = z[f"c{i}_meta"]
+        planes_T, protos_T = orc.build_planes_protos(int(D), int(Kb), int(L), seed=int(seed))
+        assert np.array_equal(planes_T.numpy(), z[f"c{i}_planes_T"])
+        assert np.array_equal(protos_T.numpy(), z[f"c{i}_protos_T"])
+
+
+def test_planes_unshared_layout():
+    pl, _ = orc.build_planes_protos(16, 3, 4, M=3, share_planes=False, seed=5)
+    g = torch.Generator().manual_seed(5)
+    raw = torch.randn(3, 4, 3, 16, generator=g)
+    assert pl.shape == (3, 16, 12)
+    # column j = l*K + k of ensemble m is plane (m, l, k)
+    assert torch.equal(pl[2, :, 1 * 3 + 2], raw[2, 1, 2])
+
+
+# ----------------------------------------------------------------------------- a2
+@pytest.mark.parametrize("L,Kb,scale", [(2, 2, None), (8, 4, None), (3, 3, 1.0), (16, 4, 1.0)])
+def test_softhash_softmax_equals_sigmoid_product(L, Kb, scale):
+    g = torch.Generator().manual_seed(L * 10 + Kb)
+    B, H, T, D = 2, 2, 9, 32
+    X = torch.randn(B, H, T, D, generator=g, dtype=F64) * 3
+    planes_T, protos_T = orc.build_planes_protos(D, Kb, L, seed=3)
+    p_soft = orc.soft_hash_probs(X, X, X, planes_T, protos_T, L, Kb, scale=scale)[0]
+    p_sig = orc.soft_hash_sigmoid(X, planes_T, L, Kb, scale=scale)
+    assert (p_soft - p_sig).abs().max().item() < 1e-14
+    R = 1 << Kb
+    sums = p_soft.view(B * H, T, L, R).sum(-1)
+    assert (sums - 1).abs().max().item() < 1e-14
+
+
+def test_softhash_zero_planes_uniform_and_k1():
+    X = torch.randn(1, 1, 5, 8, dtype=F64)
+    _, protos = orc.build_planes_protos(8, 3, 2)
+    p = orc.soft_hash_probs(X, X, X, torch.zeros(8, 6), protos, 2, 3)[0]
+    assert torch.all(p == 1.0 / 8)
+    # K=1: logits (-u, +u) -> [sigmoid(-2u), sigmoid(2u)]
+    planes_T, protos1 = orc.build_planes_protos(8, 1, 1, seed=1)
+    p1 = orc.soft_hash_probs(X, X, X, planes_T, protos1, 1, 1)[0]
+    u = torch.tanh(X.view(5, 8) @ planes_T.to(F64)) / math.sqrt(8)
+    assert torch.allclose(p1[0, :, 0], torch.sigmoid(-2 * u[:, 0]), atol=1e-15)
+    assert torch.allclose(p1[0, :, 1], torch.sigmoid(2 * u[:, 0]), atol=1e-15)
+
+
+def test_softhash_against_reference_golden():
+    """fp32 golden: bit-level agreement to fp32 rounding; bf16 golden: the reference's
+    own bf16 roundings stay within the bf16 parity tolerance of the fp64 oracle."""
+    z = np.load(GOLDEN)
+    for i in range(6):
+        B, H, T, D, L, Kb, seed, is_bf16 = (int(x) for x in z[f"c{i}_meta"])
+        Q, K, V = (torch.from_numpy(z[f"c{i}_{n}"]) for n in "QKV")
+        planes_T = torch.from_numpy(z[f"c{i}_planes_T"])
+        protos_T = torch.from_numpy(z[f"c{i}_protos_T"])
+        if is_bf16:  # the reference casts the planes to the input dtype (race_common.py:54)
+            planes_T = planes_T.to(torch.bfloat16).float()
+        pK, pQ, _, _ = orc.soft_hash_probs(Q, K, V, planes_T, protos_T, L, Kb)
+        tol = 2e-2 if is_bf16 else 1e-6
+        assert orc.relerr(torch.from_numpy(z[f"c{i}_probsK"]), pK) < tol
+        assert orc.relerr(torch.from_numpy(z[f"c{i}_probsQ"]), pQ) < tol
+
+
+# ----------------------------------------------------------------------------- a3
+def test_prefix_ref_equals_brute_force():
+    g = torch.Generator().manual_seed(0)
+    N, T, L, R, D = 2, 7, 3, 4, 5
+    pk, pq = softmax_probs(N, T, L, R, g), softmax_probs(N, T, L, R, g)
+    v = torch.randn(N, T, D, generator=g, dtype=F64)
+    out, A, B = orc.race_prefix_ref(pk, pq, v, 1e-6)
+    assert (out - orc.race_prefix_brute(pk, pq, v, 1e-6)).abs().max().item() < 1e-13
+    assert torch.allclose(A, pk.sum(1)) and torch.allclose(B, torch.einsum("nts,ntd->nsd", pk, v))
+
+
+def test_prefix_ref_zero_planes_known_answer():
+    """planes = 0 -> p = 1/R everywhere -> out_t = L * sum_{tau<=t} v / (t+1+R*eps)."""
+    L, Kb, eps = 4, 3, 1e-3
+    R = 1 << Kb
+    B, H, T, D = 1, 2, 11, 6
+    V = torch.randn(B, H, T, D, dtype=F64)
+    _, protos = orc.build_planes_protos(D, Kb, L)
+    out = orc.race_module_ref(V, V, V, torch.zeros(D, L * Kb), protos, L, Kb, eps=eps)
+    t = torch.arange(T, dtype=F64).view(1, 1, T, 1)
+    known = L * V.cumsum(2) / (t + 1 + R * eps)
+    assert (out - known).abs().max().item() < 1e-13
+
+
+def test_prefix_ref_t1_closed_form():
+    g = torch.Generator().manual_seed(1)
+    pk, pq = softmax_probs(3, 1, 2, 4, g), softmax_probs(3, 1, 2, 4, g)
+    v = torch.randn(3, 1, 4, generator=g, dtype=F64)
+    out, _, _ = orc.race_prefix_ref(pk, pq, v, 1e-6)
+    known = (pq * pk / (pk + 1e-6)).sum(-1, keepdim=True) * v
+    assert (out - known).abs().max().item() < 1e-14
+
+
+def test_gradcheck_prefix_and_module():
+    g = torch.Generator().manual_seed(2)
+    pk = softmax_probs(1, 5, 2, 4, g).requires_grad_()
+    pq = softmax_probs(1, 5, 2, 4, g).requires_grad_()
+    v = torch.randn(1, 5, 3, generator=g, dtype=F64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda a, b, c: orc.race_prefix_ref(a, b, c, 1e-3)[0], (pk, pq, v))
+    planes_T, protos = orc.build_planes_protos(6, 2, 2, seed=4)
+    Q, K, V = (torch.randn(1, 2, 4, 6, generator=g, dtype=F64, requires_grad=True) for _ in range(3))
+    assert torch.autograd.gradcheck(
+        lambda q, k, x: orc.race_module_ref(q, k, x, planes_T, protos, 2, 2, scale=1.0), (Q, K, V))
+
+
+# ---------------------------------------------------------------- C restatements
+def test_c_streaming_fwd_bwd_equal_autograd():
+    g = torch.Generator().manual_seed(3)
+    N, T, L, R, D, eps = 3, 40, 2, 8, 7, 1e-6
+    pk, pq = softmax_probs(N, T, L, R, g), softmax_probs(N, T, L, R, g)
+    v = torch.randn(N, T, D, generator=g, dtype=F64)
+    go = torch.randn(N, T, D, generator=g, dtype=F64)
+    a, b, c = (x.clone().requires_grad_() for x in (pk, pq, v))
+    out, A, B = orc.race_prefix_ref(a, b, c, eps)
+    (out * go).sum().backward()
+    o2, A2, B2 = oracle_c.race_fwd(pk, pq, v, eps)
+    assert orc.relerr(o2, out) < 1e-13 and orc.relerr(A2, A) < 1e-13 and orc.relerr(B2, B) < 1e-13
+    gpk, gpq, gv = oracle_c.race_bwd(pk, pq, v, go, eps)
+    assert orc.relerr(gpk, a.grad) < 1e-12
+    assert orc.relerr(gpq, b.grad) < 1e-12
+    assert orc.relerr(gv, c.grad) < 1e-12
+
+
+@pytest.mark.parametrize("NS,T,D", [(1, 1, 1), (4, 1, 8), (8, 16, 32), (16, 512, 64)])
+def test_c_prefix_mean_flat(NS, T, D):
+    """kernels/cpu/test_cpu_kernels.py:49-53 sweep: C restatement vs fp64 cumsum."""
+    g = torch.Generator().manual_seed(NS + T)
+    w = torch.rand(NS, T, generator=g)
+    v = torch.randn(NS, T, D, generator=g)
+    E = oracle_c.prefix_mean_flat(w, v, 1e-6)
+    ref = (w.double().unsqueeze(-1) * v.double()).cumsum(1) / (w.double().cumsum(1).unsqueeze(-1) + 1e-6)
+    assert orc.relerr(E, ref) < 1e-6
+    wr = w.double().requires_grad_()
+    vr = v.double().requires_grad_()
+    gE = torch.randn(NS, T, D, generator=g)
+    ((wr.unsqueeze(-1) * vr).cumsum(1) / (wr.cumsum(1).unsqueeze(-1) + 1e-6) * gE.double()).sum().backward()
+    gW, gV = oracle_c.prefix_mean_flat_bw(w, v, gE, 1e-6)
+    assert orc.relerr(gW, wr.grad) < 1e-5 and orc.relerr(gV, vr.grad) < 1e-5
+
+
+def test_c_restatement_matches_compiled_reference():
+    ext = oracle_c.ref_ext()
+    if ext is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    g = torch.Generator().manual_seed(9)
+    w = torch.rand(6, 300, generator=g)
+    v = torch.randn(6, 300, 24, generator=g)
+    gE = torch.randn(6, 300, 24, generator=g)
+    assert torch.equal(ext.race_prefix_mean_flat(w, v, 1e-6), oracle_c.prefix_mean_flat(w, v, 1e-6))
+    r_gw, r_gv = ext.race_prefix_mean_flat_bw(w, v, gE, 1e-6)
+    o_gw, o_gv = oracle_c.prefix_mean_flat_bw(w, v, gE, 1e-6)
+    assert torch.equal(r_gw, o_gw) and torch.equal(r_gv, o_gv)
+
+
+def test_cpu_port_matches_oracle():
+    """scaling/test_race_cpu_composite.py sweep, against the fp64 oracle."""
+    g = torch.Generator().manual_seed(0)
+    for (N, T, S, D) in [(2, 8, 6, 8), (4, 64, 24, 32)]:
+        pk = torch.rand(N, T, S, generator=g)
+        pq = torch.rand(N, T, S, generator=g)
+        v = torch.randn(N, T, D, generator=g)
+        go = torch.randn(N, T, D, generator=g)
+        a, b, c = (x.clone().requires_grad_() for x in (pk, pq, v))
+        out = race_cpu_port.RaceCausalCPUFn.apply(a, b, c, 1e-6)
+        (out * go).sum().backward()
+        ref = oracle_c.race_fwd(pk, pq, v, 1e-6)[0]
+        gk, gq, gv = oracle_c.race_bwd(pk, pq, v, go, 1e-6)
+        assert orc.relerr(out, ref) < 1e-4
+        assert orc.relerr(a.grad, gk) < 1e-3 and orc.relerr(b.grad, gq) < 1e-3 and orc.relerr(c.grad, gv) < 1e-3
+
+
+# ----------------------------------------------------------------------------- a11
+def test_decode_ref_equals_module_position():
+    g = torch.Generator().manual_seed(4)
+    B, H, T, D, L, Kb = 2, 2, 6, 16, 2, 3
+    planes_T, protos = orc.build_planes_protos(D, Kb, L, seed=0)
+    Q, K, V = (torch.randn(B, H, T + 1, D, generator=g, dtype=F64) for _ in range(3))
+    full = orc.race_module_ref(Q, K, V, planes_T, protos, L, Kb)
+    out, A, Bst = orc.decode_ref(K[:, :, :T], V[:, :, :T], Q[:, :, T], K[:, :, T], V[:, :, T],
+                                 planes_T, L, Kb)
+    assert (out - full[:, :, T]).abs().max().item() < 1e-13
+
+
+def test_gqa_ref_is_repeated_kv():
+    g = torch.Generator().manual_seed(5)
+    B, Hq, Hkv, T, D, L, Kb = 1, 4, 2, 5, 8, 2, 2
+    planes_T, protos = orc.build_planes_protos(D, Kb, L, seed=0)
+    Q = torch.randn(B, Hq, T, D, generator=g, dtype=F64)
+    K, V = (torch.randn(B, Hkv, T, D, generator=g, dtype=F64) for _ in range(2))
+    out = orc.race_gqa_ref(Q, K, V, planes_T, L, Kb)
+    for h in range(Hq):
+        one = orc.race_module_ref(Q[:, h:h + 1], K[:, h // 2:h // 2 + 1], V[:, h // 2:h // 2 + 1],
+                                  planes_T, protos, L, Kb)
+        assert (out[:, h:h + 1] - one).abs().max().item() < 1e-14
