@@ -1,0 +1,243 @@
+"""Benchmark of the causal RACE hot path on one MI355X.
+
+Headline (BASELINE.json metric "RACE layer fwd+bwd tokens/sec at 1M ctx"):
+one causal RACE layer forward+backward, B=1, H=4, T=2^20, D=64, L=8, K=4,
+bf16 q/k/v ~ N(0, 1/sqrt(D)) and upstream grad ~ N(0,1), planes seed 0, inputs
+drawn from torch.Generator(cuda).manual_seed(1) in the order q, k, v, go and
+resident in HBM before the timed region. A step is forward + backward of the
+layer; value = B*T / seconds per step.
+
+The same JSON line also carries:
+  roofline       dominant kernel of the step: algorithmic HBM bytes per launch over
+                 its average launch time (HIP events inside librace_amd, on the
+                 launch stream), against 8 TB/s
+  layer_roofline the whole step against t_bound = max(F_alg/2.5e15, B_alg/8e12)
+  decode         fused decode tokens/s (256 sequences, 32 q / 8 kv heads, 512-token
+                 prefill, 1024 steps)
+  cpu_baseline   the reference CPU path (faithful port, oracle/race_cpu_port.py)
+                 timed on this host on a bounded sample of the same layer
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12      # B/s
+BF16_PEAK = 2.5e15     # dense MFMA flop/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--T", type=int, default=1 << 20)
+    ap.add_argument("--B", type=int, default=1)
+    ap.add_argument("--H", type=int, default=4)
+    ap.add_argument("--L", type=int, default=8)
+    ap.add_argument("--decode-steps", type=int, default=1024)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-T", type=int, default=8192)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- algorithmic counts
+def layer_counts(S, D, L, K, elt=2):
+    """Per (token, head) of one layer fwd+bwd: flops and compulsory HBM bytes."""
+    R = 1 << K
+    f_scan = 14 * S * D + 9 * S
+    f_hash = 6 * (2 * D * L * K + 2 * L * K * R + 4 * S)
+    return f_scan + f_hash, 11 * D * elt
+
+
+def kernel_bytes(name, Hq, Hkv, D, elt=2):
+    """Algorithmic HBM bytes per kv-head token of one fused kernel launch."""
+    G = Hq // Hkv
+    row = D * elt
+    return {
+        "qkv_fwd_totals": 2 * row,                    # k, v
+        "qkv_fwd_readout": 2 * row + 2 * G * row,     # k, v, q, out
+        "qkv_bwd_totals": 2 * row + 3 * G * row,      # k, v, q, go, dq
+        "qkv_bwd_main": 4 * row + 2 * G * row,        # k, v, dk, dv, q, go
+    }.get(name)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
+              "(the hot path shards over heads/sequence with one exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from race_attention_amd import RaceDecodeState, build_planes_protos, race_causal_attention
+    from race_attention_amd import _lib
+
+    dev = torch.device("cuda:0")
+    B, H, T, D, L, K = args.B, args.H, args.T, 64, args.L, 4
+    S = L << K
+    planes_T, _ = build_planes_protos(D, K, L, 1, device=dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(1)
+    std = 1.0 / math.sqrt(D)
+    q = (torch.randn(B, H, T, D, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(True)
+    k = (torch.randn(B, H, T, D, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(True)
+    v = (torch.randn(B, H, T, D, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(True)
+    go = torch.randn(B, H, T, D, generator=g, device=dev).to(torch.bfloat16)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = race_causal_attention(q, k, v, planes_T, L, K)
+        out.backward(go)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    tokens_per_s = B * T / (ms_per_step / 1e3)
+
+    # per-kernel launch times (HIP events recorded by the library on the launch stream)
+    _lib.profile(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    kern = _lib.profile_read()
+    _lib.profile(False)
+    dom = max(kern, key=lambda n: kern[n][0])
+    dom_ms = kern[dom][0] / kern[dom][1]
+    per_tok = kernel_bytes(dom, H, H, D)
+    roofline = None
+    if per_tok is not None:
+        traffic_bytes = per_tok * B * H * T
+        achieved = traffic_bytes / (dom_ms / 1e3) / 1e9
+        roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
+                    "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": None,
+                    "algorithmic_bytes_per_launch": traffic_bytes, "avg_launch_ms": round(dom_ms, 4)}
+    f_alg, b_alg = layer_counts(S, D, L, K)
+    n_tok = B * H * T
+    t_bound = max(f_alg * n_tok / BF16_PEAK, b_alg * n_tok / HBM_PEAK)
+    layer_roofline = {"t_bound_ms": round(t_bound * 1e3, 4), "frac": round(t_bound * 1e3 / ms_per_step, 4),
+                      "bound": "hbm" if b_alg / HBM_PEAK > f_alg / BF16_PEAK else "mfma",
+                      "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kern.items()}}
+
+    result = {
+        "metric": "RACE layer fwd+bwd tokens/sec at 1M ctx; fused-decode tokens/sec",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg3: one causal RACE layer fwd+bwd", "B": B, "H": H, "T": T, "D": D, "L": L,
+                   "K": K, "S": S, "inputs": "bf16 q,k,v ~ N(0,1/sqrt(D)), go ~ N(0,1), seed 1; planes seed 0",
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "layer_roofline": layer_roofline,
+        "wall_s_timed": round(wall, 3),
+    }
+
+    del q, k, v, go
+    torch.cuda.empty_cache()
+    if not args.no_decode:
+        result["decode"] = bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, args.decode_steps)
+    if not args.no_cpu:
+        result["cpu_baseline"] = bench_cpu(torch, args.cpu_T, H, D, L, K)
+    print(json.dumps(result))
+
+
+def bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, steps):
+    """cfg4: 256 sequences with a 512-token prefilled state, 32 q / 8 kv heads, D=64,
+    L=8, K=4; `steps` single-token decode steps updating the fp32 state in place."""
+    Bs, Hq, Hkv, D, L, K, T0 = 256, 32, 8, 64, 8, 4, 512
+    S = L << K
+    planes_T, _ = build_planes_protos(D, K, L, 1, device=dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(1)
+    st = RaceDecodeState(Bs, Hq, Hkv, D, L, K, planes_T, device=dev)
+    qp = torch.randn(Bs, Hq, T0, D, generator=g, device=dev).to(torch.bfloat16)
+    kp = torch.randn(Bs, Hkv, T0, D, generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn(Bs, Hkv, T0, D, generator=g, device=dev).to(torch.bfloat16)
+    st.prefill(qp, kp, vp)
+    del qp, kp, vp
+    qs = torch.randn(steps, Bs, Hq, D, generator=g, device=dev).to(torch.bfloat16)
+    ks = torch.randn(steps, Bs, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
+    vs = torch.randn(steps, Bs, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty(Bs, Hq, D, dtype=torch.bfloat16, device=dev)
+    for i in range(4):
+        st.step(qs[i], ks[i], vs[i], out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        st.step(qs[i], ks[i], vs[i], out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    _lib.profile(True)
+    for i in range(min(steps, 64)):
+        st.step(qs[i], ks[i], vs[i], out)
+    torch.cuda.synchronize()
+    kern = _lib.profile_read()
+    _lib.profile(False)
+    k_ms = kern["decode_step"][0] / kern["decode_step"][1]
+    bytes_step = 2 * 4 * Bs * Hkv * S * (D + 1) + 2 * Bs * (2 * Hq + 2 * Hkv) * D
+    achieved = bytes_step / (k_ms / 1e3) / 1e9
+    return {"value": round(Bs * steps / (ms / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms / steps, 5),
+            "config": {"workload": "cfg4 fused decode", "sequences": Bs, "Hq": Hq, "Hkv": Hkv, "D": D, "L": L,
+                       "K": K, "prefill": T0, "steps": steps},
+            "roofline": {"kernel": "decode_step", "bound": "hbm", "achieved": round(achieved, 1),
+                         "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4),
+                         "algorithmic_bytes_per_launch": bytes_step, "avg_launch_ms": round(k_ms, 5)}}
+
+
+def bench_cpu(torch, T, H, D, L, K, reps=3):
+    """The reference CPU path (soft-hash + RaceCausalCPUFn, fp32, fp64 prefix-mean
+    kernel on OpenMP threads) on the same layer shape with a bounded T."""
+    from oracle import race_cpu_port
+    from oracle import race_oracle as orc
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    planes_T, protos_T = orc.build_planes_protos(D, K, L, seed=0)
+    g = torch.Generator().manual_seed(1)
+    std = 1.0 / math.sqrt(D)
+    q, k, v = ((torch.randn(1, H, T, D, generator=g) * std).requires_grad_(True) for _ in range(3))
+    go = torch.randn(1, H, T, D, generator=g)
+
+    def run():
+        q.grad = k.grad = v.grad = None
+        out = race_cpu_port.race_layer_cpu(q, k, v, planes_T, protos_T, L, K)
+        out.backward(go)
+
+    run()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    sec = ts[len(ts) // 2]
+    return {"value": round(T / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one layer fwd+bwd, B=1 H={H} T={T} D={D} L={L} K={K} fp32, median of {reps}",
+            "seconds_per_step": round(sec, 3)}
+
+
+if __name__ == "__main__":
+    main()

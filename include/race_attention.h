@@ -1,0 +1,155 @@
+/*
+ * race_attention.h -- C ABI of the MI355X (gfx950) causal RACE attention library
+ * (librace_amd.so). Plain pointers, sizes and a stream handle; no C++ or torch
+ * types cross this boundary. Every call is asynchronous on `stream` (a
+ * hipStream_t; NULL is the null stream), allocates nothing, and returns a
+ * race_status; race_last_error() gives the message of the last failure on the
+ * calling thread.
+ *
+ * Reference interfaces replaced (sahiljoshi515/RACE_Attention):
+ *   race_soft_hash_fwd/bwd  scaling/race_common.py:36-73  soft_hash_probs (+ its autograd)
+ *   race_op_fwd             kernels/gpu/forward_kernel.cu:110-137  race_fused_fwd
+ *                           (bound at kernels/gpu/race_cuda_binding.cpp:12,18)
+ *   race_op_bwd             kernels/gpu/backward_kernels.cu:174-215  race_backward
+ *                           (bound at kernels/gpu/race_cuda_binding.cpp:13-14,21)
+ *   race_qkv_fwd/bwd        scaling/race_causal_cuda.py:94-102 RaceCausalCuda.forward
+ *                           (soft-hash + RaceCausalFn, race_causal_cuda.py:47-69) and its
+ *                           backward, fused: q,k,v in, out / dq,dk,dv out
+ *   race_qkv_final_state    the (A_final, B_final) returned by race_prefix_ref,
+ *                           scaling/race_common.py:88-90
+ *   race_decode_step        no reference counterpart (chat/nanochat/gpt.py:143-146 raises);
+ *                           single-token step on the carried (A, B) state
+ */
+#ifndef RACE_ATTENTION_H
+#define RACE_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RACE_ABI_VERSION 1
+
+typedef enum {
+    RACE_OK = 0,
+    RACE_ERR_INVALID = 1,     /* bad shape, pointer, stride or argument */
+    RACE_ERR_UNSUPPORTED = 2, /* valid but not compiled for (e.g. head dim) */
+    RACE_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+    RACE_ERR_HIP = 4          /* HIP runtime error while launching */
+} race_status;
+
+typedef enum { RACE_F32 = 0, RACE_BF16 = 1 } race_dtype;
+
+typedef void *race_stream; /* hipStream_t */
+
+/* A [B][H][T][D] tensor with contiguous last dimension; strides in elements. */
+typedef struct {
+    void *data;
+    int64_t stride_b, stride_h, stride_t;
+} race_tensor;
+
+int race_abi_version(void);
+const char *race_last_error(void);
+
+/* ---------------------------------------------------------------- soft-hash */
+typedef struct {
+    int B, H, T, D; /* x is [B][H][T][D] */
+    int L, K;       /* L tables of K bits: S = L * 2^K buckets */
+    int M;          /* ensemble copies (N = M*B*H rows of probabilities) */
+    int unshared;   /* 1: planes_T is [M][D][L*K] (share_planes=False), else [D][L*K] */
+    float scale;    /* logits divisor; the reference uses sqrt(D) */
+} race_hash_shape;
+
+/* probs [Mp][B*H][T][L*2^K] fp32, Mp = M if unshared else 1 (shared planes give
+ * identical rows for every ensemble copy). x fp32 or bf16; bf16 rounds the planes
+ * to bf16 as the reference does (race_common.py:54). */
+int race_soft_hash_fwd(const race_hash_shape *sh, race_tensor x, int x_dtype,
+                       const float *planes_T, float *probs, race_stream stream);
+/* dx (dtype of x, layout of dx) from gprobs [M][B*H][T][L*2^K] (summed over M). */
+int race_soft_hash_bwd(const race_hash_shape *sh, race_tensor x, int x_dtype,
+                       const float *planes_T, const float *gprobs, race_tensor dx,
+                       race_stream stream);
+
+/* ---------------------------------------------------------------- op-level scan */
+/* pK, pQ [N][T][S], V / out / gO / gV [N][T][D], gpK / gpQ [N][T][S]; fp32,
+ * contiguous. `block` = tokens per workgroup (0: automatic; results do not depend
+ * on it beyond fp32 rounding). */
+size_t race_op_workspace_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block,
+                               int backward);
+int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N,
+                int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
+                size_t workspace_bytes, race_stream stream);
+int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK,
+                float *gpQ, float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps,
+                int64_t block, void *workspace, size_t workspace_bytes, race_stream stream);
+
+/* ---------------------------------------------------------------- fused layer */
+typedef struct {
+    int B, Hq, Hkv, T, D; /* q [B][Hq][T][D], k/v [B][Hkv][T][D]; query head h reads kv head h/(Hq/Hkv) */
+    int L, K;             /* hash tables and bits, K <= 4 */
+    float scale, eps;     /* logits divisor (reference: sqrt(D)) and denominator eps */
+    int64_t block;        /* tokens per workgroup, 0: automatic */
+} race_qkv_shape;
+
+/* Bytes of the state the forward writes and the backward / final_state read. */
+size_t race_qkv_state_bytes(const race_qkv_shape *sh);
+/* Bytes of scratch for the forward (backward = 0) or backward (backward = 1). */
+size_t race_qkv_scratch_bytes(const race_qkv_shape *sh, int backward);
+/* bf16 q, k, v; planes_T fp32 [D][L*K]; out bf16 or fp32 (out_dtype). */
+int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v,
+                 const float *planes_T, race_tensor out, int out_dtype, void *state,
+                 size_t state_bytes, void *scratch, size_t scratch_bytes, race_stream stream);
+/* go bf16; dq, dk, dv bf16 (overwritten, not accumulated). */
+int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v,
+                 race_tensor go, const float *planes_T, const void *state, size_t state_bytes,
+                 race_tensor dq, race_tensor dk, race_tensor dv, void *scratch,
+                 size_t scratch_bytes, race_stream stream);
+/* Final bucket state after the forward: A [B*Hkv][S], Bs [B*Hkv][S][D] fp32. */
+int race_qkv_final_state(const race_qkv_shape *sh, const void *state, size_t state_bytes,
+                         float *A, float *Bs, race_stream stream);
+
+/* ---------------------------------------------------------------- decode */
+typedef struct {
+    int B, Hq, Hkv, D, L, K; /* q [B][Hq][D], k/v [B][Hkv][D]; Hq/Hkv <= 8; D in {64,128} */
+    float scale, eps;
+} race_decode_shape;
+
+/* One token per sequence: A += pK, Bs += pK v^T (in place, state [B*Hkv][S] /
+ * [B*Hkv][S][D] fp32), then out = sum_s pQ Bs / (A + eps). q/k/v/out share dtype. */
+int race_decode_step(const race_decode_shape *sh, const void *q, const void *k, const void *v,
+                     int dtype, const float *planes_T, float *A, float *Bs, void *out,
+                     race_stream stream);
+
+/* ---------------------------------------------------------------- kernel timing */
+/* No reference counterpart (the reference times with wall clocks only,
+ * scaling/benchmark_time.py:337-351). When enabled, every kernel launch of this
+ * library is bracketed by HIP events on its own stream; race_profile_read
+ * waits for the recorded events of one kernel and returns its accumulated time
+ * and launch count since the last reset. */
+enum {
+    RACE_PROF_QKV_FWD_TOTALS = 0,
+    RACE_PROF_QKV_FWD_READOUT = 1,
+    RACE_PROF_QKV_BWD_TOTALS = 2,
+    RACE_PROF_QKV_BWD_MAIN = 3,
+    RACE_PROF_OP_FWD_TOTALS = 4,
+    RACE_PROF_OP_FWD_READOUT = 5,
+    RACE_PROF_OP_BWD_TOTALS = 6,
+    RACE_PROF_OP_BWD_MAIN = 7,
+    RACE_PROF_BLOCK_SCAN = 8,
+    RACE_PROF_REDUCE = 9,
+    RACE_PROF_SOFTHASH_FWD = 10,
+    RACE_PROF_SOFTHASH_BWD = 11,
+    RACE_PROF_DECODE = 12,
+    RACE_PROF_KERNELS = 13
+};
+int race_profile_enable(int on);
+int race_profile_read(int kernel, double *total_ms, int64_t *launches);
+int race_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RACE_ATTENTION_H */

@@ -1,0 +1,758 @@
+// extern "C" entry points of librace_amd.so (declared in include/race_attention.h):
+// argument validation, kernel-variant selection, workspace layout and launches.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/race_attention.h"
+#include "race_decode.h"
+#include "race_launch.h"
+#include "race_softhash.h"
+
+using namespace race;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_check(hipError_t e, const char *what)
+{
+    if (e != hipSuccess)
+        return fail(RACE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return RACE_OK;
+}
+
+#define RACE_TRY(expr)            \
+    do {                          \
+        const int _rc = (expr);   \
+        if (_rc != RACE_OK)       \
+            return _rc;           \
+    } while (0)
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t rup(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Tokens per workgroup: enough blocks for ~2048 workgroups in total, at least
+// four sub-chunks per block; an explicit request is rounded to the sub-chunk.
+int64_t resolve_block(int64_t T, int64_t streams, int C, int64_t req)
+{
+    int64_t cb;
+    if (req > 0) {
+        cb = rup(req, C);
+    } else {
+        const int64_t nb = std::max<int64_t>(1, cdiv(2048, std::max<int64_t>(1, streams)));
+        cb = std::max<int64_t>(4 * C, rup(cdiv(T, nb), C));
+    }
+    return std::min(cb, rup(T, C));
+}
+
+// ------------------------------------------------------------------ geometry
+struct Geo {
+    int ST, DP, C, n_st, S_pad;
+    int64_t CB, NB;
+    int64_t Z;               // kv streams
+    size_t state_elems_B;    // per workspace array
+    size_t state_elems_A;
+};
+
+void fill_ws_sizes(Geo &g)
+{
+    g.state_elems_B = (size_t)g.Z * (g.NB + 1) * g.S_pad * g.DP;
+    g.state_elems_A = (size_t)g.Z * (g.NB + 1) * g.S_pad;
+}
+
+int op_geometry(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block, Geo &g)
+{
+    if (N <= 0 || T <= 0 || S <= 0 || D <= 0)
+        return fail(RACE_ERR_INVALID, "race_op: N, T, S, D must be positive (got %lld, %lld, %lld, %lld)",
+                    (long long)N, (long long)T, (long long)S, (long long)D);
+    if (N > 65535)
+        return fail(RACE_ERR_UNSUPPORTED, "race_op: N = %lld streams exceeds 65535", (long long)N);
+    if (T > (int64_t)1 << 30 || S > 4096)
+        return fail(RACE_ERR_UNSUPPORTED, "race_op: T <= 2^30 and S <= 4096 required");
+    if (D > 256)
+        return fail(RACE_ERR_UNSUPPORTED, "race_op: head dim D = %lld > 256 is not compiled", (long long)D);
+    g.DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+    const int st_max = 4096 / g.DP;
+    g.ST = st_max;
+    for (int st : {16, 32, 64, 128})
+        if (st <= st_max && st >= S) {
+            g.ST = st;
+            break;
+        }
+    if (!op_variant_exists(g.ST, g.DP))
+        return fail(RACE_ERR_UNSUPPORTED, "race_op: no kernel for tile (%d, %d)", g.ST, g.DP);
+    g.C = OP_C;
+    g.n_st = (int)cdiv(S, g.ST);
+    g.S_pad = g.n_st * g.ST;
+    g.Z = N;
+    g.CB = resolve_block(T, N * g.n_st, g.C, block);
+    g.NB = cdiv(T, g.CB);
+    fill_ws_sizes(g);
+    return RACE_OK;
+}
+
+int qkv_geometry(const race_qkv_shape *sh, Geo &g)
+{
+    if (!sh)
+        return fail(RACE_ERR_INVALID, "race_qkv: null shape");
+    if (sh->B <= 0 || sh->Hq <= 0 || sh->Hkv <= 0 || sh->T <= 0 || sh->L <= 0)
+        return fail(RACE_ERR_INVALID, "race_qkv: B, Hq, Hkv, T, L must be positive");
+    if (sh->Hq % sh->Hkv)
+        return fail(RACE_ERR_INVALID, "race_qkv: Hq = %d is not a multiple of Hkv = %d", sh->Hq, sh->Hkv);
+    if (sh->K < 1 || sh->K > 4)
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv: K = %d bits, the fused path supports 1..4", sh->K);
+    if (sh->D != 64 && sh->D != 128)
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv: head dim %d, the fused path supports 64 and 128", sh->D);
+    if (!(sh->eps > 0.0f) || !(sh->scale > 0.0f))
+        return fail(RACE_ERR_INVALID, "race_qkv: eps and scale must be positive");
+    const int R = 1 << sh->K;
+    const int64_t S = (int64_t)sh->L * R;
+    if (S > 4096)
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv: S = %lld buckets > 4096", (long long)S);
+    g.DP = sh->D;
+    const int st_max = g.DP == 64 ? 128 : 64;
+    g.ST = st_max;
+    for (int st : {32, 64, 128})
+        if (st <= st_max && st >= S) {
+            g.ST = st;
+            break;
+        }
+    if (!qkv_variant_exists(g.ST, g.DP))
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv: no kernel for tile (%d, %d)", g.ST, g.DP);
+    g.C = QKV_C;
+    g.n_st = (int)cdiv(S, g.ST);
+    g.S_pad = g.n_st * g.ST;
+    g.Z = (int64_t)sh->B * sh->Hkv;
+    if (g.Z > 65535)
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv: B*Hkv = %lld exceeds 65535", (long long)g.Z);
+    g.CB = resolve_block(sh->T, g.Z * g.n_st, g.C, sh->block);
+    g.NB = cdiv(sh->T, g.CB);
+    fill_ws_sizes(g);
+    return RACE_OK;
+}
+
+// Carve a workspace into 256-byte aligned pieces.
+struct Carver {
+    char *base;
+    size_t used = 0, cap;
+    Carver(void *p, size_t c) : base((char *)p), cap(c) {}
+    float *take(size_t elems)
+    {
+        float *p = (float *)(base ? base + used : nullptr);
+        used += align256(elems * sizeof(float));
+        return p;
+    }
+};
+
+int check_view(const race_tensor &t, const char *name, bool bf16_vec)
+{
+    if (!t.data)
+        return fail(RACE_ERR_INVALID, "%s: null data pointer", name);
+    if (t.stride_b < 0 || t.stride_h < 0 || t.stride_t < 0)
+        return fail(RACE_ERR_INVALID, "%s: negative stride", name);
+    if (bf16_vec) {
+        if (((uintptr_t)t.data & 15) || (t.stride_b & 7) || (t.stride_h & 7) || (t.stride_t & 7))
+            return fail(RACE_ERR_INVALID,
+                        "%s: bf16 rows must be 16-byte aligned (pointer %% 16 == 0, strides %% 8 == 0)", name);
+    }
+    return RACE_OK;
+}
+
+View to_view(const race_tensor &t) { return View{t.data, t.stride_b, t.stride_h, t.stride_t}; }
+OutView to_out(const race_tensor &t, int f32) { return OutView{t.data, t.stride_b, t.stride_h, t.stride_t, 0, f32}; }
+
+hipStream_t hs(race_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------------ kernel timing
+// When enabled, every launch is bracketed by a pair of HIP events recorded on the
+// launch stream; race_profile_read resolves them into per-kernel totals.
+struct EventPair {
+    hipEvent_t a, b;
+};
+struct Profiler {
+    std::mutex mu;
+    bool on = false;
+    std::vector<EventPair> pending[RACE_PROF_KERNELS];
+    double total_ms[RACE_PROF_KERNELS] = {};
+    int64_t count[RACE_PROF_KERNELS] = {};
+};
+Profiler &prof()
+{
+    static Profiler p;
+    return p;
+}
+
+struct ProfScope {
+    int id;
+    hipStream_t s;
+    EventPair ev{nullptr, nullptr};
+    ProfScope(int id_, hipStream_t s_) : id(id_), s(s_)
+    {
+        Profiler &p = prof();
+        std::lock_guard<std::mutex> g(p.mu);
+        if (!p.on)
+            return;
+        if (hipEventCreate(&ev.a) != hipSuccess || hipEventCreate(&ev.b) != hipSuccess) {
+            ev = EventPair{nullptr, nullptr};
+            return;
+        }
+        (void)hipEventRecord(ev.a, s);
+    }
+    ~ProfScope()
+    {
+        if (!ev.a)
+            return;
+        (void)hipEventRecord(ev.b, s);
+        Profiler &p = prof();
+        std::lock_guard<std::mutex> g(p.mu);
+        p.pending[id].push_back(ev);
+    }
+};
+
+hipError_t prof_block_scan(float *ws, int64_t elems, int NB, int Z, int rev, hipStream_t s)
+{
+    ProfScope ps(RACE_PROF_BLOCK_SCAN, s);
+    return launch_block_scan(ws, elems, NB, Z, rev, s);
+}
+hipError_t prof_reduce(const float *part, int n_st, int64_t tile, const OutView &out, int B, int H, int T, int D,
+                       hipStream_t s)
+{
+    ProfScope ps(RACE_PROF_REDUCE, s);
+    return launch_reduce_partials(part, n_st, tile, out, B, H, T, D, s);
+}
+hipError_t prof_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s)
+{
+    ProfScope ps(bwd ? RACE_PROF_SOFTHASH_BWD : RACE_PROF_SOFTHASH_FWD, s);
+    return launch_softhash(P, bf16, bwd, s);
+}
+hipError_t prof_decode(const DecodeParams &P, int bf16, hipStream_t s)
+{
+    ProfScope ps(RACE_PROF_DECODE, s);
+    return launch_decode(P, bf16, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int race_abi_version(void) { return RACE_ABI_VERSION; }
+
+const char *race_last_error(void) { return g_err.c_str(); }
+
+// ============================================================================ soft-hash
+static int hash_common(const race_hash_shape *sh, const race_tensor &x, int x_dtype,
+                       const float *planes_T, SoftHashParams &P)
+{
+    if (!sh)
+        return fail(RACE_ERR_INVALID, "race_soft_hash: null shape");
+    if (sh->B <= 0 || sh->H <= 0 || sh->T <= 0 || sh->D <= 0 || sh->L <= 0 || sh->M <= 0)
+        return fail(RACE_ERR_INVALID, "race_soft_hash: B, H, T, D, L, M must be positive");
+    if (sh->K < 1 || sh->K > 8)
+        return fail(RACE_ERR_UNSUPPORTED, "race_soft_hash: K = %d, supported 1..8", sh->K);
+    if (x_dtype != RACE_F32 && x_dtype != RACE_BF16)
+        return fail(RACE_ERR_INVALID, "race_soft_hash: dtype must be RACE_F32 or RACE_BF16");
+    if (sh->D > 256 || (int64_t)sh->D * sh->L * sh->K > 16384)
+        return fail(RACE_ERR_UNSUPPORTED, "race_soft_hash: D <= 256 and D*L*K <= 16384 required");
+    if (!(sh->scale > 0.0f))
+        return fail(RACE_ERR_INVALID, "race_soft_hash: scale must be positive");
+    if (!planes_T)
+        return fail(RACE_ERR_INVALID, "race_soft_hash: null planes");
+    RACE_TRY(check_view(x, "race_soft_hash: x", false));
+    std::memset(&P, 0, sizeof(P));
+    P.x = to_view(x);
+    P.planes = planes_T;
+    P.B = sh->B;
+    P.H = sh->H;
+    P.T = sh->T;
+    P.D = sh->D;
+    P.L = sh->L;
+    P.K = sh->K;
+    P.LK = sh->L * sh->K;
+    P.M = sh->M;
+    P.unshared = sh->unshared ? 1 : 0;
+    P.plane_stride = (int64_t)sh->D * P.LK;
+    P.round_planes = x_dtype == RACE_BF16;
+    P.scale = sh->scale;
+    P.inv_scale = 1.0f / sh->scale;
+    return hip_check(softhash_prepare(P.D, P.LK), "race_soft_hash: set shared memory");
+}
+
+int race_soft_hash_fwd(const race_hash_shape *sh, race_tensor x, int x_dtype, const float *planes_T,
+                       float *probs, race_stream stream)
+{
+    SoftHashParams P;
+    RACE_TRY(hash_common(sh, x, x_dtype, planes_T, P));
+    if (!probs)
+        return fail(RACE_ERR_INVALID, "race_soft_hash_fwd: null probs");
+    P.probs = probs;
+    return hip_check(prof_softhash(P, x_dtype == RACE_BF16, 0, hs(stream)), "race_soft_hash_fwd");
+}
+
+int race_soft_hash_bwd(const race_hash_shape *sh, race_tensor x, int x_dtype, const float *planes_T,
+                       const float *gprobs, race_tensor dx, race_stream stream)
+{
+    SoftHashParams P;
+    RACE_TRY(hash_common(sh, x, x_dtype, planes_T, P));
+    if (!gprobs)
+        return fail(RACE_ERR_INVALID, "race_soft_hash_bwd: null gprobs");
+    RACE_TRY(check_view(dx, "race_soft_hash_bwd: dx", false));
+    P.gprobs = gprobs;
+    P.dx = to_view(dx);
+    return hip_check(prof_softhash(P, x_dtype == RACE_BF16, 1, hs(stream)), "race_soft_hash_bwd");
+}
+
+// ============================================================================ op-level scan
+static size_t op_bytes(const Geo &g, int64_t T, int64_t D, int backward)
+{
+    size_t b = align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+    if (backward)
+        b += align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+    if (g.n_st > 1)
+        b += align256((size_t)g.n_st * g.Z * T * D * 4);
+    return b;
+}
+
+size_t race_op_workspace_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block, int backward)
+{
+    Geo g;
+    if (op_geometry(N, T, S, D, block, g) != RACE_OK)
+        return 0;
+    return op_bytes(g, T, D, backward);
+}
+
+static ScanParams op_params(const Geo &g, int64_t T, int64_t S, int64_t D, float eps)
+{
+    ScanParams P;
+    std::memset(&P, 0, sizeof(P));
+    P.T = (int)T;
+    P.S = (int)S;
+    P.D = (int)D;
+    P.L = 1;
+    P.K = 0;
+    P.R = 1;
+    P.G = 1;
+    P.Hkv = 1;
+    P.CB = (int)g.CB;
+    P.NB = (int)g.NB;
+    P.n_st = g.n_st;
+    P.S_pad = g.S_pad;
+    P.DPw = g.DP;
+    P.eps = eps;
+    P.scale = 1.0f;
+    P.inv_scale = 1.0f;
+    return P;
+}
+
+static int run_scan_op(ScanKernel k, const Geo &g, const ScanParams &P, hipStream_t s)
+{
+    ProfScope ps(RACE_PROF_OP_FWD_TOTALS + (int)k, s);
+    const dim3 grid((unsigned)g.NB, (unsigned)g.n_st, (unsigned)g.Z);
+    return hip_check(launch_scan_op(k, g.ST, g.DP, P, grid, s), "race_op kernel launch");
+}
+
+static int op_check(const float *pK, const float *pQ, const float *V, float eps, void *ws,
+                    size_t ws_bytes, size_t need, const char *who)
+{
+    if (!pK || !pQ || !V)
+        return fail(RACE_ERR_INVALID, "%s: null input pointer", who);
+    if (!(eps >= 0.0f))
+        return fail(RACE_ERR_INVALID, "%s: eps must be >= 0", who);
+    if (!ws || ws_bytes < need)
+        return fail(RACE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", who, need, ws ? ws_bytes : 0);
+    return RACE_OK;
+}
+
+int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
+                int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
+                race_stream stream)
+{
+    Geo g;
+    RACE_TRY(op_geometry(N, T, S, D, block, g));
+    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, op_bytes(g, T, D, 0), "race_op_fwd"));
+    if (!out)
+        return fail(RACE_ERR_INVALID, "race_op_fwd: null out");
+    Carver cv(workspace, workspace_bytes);
+    ScanParams P = op_params(g, T, S, D, eps);
+    P.pK = pK;
+    P.pQ = pQ;
+    P.V = V;
+    P.wsB = cv.take(g.state_elems_B);
+    P.wsA = cv.take(g.state_elems_A);
+    float *part = g.n_st > 1 ? cv.take((size_t)g.n_st * N * T * D) : nullptr;
+    P.out = part ? OutView{part, T * D, 0, D, N * T * D, 1} : OutView{out, T * D, 0, D, 0, 1};
+    const hipStream_t s = hs(stream);
+    RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
+    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(run_scan_op(K_FWD_READOUT, g, P, s));
+    if (part)
+        RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{out, T * D, 0, D, 0, 1},
+                                                  (int)N, 1, (int)T, (int)D, s), "reduce partials"));
+    return RACE_OK;
+}
+
+int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                void *workspace, size_t workspace_bytes, race_stream stream)
+{
+    Geo g;
+    RACE_TRY(op_geometry(N, T, S, D, block, g));
+    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, op_bytes(g, T, D, 1), "race_op_bwd"));
+    if (!gO || !gpK || !gpQ || !gV)
+        return fail(RACE_ERR_INVALID, "race_op_bwd: null gradient pointer");
+    Carver cv(workspace, workspace_bytes);
+    ScanParams P = op_params(g, T, S, D, eps);
+    P.pK = pK;
+    P.pQ = pQ;
+    P.V = V;
+    P.gO = gO;
+    P.gpK = gpK;
+    P.gpQ = gpQ;
+    P.wsB = cv.take(g.state_elems_B);
+    P.wsA = cv.take(g.state_elems_A);
+    P.ws2B = cv.take(g.state_elems_B);
+    P.ws2A = cv.take(g.state_elems_A);
+    float *part = g.n_st > 1 ? cv.take((size_t)g.n_st * N * T * D) : nullptr;
+    P.dv = part ? OutView{part, T * D, 0, D, N * T * D, 1} : OutView{gV, T * D, 0, D, 0, 1};
+    const hipStream_t s = hs(stream);
+    // forward block states (the backward recomputes them; nothing is saved between calls)
+    RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
+    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(run_scan_op(K_BWD_TOTALS, g, P, s));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(run_scan_op(K_BWD_MAIN, g, P, s));
+    if (part)
+        RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{gV, T * D, 0, D, 0, 1},
+                                                  (int)N, 1, (int)T, (int)D, s), "reduce partials"));
+    return RACE_OK;
+}
+
+// ============================================================================ fused layer
+size_t race_qkv_state_bytes(const race_qkv_shape *sh)
+{
+    Geo g;
+    if (qkv_geometry(sh, g) != RACE_OK)
+        return 0;
+    return align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+}
+
+static size_t qkv_scratch(const race_qkv_shape *sh, const Geo &g, int backward)
+{
+    const size_t q_elems = (size_t)sh->B * sh->Hq * sh->T * sh->D;
+    const size_t kv_elems = (size_t)sh->B * sh->Hkv * sh->T * sh->D;
+    size_t b = 0;
+    if (backward)
+        b += align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+    if (g.n_st > 1) {
+        b += align256((size_t)g.n_st * q_elems * 4);
+        if (backward)
+            b += 2 * align256((size_t)g.n_st * kv_elems * 4);
+    }
+    return b;
+}
+
+size_t race_qkv_scratch_bytes(const race_qkv_shape *sh, int backward)
+{
+    Geo g;
+    if (qkv_geometry(sh, g) != RACE_OK)
+        return 0;
+    return qkv_scratch(sh, g, backward);
+}
+
+static ScanParams qkv_params(const race_qkv_shape *sh, const Geo &g)
+{
+    ScanParams P;
+    std::memset(&P, 0, sizeof(P));
+    P.T = sh->T;
+    P.R = 1 << sh->K;
+    P.S = sh->L * P.R;
+    P.D = sh->D;
+    P.L = sh->L;
+    P.K = sh->K;
+    P.G = sh->Hq / sh->Hkv;
+    P.Hkv = sh->Hkv;
+    P.CB = (int)g.CB;
+    P.NB = (int)g.NB;
+    P.n_st = g.n_st;
+    P.S_pad = g.S_pad;
+    P.DPw = g.DP;
+    P.eps = sh->eps;
+    P.scale = sh->scale;
+    P.inv_scale = 1.0f / sh->scale;
+    return P;
+}
+
+static int run_scan_qkv(ScanKernel k, const Geo &g, const ScanParams &P, hipStream_t s)
+{
+    ProfScope ps(RACE_PROF_QKV_FWD_TOTALS + (int)k, s);
+    const dim3 grid((unsigned)g.NB, (unsigned)g.n_st, (unsigned)g.Z);
+    return hip_check(launch_scan_qkv(k, g.ST, g.DP, P, grid, s), "race_qkv kernel launch");
+}
+
+static int qkv_inputs(const race_qkv_shape *sh, const race_tensor &q, const race_tensor &k,
+                      const race_tensor &v, const float *planes_T, const char *who)
+{
+    (void)sh;
+    RACE_TRY(check_view(q, who, true));
+    RACE_TRY(check_view(k, who, true));
+    RACE_TRY(check_view(v, who, true));
+    if (!planes_T)
+        return fail(RACE_ERR_INVALID, "%s: null planes", who);
+    return RACE_OK;
+}
+
+int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v, const float *planes_T,
+                 race_tensor out, int out_dtype, void *state, size_t state_bytes, void *scratch,
+                 size_t scratch_bytes, race_stream stream)
+{
+    Geo g;
+    RACE_TRY(qkv_geometry(sh, g));
+    RACE_TRY(qkv_inputs(sh, q, k, v, planes_T, "race_qkv_fwd"));
+    if (out_dtype != RACE_F32 && out_dtype != RACE_BF16)
+        return fail(RACE_ERR_INVALID, "race_qkv_fwd: out_dtype must be RACE_F32 or RACE_BF16");
+    RACE_TRY(check_view(out, "race_qkv_fwd: out", false));
+    const size_t need_state = race_qkv_state_bytes(sh), need_scr = qkv_scratch(sh, g, 0);
+    if (!state || state_bytes < need_state)
+        return fail(RACE_ERR_WORKSPACE, "race_qkv_fwd: state of %zu bytes needed, got %zu", need_state,
+                    state ? state_bytes : 0);
+    if (need_scr && (!scratch || scratch_bytes < need_scr))
+        return fail(RACE_ERR_WORKSPACE, "race_qkv_fwd: scratch of %zu bytes needed, got %zu", need_scr,
+                    scratch ? scratch_bytes : 0);
+    ScanParams P = qkv_params(sh, g);
+    P.q = to_view(q);
+    P.k = to_view(k);
+    P.v = to_view(v);
+    P.planes = planes_T;
+    Carver cs(state, state_bytes);
+    P.wsB = cs.take(g.state_elems_B);
+    P.wsA = cs.take(g.state_elems_A);
+    const int64_t T = sh->T, D = sh->D;
+    const int64_t q_elems = (int64_t)sh->B * sh->Hq * T * D;
+    float *part = nullptr;
+    if (g.n_st > 1) {
+        Carver cw(scratch, scratch_bytes);
+        part = cw.take((size_t)g.n_st * q_elems);
+        P.out = OutView{part, (int64_t)sh->Hq * T * D, T * D, D, q_elems, 1};
+    } else {
+        P.out = to_out(out, out_dtype == RACE_F32);
+    }
+    const hipStream_t s = hs(stream);
+    RACE_TRY(run_scan_qkv(K_FWD_TOTALS, g, P, s));
+    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(run_scan_qkv(K_FWD_READOUT, g, P, s));
+    if (part)
+        RACE_TRY(hip_check(prof_reduce(part, g.n_st, q_elems, to_out(out, out_dtype == RACE_F32), sh->B,
+                                                  sh->Hq, sh->T, sh->D, s), "reduce partials"));
+    return RACE_OK;
+}
+
+int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v, race_tensor go,
+                 const float *planes_T, const void *state, size_t state_bytes, race_tensor dq, race_tensor dk,
+                 race_tensor dv, void *scratch, size_t scratch_bytes, race_stream stream)
+{
+    Geo g;
+    RACE_TRY(qkv_geometry(sh, g));
+    RACE_TRY(qkv_inputs(sh, q, k, v, planes_T, "race_qkv_bwd"));
+    RACE_TRY(check_view(go, "race_qkv_bwd: go", true));
+    RACE_TRY(check_view(dq, "race_qkv_bwd: dq", false));
+    RACE_TRY(check_view(dk, "race_qkv_bwd: dk", false));
+    RACE_TRY(check_view(dv, "race_qkv_bwd: dv", false));
+    const size_t need_state = race_qkv_state_bytes(sh), need_scr = qkv_scratch(sh, g, 1);
+    if (!state || state_bytes < need_state)
+        return fail(RACE_ERR_WORKSPACE, "race_qkv_bwd: state of %zu bytes needed, got %zu", need_state,
+                    state ? state_bytes : 0);
+    if (!scratch || scratch_bytes < need_scr)
+        return fail(RACE_ERR_WORKSPACE, "race_qkv_bwd: scratch of %zu bytes needed, got %zu", need_scr,
+                    scratch ? scratch_bytes : 0);
+    ScanParams P = qkv_params(sh, g);
+    P.q = to_view(q);
+    P.k = to_view(k);
+    P.v = to_view(v);
+    P.go = to_view(go);
+    P.planes = planes_T;
+    Carver cs(const_cast<void *>(state), state_bytes);
+    P.wsB = cs.take(g.state_elems_B);
+    P.wsA = cs.take(g.state_elems_A);
+    Carver cw(scratch, scratch_bytes);
+    P.ws2B = cw.take(g.state_elems_B);
+    P.ws2A = cw.take(g.state_elems_A);
+    const int64_t T = sh->T, D = sh->D;
+    const int64_t q_elems = (int64_t)sh->B * sh->Hq * T * D, kv_elems = (int64_t)sh->B * sh->Hkv * T * D;
+    float *pq = nullptr, *pk = nullptr, *pv = nullptr;
+    if (g.n_st > 1) {
+        pq = cw.take((size_t)g.n_st * q_elems);
+        pk = cw.take((size_t)g.n_st * kv_elems);
+        pv = cw.take((size_t)g.n_st * kv_elems);
+        P.dq = OutView{pq, (int64_t)sh->Hq * T * D, T * D, D, q_elems, 1};
+        P.dk = OutView{pk, (int64_t)sh->Hkv * T * D, T * D, D, kv_elems, 1};
+        P.dv = OutView{pv, (int64_t)sh->Hkv * T * D, T * D, D, kv_elems, 1};
+    } else {
+        P.dq = to_out(dq, 0);
+        P.dk = to_out(dk, 0);
+        P.dv = to_out(dv, 0);
+    }
+    const hipStream_t s = hs(stream);
+    RACE_TRY(run_scan_qkv(K_BWD_TOTALS, g, P, s));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(run_scan_qkv(K_BWD_MAIN, g, P, s));
+    if (g.n_st > 1) {
+        RACE_TRY(hip_check(prof_reduce(pq, g.n_st, q_elems, to_out(dq, 0), sh->B, sh->Hq, sh->T, sh->D, s),
+                           "reduce partials"));
+        RACE_TRY(hip_check(prof_reduce(pk, g.n_st, kv_elems, to_out(dk, 0), sh->B, sh->Hkv, sh->T, sh->D, s),
+                           "reduce partials"));
+        RACE_TRY(hip_check(prof_reduce(pv, g.n_st, kv_elems, to_out(dv, 0), sh->B, sh->Hkv, sh->T, sh->D, s),
+                           "reduce partials"));
+    }
+    return RACE_OK;
+}
+
+int race_qkv_final_state(const race_qkv_shape *sh, const void *state, size_t state_bytes, float *A, float *Bs,
+                         race_stream stream)
+{
+    Geo g;
+    RACE_TRY(qkv_geometry(sh, g));
+    const size_t need = race_qkv_state_bytes(sh);
+    if (!state || state_bytes < need)
+        return fail(RACE_ERR_WORKSPACE, "race_qkv_final_state: state of %zu bytes needed", need);
+    if (!A || !Bs)
+        return fail(RACE_ERR_INVALID, "race_qkv_final_state: null output");
+    Carver cs(const_cast<void *>(state), state_bytes);
+    const float *wsB = cs.take(g.state_elems_B);
+    const float *wsA = cs.take(g.state_elems_A);
+    const int S = sh->L << sh->K;
+    return hip_check(launch_state_extract(wsB, wsA, (int)g.NB, g.S_pad, g.DP, (int)g.Z, S, sh->D, A, Bs, hs(stream)),
+                     "race_qkv_final_state");
+}
+
+// ============================================================================ decode
+int race_decode_step(const race_decode_shape *sh, const void *q, const void *k, const void *v, int dtype,
+                     const float *planes_T, float *A, float *Bs, void *out, race_stream stream)
+{
+    if (!sh)
+        return fail(RACE_ERR_INVALID, "race_decode_step: null shape");
+    if (sh->B <= 0 || sh->Hq <= 0 || sh->Hkv <= 0 || sh->L <= 0)
+        return fail(RACE_ERR_INVALID, "race_decode_step: B, Hq, Hkv, L must be positive");
+    if (sh->Hq % sh->Hkv || sh->Hq / sh->Hkv > DEC_GMAX)
+        return fail(RACE_ERR_UNSUPPORTED, "race_decode_step: Hq/Hkv must be an integer <= %d", DEC_GMAX);
+    if (sh->D != 64 && sh->D != 128)
+        return fail(RACE_ERR_UNSUPPORTED, "race_decode_step: head dim %d, supported 64 and 128", sh->D);
+    if (sh->K < 1 || sh->K > 4 || sh->L * sh->K > DEC_LKMAX || (sh->L << sh->K) > DEC_SMAX)
+        return fail(RACE_ERR_UNSUPPORTED, "race_decode_step: K <= 4, L*K <= %d, L*2^K <= %d required", DEC_LKMAX,
+                    DEC_SMAX);
+    if (dtype != RACE_F32 && dtype != RACE_BF16)
+        return fail(RACE_ERR_INVALID, "race_decode_step: dtype must be RACE_F32 or RACE_BF16");
+    if (!q || !k || !v || !out || !A || !Bs || !planes_T)
+        return fail(RACE_ERR_INVALID, "race_decode_step: null pointer");
+    if (((uintptr_t)Bs & 15))
+        return fail(RACE_ERR_INVALID, "race_decode_step: state Bs must be 16-byte aligned");
+    if (!(sh->eps > 0.0f) || !(sh->scale > 0.0f))
+        return fail(RACE_ERR_INVALID, "race_decode_step: eps and scale must be positive");
+    DecodeParams P;
+    std::memset(&P, 0, sizeof(P));
+    P.q = q;
+    P.k = k;
+    P.v = v;
+    P.out = out;
+    P.A = A;
+    P.Bs = Bs;
+    P.planes = planes_T;
+    P.B = sh->B;
+    P.Hkv = sh->Hkv;
+    P.G = sh->Hq / sh->Hkv;
+    P.D = sh->D;
+    P.L = sh->L;
+    P.K = sh->K;
+    P.round_planes = dtype == RACE_BF16;
+    P.eps = sh->eps;
+    P.inv_scale = 1.0f / sh->scale;
+    return hip_check(prof_decode(P, dtype == RACE_BF16, hs(stream)), "race_decode_step");
+}
+
+// ============================================================================ kernel timing
+int race_profile_enable(int on)
+{
+    Profiler &p = prof();
+    std::lock_guard<std::mutex> g(p.mu);
+    p.on = on != 0;
+    return RACE_OK;
+}
+
+int race_profile_read(int kernel, double *total_ms, int64_t *launches)
+{
+    if (kernel < 0 || kernel >= RACE_PROF_KERNELS || !total_ms || !launches)
+        return fail(RACE_ERR_INVALID, "race_profile_read: bad kernel id or null output");
+    Profiler &p = prof();
+    std::vector<EventPair> evs;
+    {
+        std::lock_guard<std::mutex> g(p.mu);
+        evs.swap(p.pending[kernel]);
+    }
+    double add = 0.0;
+    int rc = RACE_OK;
+    for (const EventPair &e : evs) {
+        float ms = 0.0f;
+        if (rc == RACE_OK) {
+            hipError_t err = hipEventSynchronize(e.b);
+            if (err == hipSuccess)
+                err = hipEventElapsedTime(&ms, e.a, e.b);
+            if (err != hipSuccess)
+                rc = hip_check(err, "race_profile_read");
+        }
+        add += ms;
+        (void)hipEventDestroy(e.a);
+        (void)hipEventDestroy(e.b);
+    }
+    std::lock_guard<std::mutex> g(p.mu);
+    p.total_ms[kernel] += add;
+    p.count[kernel] += (int64_t)evs.size();
+    *total_ms = p.total_ms[kernel];
+    *launches = p.count[kernel];
+    return rc;
+}
+
+int race_profile_reset(void)
+{
+    Profiler &p = prof();
+    std::vector<EventPair> evs;
+    {
+        std::lock_guard<std::mutex> g(p.mu);
+        for (int k = 0; k < RACE_PROF_KERNELS; ++k) {
+            evs.insert(evs.end(), p.pending[k].begin(), p.pending[k].end());
+            p.pending[k].clear();
+            p.total_ms[k] = 0.0;
+            p.count[k] = 0;
+        }
+    }
+    for (const EventPair &e : evs) {
+        (void)hipEventSynchronize(e.b);
+        (void)hipEventDestroy(e.a);
+        (void)hipEventDestroy(e.b);
+    }
+    return RACE_OK;
+}
+
+}  // extern "C"

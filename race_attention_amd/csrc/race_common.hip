@@ -1,0 +1,401 @@
+// Small kernels around the chunked scan:
+//   race_block_scan        prefix / suffix scan of block states (fp64 running sums)
+//   race_reduce_partials   sum of per-bucket-tile partial outputs
+//   race_softhash_fwd      probs [N,T,L*R] from x [B,H,T,D] (scaling/race_common.py:36-73)
+//   race_softhash_bwd      dx from d(probs) (torch autograd of the same map)
+//   race_decode_step       fused single-token GQA decode with carried state
+//   race_state_extract     final (A, B) state of a forward pass -> decode state
+#include "race_decode.h"
+#include "race_device.h"
+#include "race_launch.h"
+#include "race_softhash.h"
+
+namespace race {
+
+// ============================================================================ block scan
+__global__ void race_block_scan(float *ws, int64_t elems, int NB, int rev)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= elems)
+        return;
+    float *base = ws + (int64_t)blockIdx.y * (NB + 1) * elems + e;
+    double run = 0.0;
+    if (!rev) {
+        for (int b = 0; b <= NB; ++b) {
+            const float x = (b < NB) ? base[(int64_t)b * elems] : 0.0f;
+            base[(int64_t)b * elems] = (float)run;
+            run += (double)x;
+        }
+    } else {
+        base[(int64_t)NB * elems] = 0.0f;
+        for (int b = NB - 1; b >= 0; --b) {
+            run += (double)base[(int64_t)b * elems];
+            base[(int64_t)b * elems] = (float)run;
+        }
+    }
+}
+
+hipError_t launch_block_scan(float *ws, int64_t elems, int NB, int Z, int rev, hipStream_t s)
+{
+    const dim3 grid((unsigned)((elems + 255) / 256), (unsigned)Z);
+    hipLaunchKernelGGL(race_block_scan, grid, dim3(256), 0, s, ws, elems, NB, rev);
+    return hipGetLastError();
+}
+
+// ============================================================================ partial sums
+__global__ void race_reduce_partials(const float *part, int n_st, int64_t tile, OutView out, int H,
+                                     int T, int D, int64_t total)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total)
+        return;
+    float acc = 0.0f;
+    for (int st = 0; st < n_st; ++st)
+        acc += part[(int64_t)st * tile + i];
+    const int d = (int)(i % D);
+    const int64_t r = i / D;
+    const int t = (int)(r % T);
+    const int64_t bh = r / T;
+    const int h = (int)(bh % H);
+    const int64_t b = bh / H;
+    const int64_t off = b * out.sb + h * out.sh + (int64_t)t * out.st + d;
+    if (out.f32)
+        reinterpret_cast<float *>(out.p)[off] = acc;
+    else
+        reinterpret_cast<__bf16 *>(out.p)[off] = (__bf16)acc;
+}
+
+hipError_t launch_reduce_partials(const float *part, int n_st, int64_t tile, const OutView &out,
+                                  int B, int H, int T, int D, hipStream_t s)
+{
+    const int64_t total = (int64_t)B * H * T * D;
+    hipLaunchKernelGGL(race_reduce_partials, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       part, n_st, tile, out, H, T, D, total);
+    return hipGetLastError();
+}
+
+// ============================================================================ soft-hash
+// Per table: p[r] = prod_k (bit_k(r) ? s1_k : s0_k), s1 = sigmoid(2u), s0 = sigmoid(-2u),
+// generic over K <= 8 (probabilities written directly, O(R*K) per table).
+RACE_DEV void sigm_pair(float u, float &s0, float &s1)
+{
+    const float e = __expf(-2.0f * u);
+    s1 = frcp(1.0f + e);
+    s0 = e * s1;
+}
+
+RACE_DEV float corner_prob(const float *s0, const float *s1, int K, int r)
+{
+    float p = 1.0f;
+    for (int k = 0; k < K; ++k)
+        p *= ((r >> (K - 1 - k)) & 1) ? s1[k] : s0[k];
+    return p;
+}
+
+template <class TX>
+__global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
+{
+    extern __shared__ float sm[];
+    float *sPl = sm;                     // [D][LK]
+    float *sX = sPl + P.D * P.LK;        // [TT][D]
+    float *sU = sX + SH_TT * P.D;        // [TT][LK]
+    const int bh = blockIdx.y;
+    const int m = blockIdx.z;            // ensemble member (unshared planes) or 0
+    const int t0 = blockIdx.x * SH_TT;
+    const int nv = min(SH_TT, P.T - t0);
+    const int b = bh / P.H, h = bh % P.H;
+    const float *planes = P.planes + (int64_t)m * P.plane_stride;
+    for (int i = threadIdx.x; i < P.D * P.LK; i += blockDim.x)
+        sPl[i] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
+    const TX *x = reinterpret_cast<const TX *>(P.x.p);
+    for (int i = threadIdx.x; i < SH_TT * P.D; i += blockDim.x) {
+        const int r = i / P.D, d = i % P.D;
+        sX[i] = (r < nv) ? (float)x[b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d] : 0.0f;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < SH_TT * P.LK; i += blockDim.x) {
+        const int r = i / P.LK, j = i % P.LK;
+        float acc = 0.0f;
+        for (int d = 0; d < P.D; ++d)
+            acc += sX[r * P.D + d] * sPl[d * P.LK + j];
+        sU[i] = tanh_f(acc) * P.inv_scale;
+    }
+    __syncthreads();
+    const int R = 1 << P.K, S = P.L * R;
+    float *out = P.probs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
+    for (int i = threadIdx.x; i < nv * P.L; i += blockDim.x) {
+        const int r = i / P.L, l = i % P.L;
+        float s0[8], s1[8];
+        for (int k = 0; k < P.K; ++k)
+            sigm_pair(sU[r * P.LK + l * P.K + k], s0[k], s1[k]);
+        float *o = out + (int64_t)(t0 + r) * S + l * R;
+        for (int c = 0; c < R; ++c)
+            o[c] = corner_prob(s0, s1, P.K, c);
+    }
+}
+
+// dx[b,h,t,:] = sum_m sum_j gproj_m[t,j] planes_m[:, j]
+template <class TX>
+__global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
+{
+    extern __shared__ float sm[];
+    float *sPl = sm;
+    float *sX = sPl + P.D * P.LK;
+    float *sU = sX + SH_TT * P.D;
+    float *sGP = sU + SH_TT * P.LK;  // [TT][LK]
+    const int bh = blockIdx.y;
+    const int t0 = blockIdx.x * SH_TT;
+    const int nv = min(SH_TT, P.T - t0);
+    const int b = bh / P.H, h = bh % P.H;
+    const TX *x = reinterpret_cast<const TX *>(P.x.p);
+    for (int i = threadIdx.x; i < SH_TT * P.D; i += blockDim.x) {
+        const int r = i / P.D, d = i % P.D;
+        sX[i] = (r < nv) ? (float)x[b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d] : 0.0f;
+    }
+    const int R = 1 << P.K, S = P.L * R;
+    constexpr int MAXO = (SH_TT * 256 + 255) / 256;  // outputs per thread for D <= 256
+    float gx[MAXO];
+    for (int o = 0; o < MAXO; ++o)
+        gx[o] = 0.0f;
+    for (int m = 0; m < P.M; ++m) {
+        const float *planes = P.planes + (int64_t)(P.unshared ? m : 0) * P.plane_stride;
+        __syncthreads();
+        for (int i = threadIdx.x; i < P.D * P.LK; i += blockDim.x)
+            sPl[i] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
+        __syncthreads();
+        for (int i = threadIdx.x; i < SH_TT * P.LK; i += blockDim.x) {
+            const int r = i / P.LK, j = i % P.LK;
+            float acc = 0.0f;
+            for (int d = 0; d < P.D; ++d)
+                acc += sX[r * P.D + d] * sPl[d * P.LK + j];
+            sU[i] = tanh_f(acc) * P.inv_scale;
+        }
+        __syncthreads();
+        const float *gprobs = P.gprobs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
+        for (int i = threadIdx.x; i < SH_TT * P.L; i += blockDim.x) {
+            const int r = i / P.L, l = i % P.L;
+            float u[8], s0[8], s1[8], gu[8];
+            for (int k = 0; k < P.K; ++k) {
+                u[k] = sU[r * P.LK + l * P.K + k];
+                sigm_pair(u[k], s0[k], s1[k]);
+                gu[k] = 0.0f;
+            }
+            if (r < nv) {
+                const float *gp = gprobs + (int64_t)(t0 + r) * S + l * R;
+                float dot = 0.0f;
+                for (int c = 0; c < R; ++c)
+                    dot += corner_prob(s0, s1, P.K, c) * gp[c];
+                for (int c = 0; c < R; ++c) {
+                    const float gz = corner_prob(s0, s1, P.K, c) * (gp[c] - dot);
+                    for (int k = 0; k < P.K; ++k)
+                        gu[k] += ((c >> (P.K - 1 - k)) & 1) ? gz : -gz;
+                }
+            }
+            for (int k = 0; k < P.K; ++k) {
+                const float th = u[k] * P.scale;
+                sGP[r * P.LK + l * P.K + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+            }
+        }
+        __syncthreads();
+        for (int o = 0; o < MAXO; ++o) {
+            const int i = threadIdx.x + o * 256;
+            if (i < SH_TT * P.D) {
+                const int r = i / P.D, d = i % P.D;
+                float acc = 0.0f;
+                for (int j = 0; j < P.LK; ++j)
+                    acc += sGP[r * P.LK + j] * sPl[d * P.LK + j];
+                gx[o] += acc;
+            }
+        }
+    }
+    TX *dx = reinterpret_cast<TX *>(const_cast<void *>(P.dx.p));
+    for (int o = 0; o < MAXO; ++o) {
+        const int i = threadIdx.x + o * 256;
+        if (i < SH_TT * P.D) {
+            const int r = i / P.D, d = i % P.D;
+            if (r < nv)
+                dx[b * P.dx.sb + h * P.dx.sh + (int64_t)(t0 + r) * P.dx.st + d] = (TX)gx[o];
+        }
+    }
+}
+
+size_t softhash_smem(int D, int LK, bool bwd)
+{
+    return sizeof(float) * ((size_t)D * LK + (size_t)SH_TT * D + (size_t)SH_TT * LK * (bwd ? 2 : 1));
+}
+
+hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s)
+{
+    const dim3 grid((unsigned)((P.T + SH_TT - 1) / SH_TT), (unsigned)(P.B * P.H),
+                    (unsigned)(bwd ? 1 : (P.unshared ? P.M : 1)));
+    const size_t smem = softhash_smem(P.D, P.LK, bwd);
+    if (bwd) {
+        if (bf16)
+            hipLaunchKernelGGL(race_softhash_bwd<__bf16>, grid, dim3(256), smem, s, P);
+        else
+            hipLaunchKernelGGL(race_softhash_bwd<float>, grid, dim3(256), smem, s, P);
+    } else {
+        if (bf16)
+            hipLaunchKernelGGL(race_softhash_fwd<__bf16>, grid, dim3(256), smem, s, P);
+        else
+            hipLaunchKernelGGL(race_softhash_fwd<float>, grid, dim3(256), smem, s, P);
+    }
+    return hipGetLastError();
+}
+
+hipError_t softhash_prepare(int D, int LK)
+{
+    const int smem = (int)softhash_smem(D, LK, true);
+    hipError_t e = hipSuccess;
+    if (smem > 64 * 1024) {
+        e = hipFuncSetAttribute((const void *)race_softhash_fwd<float>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)race_softhash_fwd<__bf16>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)race_softhash_bwd<float>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)race_softhash_bwd<__bf16>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    }
+    return e;
+}
+
+// ============================================================================ decode
+// One workgroup per (sequence b, kv head hk). State A [S], Bs [S][D] fp32 in HBM,
+// updated in place: A += pK, Bs += pK (x) v (inclusive prefix: the new token is
+// part of its own readout), then out_g = sum_s pQ_g[s] Bs[s,:] / (A[s] + eps)
+// for the G query heads of the group.
+template <class TX, int D>
+__global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
+{
+    constexpr int VEC = 4, TPR = D / VEC, RIF = 256 / TPR;  // threads per row, rows in flight
+    __shared__ float sIn[DEC_GMAX + 2][D];                  // k, v, q_0..q_{G-1}
+    __shared__ float sU[DEC_GMAX + 1][DEC_LKMAX];           // u for k, q_g
+    __shared__ float sP[DEC_GMAX + 1][DEC_SMAX];            // pK, pQ_g
+    __shared__ float sRed[RIF][DEC_GMAX][D];
+    const int z = blockIdx.x;                                // b * Hkv + hk
+    const int b = z / P.Hkv, hk = z % P.Hkv;
+    const int G = P.G, LK = P.L * P.K, R = 1 << P.K, S = P.L * R;
+    const TX *q = reinterpret_cast<const TX *>(P.q);
+    const TX *k = reinterpret_cast<const TX *>(P.k);
+    const TX *v = reinterpret_cast<const TX *>(P.v);
+    for (int i = threadIdx.x; i < (G + 2) * D; i += 256) {
+        const int row = i / D, d = i % D;
+        float x;
+        if (row == 0)
+            x = (float)k[((int64_t)b * P.Hkv + hk) * D + d];
+        else if (row == 1)
+            x = (float)v[((int64_t)b * P.Hkv + hk) * D + d];
+        else
+            x = (float)q[((int64_t)b * P.Hkv * G + hk * G + (row - 2)) * D + d];
+        sIn[row][d] = x;
+    }
+    __syncthreads();
+    // projections: row 0 = k, rows 1.. = q_g
+    for (int i = threadIdx.x; i < (G + 1) * LK; i += 256) {
+        const int row = i / LK, j = i % LK;
+        const float *x = sIn[row == 0 ? 0 : row + 1];
+        float acc = 0.0f;
+        for (int d = 0; d < D; ++d) {
+            const float pl = P.planes[d * LK + j];
+            acc += x[d] * (P.round_planes ? (float)(__bf16)pl : pl);
+        }
+        sU[row][j] = tanh_f(acc) * P.inv_scale;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < (G + 1) * P.L; i += 256) {
+        const int row = i / P.L, l = i % P.L;
+        float u[4], p[16];
+        for (int kk = 0; kk < 4; ++kk)
+            u[kk] = (kk < P.K) ? sU[row][l * P.K + kk] : 0.0f;
+        expand_probs(u, P.K, p);
+        for (int r = 0; r < 16; ++r)
+            if (r < R)
+                sP[row][l * R + r] = p[r];
+    }
+    __syncthreads();
+    // state update + readout
+    const int rr = threadIdx.x / TPR, dv = (threadIdx.x % TPR) * VEC;
+    float acc[DEC_GMAX][VEC];
+    for (int g = 0; g < DEC_GMAX; ++g)
+        for (int e = 0; e < VEC; ++e)
+            acc[g][e] = 0.0f;
+    float *A = P.A + (int64_t)z * S;
+    float *Bs = P.Bs + (int64_t)z * S * D;
+    float vv[VEC];
+    for (int e = 0; e < VEC; ++e)
+        vv[e] = sIn[1][dv + e];
+    for (int s = rr; s < S; s += RIF) {
+        const float pk = sP[0][s];
+        const float a = A[s] + pk;
+        f32x4 bv = *reinterpret_cast<const f32x4 *>(Bs + (int64_t)s * D + dv);
+        for (int e = 0; e < VEC; ++e)
+            bv[e] += pk * vv[e];
+        *reinterpret_cast<f32x4 *>(Bs + (int64_t)s * D + dv) = bv;
+        if (dv == 0)
+            A[s] = a;
+        const float inv = frcp(a + P.eps);
+        for (int g = 0; g < DEC_GMAX; ++g)
+            if (g < G) {
+                const float w = sP[1 + g][s] * inv;
+                for (int e = 0; e < VEC; ++e)
+                    acc[g][e] += w * bv[e];
+            }
+    }
+    for (int g = 0; g < DEC_GMAX; ++g)
+        if (g < G)
+            for (int e = 0; e < VEC; ++e)
+                sRed[rr][g][dv + e] = acc[g][e];
+    __syncthreads();
+    TX *out = reinterpret_cast<TX *>(P.out);
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        float sum = 0.0f;
+        for (int r = 0; r < RIF; ++r)
+            sum += sRed[r][g][d];
+        out[((int64_t)b * P.Hkv * G + hk * G + g) * D + d] = (TX)sum;
+    }
+}
+
+hipError_t launch_decode(const DecodeParams &P, int bf16, hipStream_t s)
+{
+    const dim3 grid((unsigned)(P.B * P.Hkv));
+#define DEC(TX, DD) hipLaunchKernelGGL((race_decode_step<TX, DD>), grid, dim3(256), 0, s, P)
+    if (P.D == 64) {
+        if (bf16) DEC(__bf16, 64); else DEC(float, 64);
+    } else if (P.D == 128) {
+        if (bf16) DEC(__bf16, 128); else DEC(float, 128);
+    } else {
+        return hipErrorInvalidValue;
+    }
+#undef DEC
+    return hipGetLastError();
+}
+
+// final state slot NB of a forward workspace -> dense decode state
+__global__ void race_state_extract(const float *wsB, const float *wsA, int NB, int S_pad, int DPw,
+                                   int S, int D, float *A, float *Bs, int64_t total)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total)
+        return;
+    const int d = (int)(i % (D + 1));
+    const int64_t r = i / (D + 1);
+    const int s = (int)(r % S);
+    const int64_t z = r / S;
+    const int64_t slot = z * (NB + 1) + NB;
+    if (d == D)
+        A[z * S + s] = wsA[slot * S_pad + s];
+    else
+        Bs[(z * S + s) * D + d] = wsB[(slot * S_pad + s) * DPw + d];
+}
+
+hipError_t launch_state_extract(const float *wsB, const float *wsA, int NB, int S_pad, int DPw,
+                                int Z, int S, int D, float *A, float *Bs, hipStream_t s)
+{
+    const int64_t total = (int64_t)Z * S * (D + 1);
+    hipLaunchKernelGGL(race_state_extract, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       wsB, wsA, NB, S_pad, DPw, S, D, A, Bs, total);
+    return hipGetLastError();
+}
+
+}  // namespace race

@@ -1,0 +1,37 @@
+// Host-side launch interface between the C-ABI layer and the kernel objects.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "race_params.h"
+
+namespace race {
+
+enum ScanKernel { K_FWD_TOTALS = 0, K_FWD_READOUT = 1, K_BWD_TOTALS = 2, K_BWD_MAIN = 3 };
+
+// Tile geometry of one compiled variant.
+struct Variant {
+    int ST;  // buckets per workgroup tile
+    int DP;  // padded head dim
+    int C;   // tokens per sub-chunk
+    int NW;  // waves per workgroup
+};
+
+// bf16 fused q/k/v variants (race_scan_qkv.hip). Returns hipErrorInvalidValue for
+// an uncompiled (ST, DP) pair.
+hipError_t launch_scan_qkv(ScanKernel k, int ST, int DP, const ScanParams &P, dim3 grid,
+                           hipStream_t s);
+// fp32 probabilities-in variants (race_scan_op.hip).
+hipError_t launch_scan_op(ScanKernel k, int ST, int DP, const ScanParams &P, dim3 grid,
+                          hipStream_t s);
+bool qkv_variant_exists(int ST, int DP);
+bool op_variant_exists(int ST, int DP);
+constexpr int QKV_C = 32, QKV_NW = 4;
+constexpr int OP_C = 16, OP_NW = 4;
+
+// race_common.hip
+hipError_t launch_block_scan(float *ws, int64_t elems, int NB, int Z, int rev, hipStream_t s);
+// out[i] (view, f32 or bf16) = sum_{st < n_st} part[st * tile + i] over a [B][H][T][D] box
+hipError_t launch_reduce_partials(const float *part, int n_st, int64_t tile, const OutView &out,
+                                  int B, int H, int T, int D, hipStream_t s);
+
+}  // namespace race

@@ -1,0 +1,45 @@
+// Kernel parameter blocks shared by the HIP kernels and the host dispatch code.
+#pragma once
+#include <stdint.h>
+
+namespace race {
+
+// A [B][H][T][D] tensor view with contiguous last dim (element strides).
+struct View {
+    const void *p;
+    int64_t sb, sh, st;
+};
+
+// An output view: like View, plus the element stride between s-tile partials
+// (0 when the kernel writes the final tensor) and the element type.
+struct OutView {
+    void *p;
+    int64_t sb, sh, st;
+    int64_t tile;   // element offset added per s-tile (partial-sum buffers)
+    int f32;        // 1: float32 elements, 0: bfloat16 elements
+};
+
+// One launch of the chunked causal scan.
+//   stream z:  op mode   z = n (one of N independent [T,S]/[T,D] streams)
+//              qkv mode  z = b * Hkv + hk (one kv head; query heads hk*G .. hk*G+G-1)
+//   grid:      (NB blocks along T, n_st bucket tiles, Z streams)
+struct ScanParams {
+    int T, S, D, L, K, R;  // tokens, buckets S = L*R, head dim, tables, bits, 2^K
+    int G, Hkv;            // query heads per kv head, kv heads (qkv mode)
+    int CB, NB;            // tokens per block, blocks
+    int n_st, S_pad;       // bucket tiles per stream, n_st * tile
+    int DPw;               // padded head dim used by the state workspaces
+    float eps, scale, inv_scale;
+    // qkv mode (bf16 activations; planes_T fp32 [D][L*K], shared by all heads)
+    View q, k, v, go;
+    OutView out, dq, dk, dv;
+    const float *planes;
+    // op mode (fp32): probabilities [N][T][S], values/grads [N][T][D]
+    const float *pK, *pQ, *V, *gO;
+    float *gpK, *gpQ;
+    // workspaces: block states [Z][NB+1][S_pad][DPw] and [Z][NB+1][S_pad]
+    float *wsB, *wsA;    // forward: prefix (A, B) at each block start; slot NB = final
+    float *ws2B, *ws2A;  // backward: suffix sums (of W^T go, gA) from each block's start
+};
+
+}  // namespace race

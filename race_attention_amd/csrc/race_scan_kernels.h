@@ -1,0 +1,988 @@
+// The four chunked-scan kernels (see race_scan.h for the math and layout).
+//   race_fwd_totals   per-block totals (sum pK, sum pK^T v) -> workspace slot blk
+//   race_fwd_readout  per-block causal readout from the block-start state
+//   race_bwd_totals   forward-order pass: gpQ (op) / dq (qkv) and per-block
+//                     totals of gA and W^T go -> backward workspace slot blk
+//   race_bwd_main     forward-order pass with reverse suffix states: gpK, gv (op) / dk, dv (qkv)
+#pragma once
+#include "race_scan.h"
+
+namespace race {
+
+struct PredTrilIncl {  // k <= m
+    RACE_DEV bool operator()(int m, int k) const { return k <= m; }
+};
+struct PredTriuStrict {  // k > m
+    RACE_DEV bool operator()(int m, int k) const { return k > m; }
+};
+struct PredAll {
+    RACE_DEV bool operator()(int, int) const { return true; }
+};
+
+// Store an accumulator tile to a [B][H][T][D] output (rows < nv, cols < D).
+RACE_DEV void store_out_tile(const OutView &o, int b, int h, int st, int t0, int nv, int D,
+                             int m0, int n0, int lane, const f32x4 &v)
+{
+    const int r = acc_row(m0, lane), col = acc_col(n0, lane);
+    if (col >= D)
+        return;
+    const int64_t base = (int64_t)st * o.tile;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (r + e < nv) {
+            const int64_t off = base + row_off(o, b, h, t0 + r + e) + col;
+            if (o.f32)
+                reinterpret_cast<float *>(o.p)[off] = v[e];
+            else
+                reinterpret_cast<__bf16 *>(o.p)[off] = (__bf16)v[e];
+        }
+    }
+}
+
+// Store an accumulator tile of per-bucket values to an [N][T][S] fp32 tensor.
+RACE_DEV void store_probs_tile(float *dst, int S, int s0, int S_here, int t0, int nv, int m0,
+                               int n0, int lane, const f32x4 &v)
+{
+    const int r = acc_row(m0, lane), col = acc_col(n0, lane);
+    if (col >= S_here)
+        return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (r + e < nv)
+            dst[(int64_t)(t0 + r + e) * S + s0 + col] = v[e];
+}
+
+template <class T>
+RACE_DEV void zero_lds(T *p, int n, int tid, int nth)
+{
+    for (int i = tid; i < n; i += nth)
+        p[i] = (T)0.0f;
+}
+
+// ============================================================================ forward totals
+template <class E, int MODE, int ST, int DP, int C, int NW>
+__global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
+{
+    using CF = Cfg<E, MODE, ST, DP, C, NW>;
+    using T = typename E::T;
+    constexpr int PD = CF::PD, NTH = CF::NTH;
+    constexpr int LDX = DP + PD, LDC = C + PD, LDU = CF::LKPM + 1;
+    constexpr int XR = CF::QKV ? C : 1;
+    __shared__ __align__(16) T sX[XR][LDX];
+    __shared__ __align__(16) T sVt[DP][LDC];
+    __shared__ __align__(16) float sU[XR][LDU];
+    __shared__ __align__(16) T sPKt[ST][LDC];
+
+    const Ctx c = make_ctx(P, ST);
+    PlaneFrags<E, CF> pf;
+    if constexpr (CF::QKV)
+        pf.load(P, c);
+    zero_lds(&sPKt[0][0], ST * LDC, c.tid, NTH);
+
+    constexpr int TPW_A1 = (CF::NTS + NW - 1) / NW;
+    f32x4 accS[CF::TPW_SD], accA[TPW_A1];
+#pragma unroll
+    for (int i = 0; i < CF::TPW_SD; ++i)
+        accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < TPW_A1; ++i)
+        accA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        if constexpr (CF::QKV) {
+            load_rows_bf16<C, DP, NTH, LDX, LDC, true, false>(&sX[0][0], nullptr, P.k, c.b, c.hk, t0, nv, c.tid);
+            load_rows_bf16<C, DP, NTH, LDX, LDC, false, true>(nullptr, &sVt[0][0], P.v, c.b, c.hk, t0, nv, c.tid);
+            __syncthreads();
+            project<E, CF, LDX, LDU>(&sX[0][0], &sU[0][0], pf, c, P.inv_scale);
+            __syncthreads();
+            const int R = P.R;
+            expand<CF, LDU>(&sU[0][0], c, P.K, [&](int t, int lt, const float *, const float *pr) {
+                const bool ok = t < nv;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (r < R)
+                        sPKt[lt * R + r][t] = (T)(ok ? pr[r] : 0.0f);
+            });
+        } else {
+            load_probs<T, C, ST, NTH, LDC, LDC, false, true>(nullptr, &sPKt[0][0], P.pK + (int64_t)c.z * P.T * P.S,
+                                                           P.S, c.s0, c.S_here, t0, nv, c.tid);
+            load_rows_f32<C, DP, NTH, LDC, LDC, false, true>(nullptr, reinterpret_cast<float *>(&sVt[0][0]),
+                                                           P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < CF::NTS * CF::NTD)
+                mma_tile<E, C>(accS[i], &sPKt[0][0], LDC, &sVt[0][0], LDC, (t / CF::NTD) * 16,
+                               (t % CF::NTD) * 16, c.lane);
+        }
+#pragma unroll
+        for (int i = 0; i < TPW_A1; ++i) {
+            const int tn = c.wave + i * NW;
+            if (tn < CF::NTS)
+                mma_tile_gen<E, C>(accA[i], PredAll(), 1.0f, &sPKt[0][0], LDC, 0, tn * 16, c.lane);
+        }
+        __syncthreads();
+    }
+
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+    for (int i = 0; i < CF::TPW_SD; ++i) {
+        const int t = c.wave + i * NW;
+        if (t < CF::NTS * CF::NTD) {
+            const int r = acc_row((t / CF::NTD) * 16, c.lane), col = acc_col((t % CF::NTD) * 16, c.lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                wB[(int64_t)(r + e) * P.DPw + col] = accS[i][e];
+        }
+    }
+    float *wA = P.wsA + slot * P.S_pad + c.s0;
+#pragma unroll
+    for (int i = 0; i < TPW_A1; ++i) {
+        const int tn = c.wave + i * NW;
+        if (tn < CF::NTS && c.lane < 16)
+            wA[tn * 16 + c.lane] = accA[i][0];
+    }
+}
+
+// ============================================================================ forward readout
+template <class E, int MODE, int ST, int DP, int C, int NW>
+__global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
+{
+    using CF = Cfg<E, MODE, ST, DP, C, NW>;
+    using T = typename E::T;
+    constexpr int PD = CF::PD, NTH = CF::NTH, MTC = CF::MTC;
+    constexpr int LDX = DP + PD, LDC = C + PD, LDS_ = ST + PD, LDU = CF::LKPM + 1, LDF = ST + 4;
+    constexpr int XR = CF::QKV ? C : 1;
+    __shared__ __align__(16) T sX[XR][LDX];
+    __shared__ __align__(16) T sVt[DP][LDC];
+    __shared__ __align__(16) float sU[XR][LDU];
+    __shared__ __align__(16) T sPK[C][LDS_];
+    __shared__ __align__(16) T sPKt[ST][LDC];
+    __shared__ __align__(16) float sF[C][LDF];
+    __shared__ __align__(16) T sW[C][LDS_];
+    __shared__ __align__(16) T sStT[DP][LDS_];
+    __shared__ __align__(16) T sPm[C][LDC];
+    __shared__ float sA0[ST];
+
+    const Ctx c = make_ctx(P, ST);
+    PlaneFrags<E, CF> pf;
+    if constexpr (CF::QKV)
+        pf.load(P, c);
+    zero_lds(&sPK[0][0], C * LDS_, c.tid, NTH);
+    zero_lds(&sPKt[0][0], ST * LDC, c.tid, NTH);
+    zero_lds(&sF[0][0], C * LDF, c.tid, NTH);
+
+    // block-start state
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    f32x4 accS[CF::TPW_SD];
+    {
+        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (t < CF::NTS * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                const int r = acc_row(m0, c.lane), col = acc_col(n0, c.lane);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accS[i][e] = wB[(int64_t)(r + e) * P.DPw + col];
+                st_cm(&sStT[0][0], LDS_, m0, n0, c.lane, accS[i]);
+            }
+        }
+        const float *wA = P.wsA + slot * P.S_pad + c.s0;
+        for (int s = c.tid; s < ST; s += NTH)
+            sA0[s] = wA[s];
+    }
+    __syncthreads();
+
+    f32x4 accA[CF::TPW_CS];
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        if constexpr (CF::QKV) {
+            load_rows_bf16<C, DP, NTH, LDX, LDC, true, false>(&sX[0][0], nullptr, P.k, c.b, c.hk, t0, nv, c.tid);
+            load_rows_bf16<C, DP, NTH, LDX, LDC, false, true>(nullptr, &sVt[0][0], P.v, c.b, c.hk, t0, nv, c.tid);
+            __syncthreads();
+            project<E, CF, LDX, LDU>(&sX[0][0], &sU[0][0], pf, c, P.inv_scale);
+            __syncthreads();
+            const int R = P.R;
+            expand<CF, LDU>(&sU[0][0], c, P.K, [&](int t, int lt, const float *, const float *pr) {
+                const bool ok = t < nv;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (r < R) {
+                        const T x = (T)(ok ? pr[r] : 0.0f);
+                        sPK[t][lt * R + r] = x;
+                        sPKt[lt * R + r][t] = x;
+                    }
+            });
+        } else {
+            const float *pk = P.pK + (int64_t)c.z * P.T * P.S;
+            load_probs<T, C, ST, NTH, LDS_, LDC, true, true>(&sPK[0][0], &sPKt[0][0], pk, P.S, c.s0, c.S_here, t0, nv, c.tid);
+            load_probs<float, C, ST, NTH, LDF, LDF, true, false>(&sF[0][0], nullptr, P.pQ + (int64_t)c.z * P.T * P.S,
+                                                               P.S, c.s0, c.S_here, t0, nv, c.tid);
+            load_rows_f32<C, DP, NTH, LDC, LDC, false, true>(nullptr, reinterpret_cast<float *>(&sVt[0][0]),
+                                                           P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+        }
+        __syncthreads();
+
+        // A = A0 + Tri pK  (and its last row: the carry into the next sub-chunk)
+        float carry[CF::TPW_CS];
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            carry[i] = 0.0f;
+            if (tn < CF::NTS) {
+                const float a0 = sA0[tn * 16 + (c.lane & 15)];
+                accA[i] = f32x4{a0, a0, a0, a0};
+                mma_tile_gen<E, C>(accA[i], PredTrilIncl(), 1.0f, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
+                carry[i] = accA[i][3];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            if (tn < CF::NTS && tm == MTC - 1 && (c.lane >> 4) == 3)
+                sA0[tn * 16 + (c.lane & 15)] = carry[i];
+        }
+
+        const int G = CF::QKV ? P.G : 1;
+        for (int g = 0; g < G; ++g) {
+            const int hq = c.hk * P.G + g;
+            if constexpr (CF::QKV) {
+                load_rows_bf16<C, DP, NTH, LDX, LDC, true, false>(&sX[0][0], nullptr, P.q, c.b, hq, t0, nv, c.tid);
+                __syncthreads();
+                project<E, CF, LDX, LDU>(&sX[0][0], &sU[0][0], pf, c, P.inv_scale);
+                __syncthreads();
+                const int R = P.R;
+                expand<CF, LDU>(&sU[0][0], c, P.K, [&](int t, int lt, const float *, const float *pr) {
+                    const bool ok = t < nv;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (r < R)
+                            sF[t][lt * R + r] = ok ? pr[r] : 0.0f;
+                });
+                __syncthreads();
+            }
+            // W = pQ / (A + eps)
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CS; ++i) {
+                const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+                if (tn < CF::NTS) {
+                    const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        sW[r + e][col] = (T)(sF[r + e][col] * frcp(accA[i][e] + P.eps));
+                }
+            }
+            __syncthreads();
+            // Pm = tril(W pK^T);  out = W St
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CC; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int tm = t / MTC, tn = t % MTC;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_tile<E, ST>(acc, &sW[0][0], LDS_, &sPK[0][0], LDS_, tm * 16, tn * 16, c.lane);
+                    const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col > r + e)
+                            acc[e] = 0.0f;
+                    st_rm(&sPm[0][0], LDC, tm * 16, tn * 16, c.lane, acc);
+                }
+            }
+            f32x4 accO[CF::TPW_CD];
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CD; ++i) {
+                const int t = c.wave + i * NW;
+                accO[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (t < MTC * CF::NTD)
+                    mma_tile<E, ST>(accO[i], &sW[0][0], LDS_, &sStT[0][0], LDS_, (t / CF::NTD) * 16,
+                                    (t % CF::NTD) * 16, c.lane);
+            }
+            __syncthreads();
+            // out += Pm V
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CD; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < MTC * CF::NTD) {
+                    const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                    mma_tile<E, C>(accO[i], &sPm[0][0], LDC, &sVt[0][0], LDC, m0, n0, c.lane);
+                    if constexpr (CF::QKV)
+                        store_out_tile(P.out, c.b, hq, c.st, t0, nv, P.D, m0, n0, c.lane, accO[i]);
+                    else
+                        store_out_tile(P.out, c.z, 0, c.st, t0, nv, P.D, m0, n0, c.lane, accO[i]);
+                }
+            }
+        }
+        // St += pK^T V
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < CF::NTS * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                mma_tile<E, C>(accS[i], &sPKt[0][0], LDC, &sVt[0][0], LDC, m0, n0, c.lane);
+                st_cm(&sStT[0][0], LDS_, m0, n0, c.lane, accS[i]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ============================================================================ backward totals
+template <class E, int MODE, int ST, int DP, int C, int NW>
+__global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
+{
+    using CF = Cfg<E, MODE, ST, DP, C, NW>;
+    using T = typename E::T;
+    constexpr int PD = CF::PD, NTH = CF::NTH, MTC = CF::MTC;
+    constexpr int LDX = DP + PD, LDC = C + PD, LDU = CF::LKPM + 1, LDF = ST + 4, LDG = CF::LKPM + PD;
+    constexpr int XR = CF::QKV ? C : 1;
+    constexpr int NCG = CF::TPW_CS / MTC;  // bucket-column groups per wave
+    __shared__ __align__(16) T sX[XR][LDX];
+    __shared__ __align__(16) T sV[C][LDX];
+    __shared__ __align__(16) T sVt[DP][LDC];
+    __shared__ __align__(16) T sGO[C][LDX];
+    __shared__ __align__(16) T sGOt[DP][LDC];
+    __shared__ __align__(16) float sU[XR][LDU];
+    __shared__ __align__(16) T sGU[XR][LDG];
+    __shared__ __align__(16) T sPKt[ST][LDC];
+    __shared__ __align__(16) float sF[C][LDF];
+    __shared__ __align__(16) T sWt[ST][LDC];
+    __shared__ __align__(16) T sStS[ST][LDX];
+    __shared__ __align__(16) T sMg[C][LDC];
+    __shared__ float sA0[ST];
+
+    const Ctx c = make_ctx(P, ST);
+    PlaneFrags<E, CF> pf;
+    if constexpr (CF::QKV) {
+        pf.load(P, c);
+        zero_lds(&sGU[0][0], XR * LDG, c.tid, NTH);
+    }
+    zero_lds(&sPKt[0][0], ST * LDC, c.tid, NTH);
+    zero_lds(&sF[0][0], C * LDF, c.tid, NTH);
+
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    f32x4 accS[CF::TPW_SD], accDS[CF::TPW_SD];
+    {
+        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            accDS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (t < CF::NTS * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                const int r = acc_row(m0, c.lane), col = acc_col(n0, c.lane);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accS[i][e] = wB[(int64_t)(r + e) * P.DPw + col];
+                st_rm(&sStS[0][0], LDX, m0, n0, c.lane, accS[i]);
+            }
+        }
+        const float *wA = P.wsA + slot * P.S_pad + c.s0;
+        for (int s = c.tid; s < ST; s += NTH)
+            sA0[s] = wA[s];
+    }
+    float dGA[NCG > 0 ? NCG : 1];
+#pragma unroll
+    for (int j = 0; j < NCG; ++j)
+        dGA[j] = 0.0f;
+    __syncthreads();
+
+    f32x4 accA[CF::TPW_CS], accW[CF::TPW_CS], accG[CF::TPW_CS];
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        if constexpr (CF::QKV) {
+            load_rows_bf16<C, DP, NTH, LDX, LDC, true, false>(&sX[0][0], nullptr, P.k, c.b, c.hk, t0, nv, c.tid);
+            load_rows_bf16<C, DP, NTH, LDX, LDC, true, true>(&sV[0][0], &sVt[0][0], P.v, c.b, c.hk, t0, nv, c.tid);
+            __syncthreads();
+            project<E, CF, LDX, LDU>(&sX[0][0], &sU[0][0], pf, c, P.inv_scale);
+            __syncthreads();
+            const int R = P.R;
+            expand<CF, LDU>(&sU[0][0], c, P.K, [&](int t, int lt, const float *, const float *pr) {
+                const bool ok = t < nv;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (r < R)
+                        sPKt[lt * R + r][t] = (T)(ok ? pr[r] : 0.0f);
+            });
+        } else {
+            load_probs<T, C, ST, NTH, LDC, LDC, false, true>(nullptr, &sPKt[0][0], P.pK + (int64_t)c.z * P.T * P.S,
+                                                           P.S, c.s0, c.S_here, t0, nv, c.tid);
+            load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sV[0][0]),
+                                                          reinterpret_cast<float *>(&sVt[0][0]),
+                                                          P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+        }
+        __syncthreads();
+
+        float carry[CF::TPW_CS];
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            carry[i] = 0.0f;
+            accA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (tn < CF::NTS) {
+                const float a0 = sA0[tn * 16 + (c.lane & 15)];
+                accA[i] = f32x4{a0, a0, a0, a0};
+                mma_tile_gen<E, C>(accA[i], PredTrilIncl(), 1.0f, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
+                carry[i] = accA[i][3];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accA[i][e] = frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            if (tn < CF::NTS && tm == MTC - 1 && (c.lane >> 4) == 3)
+                sA0[tn * 16 + (c.lane & 15)] = carry[i];
+        }
+
+        const int G = CF::QKV ? P.G : 1;
+        for (int g = 0; g < G; ++g) {
+            const int hq = c.hk * P.G + g;
+            if constexpr (CF::QKV) {
+                load_rows_bf16<C, DP, NTH, LDX, LDC, true, false>(&sX[0][0], nullptr, P.q, c.b, hq, t0, nv, c.tid);
+                load_rows_bf16<C, DP, NTH, LDX, LDC, true, true>(&sGO[0][0], &sGOt[0][0], P.go, c.b, hq, t0, nv, c.tid);
+                __syncthreads();
+                project<E, CF, LDX, LDU>(&sX[0][0], &sU[0][0], pf, c, P.inv_scale);
+                __syncthreads();
+                const int R = P.R;
+                expand<CF, LDU>(&sU[0][0], c, P.K, [&](int t, int lt, const float *, const float *pr) {
+                    const bool ok = t < nv;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (r < R)
+                            sF[t][lt * R + r] = ok ? pr[r] : 0.0f;
+                });
+            } else {
+                load_probs<float, C, ST, NTH, LDF, LDF, true, false>(&sF[0][0], nullptr, P.pQ + (int64_t)c.z * P.T * P.S,
+                                                                   P.S, c.s0, c.S_here, t0, nv, c.tid);
+                load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sGO[0][0]),
+                                                              reinterpret_cast<float *>(&sGOt[0][0]),
+                                                              P.gO + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+            }
+            __syncthreads();
+            // W = pQ/(A+eps) -> sWt ; gW = go St^T ; Mg = tril(go V^T)
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CS; ++i) {
+                const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+                accW[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (tn < CF::NTS) {
+                    const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accW[i][e] = sF[r + e][col] * accA[i][e];
+                    st_cm(&sWt[0][0], LDC, tm * 16, tn * 16, c.lane, accW[i]);
+                    mma_tile<E, DP>(accG[i], &sGO[0][0], LDX, &sStS[0][0], LDX, tm * 16, tn * 16, c.lane);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CC; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int tm = t / MTC, tn = t % MTC;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_tile<E, DP>(acc, &sGO[0][0], LDX, &sV[0][0], LDX, tm * 16, tn * 16, c.lane);
+                    const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col > r + e)
+                            acc[e] = 0.0f;
+                    st_rm(&sMg[0][0], LDC, tm * 16, tn * 16, c.lane, acc);
+                }
+            }
+            __syncthreads();
+            // gW += Mg pK ; gpQ = gW/(A+eps) ; gA = -gpQ W ; dS += W^T go
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CS; ++i) {
+                const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+                if (tn < CF::NTS) {
+                    mma_tile<E, C>(accG[i], &sMg[0][0], LDC, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
+                    f32x4 gpq;
+                    float colsum = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        gpq[e] = accG[i][e] * accA[i][e];
+                        colsum -= gpq[e] * accW[i][e];
+                    }
+                    accG[i] = gpq;
+                    dGA[i / MTC] += colsum;  // reduced across lanes at the end
+                    if constexpr (!CF::QKV)
+                        store_probs_tile(P.gpQ + (int64_t)c.z * P.T * P.S, P.S, c.s0, c.S_here, t0, nv,
+                                         tm * 16, tn * 16, c.lane, gpq);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CF::TPW_SD; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < CF::NTS * CF::NTD)
+                    mma_tile<E, C>(accDS[i], &sWt[0][0], LDC, &sGOt[0][0], LDC, (t / CF::NTD) * 16,
+                                   (t % CF::NTD) * 16, c.lane);
+            }
+            if constexpr (CF::QKV) {
+                // dq through the soft-hash backward
+#pragma unroll
+                for (int i = 0; i < CF::TPW_CS; ++i) {
+                    const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+                    if (tn < CF::NTS)
+                        st_rm(&sF[0][0], LDF, tm * 16, tn * 16, c.lane, accG[i]);
+                }
+                __syncthreads();
+                const int R = P.R, K = P.K;
+                const float scale = P.scale, inv_scale = P.inv_scale;
+                expand<CF, LDU>(&sU[0][0], c, K, [&](int t, int lt, const float *u, const float *pr) {
+                    float gp[16], gproj[4];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        gp[r] = (r < R) ? sF[t][lt * R + r] : 0.0f;
+                    softhash_bwd(u, pr, gp, K, scale, inv_scale, gproj);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (k < K)
+                            sGU[t][lt * K + k] = (T)gproj[k];
+                });
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < CF::TPW_CD; ++i) {
+                    const int t = c.wave + i * NW;
+                    if (t < MTC * CF::NTD) {
+                        const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                        const T *pa = &sGU[0][0] + (m0 + (c.lane & 15)) * LDG + (c.lane >> 4) * E::KPL;
+#pragma unroll
+                        for (int kb = 0; kb < CF::KB_L; ++kb)
+                            if (kb * E::KSTEP < c.LKP)
+                                E::mma(acc, E::ld(pa + kb * E::KSTEP), pf.back[i][kb]);
+                        store_out_tile(P.dq, c.b, hq, c.st, t0, nv, P.D, m0, n0, c.lane, acc);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        // St += pK^T V
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < CF::NTS * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                mma_tile<E, C>(accS[i], &sPKt[0][0], LDC, &sVt[0][0], LDC, m0, n0, c.lane);
+                st_rm(&sStS[0][0], LDX, m0, n0, c.lane, accS[i]);
+            }
+        }
+        __syncthreads();
+    }
+
+    // block totals of W^T go and gA
+    float *wB = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+    for (int i = 0; i < CF::TPW_SD; ++i) {
+        const int t = c.wave + i * NW;
+        if (t < CF::NTS * CF::NTD) {
+            const int r = acc_row((t / CF::NTD) * 16, c.lane), col = acc_col((t % CF::NTD) * 16, c.lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                wB[(int64_t)(r + e) * P.DPw + col] = accDS[i][e];
+        }
+    }
+    float *wA = P.ws2A + slot * P.S_pad + c.s0;
+#pragma unroll
+    for (int j = 0; j < NCG; ++j) {
+        float v = dGA[j];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        const int tn = c.wave + j * NW;
+        if (tn < CF::NTS && c.lane < 16)
+            wA[tn * 16 + c.lane] = v;
+    }
+}
+
+// ============================================================================ backward main
+// Walks each block FORWARD so that A_t and the bucket state St are accumulated
+// exactly as in the forward pass (small early A values are never rebuilt by
+// subtraction, where 1/A^2 in gA would amplify the rounding). The reverse states
+// come from the inclusive block suffixes of the backward workspace and shrink by
+// each sub-chunk's own contribution:
+//   dS_end(c)   = dS_start(c) - W_c^T go_c
+//   gAhat_end(c)= gAhat_start(c) - colsum(gA_c)
+// whose rounding is absolute and is not divided by A.
+template <class E, int MODE, int ST, int DP, int C, int NW>
+__global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
+{
+    using CF = Cfg<E, MODE, ST, DP, C, NW>;
+    using T = typename E::T;
+    constexpr int PD = CF::PD, NTH = CF::NTH, MTC = CF::MTC;
+    constexpr int LDX = DP + PD, LDC = C + PD, LDS_ = ST + PD, LDU = CF::LKPM + 1, LDF = ST + 4;
+    constexpr int LDG = CF::LKPM + PD;
+    constexpr int XR = CF::QKV ? C : 1;
+    __shared__ __align__(16) T sX[XR][LDX];
+    __shared__ __align__(16) T sV[C][LDX];
+    __shared__ __align__(16) T sVt[DP][LDC];
+    __shared__ __align__(16) T sGO[C][LDX];
+    __shared__ __align__(16) T sGOt[DP][LDC];
+    __shared__ __align__(16) float sUk[XR][LDU];
+    __shared__ __align__(16) float sUq[XR][LDU];  // also holds the k soft-hash grads at the end
+    __shared__ __align__(16) T sPK[C][LDS_];
+    __shared__ __align__(16) T sPKt[ST][LDC];
+    __shared__ __align__(16) float sF[C][LDF];
+    __shared__ __align__(16) T sW[C][LDS_];
+    __shared__ __align__(16) T sWt[ST][LDC];
+    __shared__ __align__(16) T sStS[ST][LDX];
+    __shared__ __align__(16) T sdS[ST][LDX];
+    __shared__ __align__(16) T sdSt[DP][LDS_];
+    __shared__ __align__(16) T sMg[C][LDC];
+    __shared__ __align__(16) T sMv[C][LDC];
+    __shared__ __align__(16) T sMp[C][LDC];
+    __shared__ float sA0[ST];
+    __shared__ float sGAe[ST];
+    static_assert(!CF::QKV || sizeof(T) * XR * LDG <= sizeof(float) * XR * LDU, "sGU alias");
+    T *sGU = reinterpret_cast<T *>(&sUq[0][0]);
+
+    const Ctx c = make_ctx(P, ST);
+    PlaneFrags<E, CF> pf;
+    if constexpr (CF::QKV)
+        pf.load(P, c);
+    zero_lds(&sPK[0][0], C * LDS_, c.tid, NTH);
+    zero_lds(&sPKt[0][0], ST * LDC, c.tid, NTH);
+    zero_lds(&sF[0][0], C * LDF, c.tid, NTH);
+
+    // forward state at the block start; reverse suffix from the block start (inclusive)
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    f32x4 accS[CF::TPW_SD], accDS[CF::TPW_SD];
+    {
+        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+        const float *wB2 = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            accDS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (t < CF::NTS * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                const int r = acc_row(m0, c.lane), col = acc_col(n0, c.lane);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    accS[i][e] = wB[(int64_t)(r + e) * P.DPw + col];
+                    accDS[i][e] = wB2[(int64_t)(r + e) * P.DPw + col];
+                }
+            }
+        }
+        const float *wA = P.wsA + slot * P.S_pad + c.s0;
+        const float *wA2 = P.ws2A + slot * P.S_pad + c.s0;
+        for (int s = c.tid; s < ST; s += NTH) {
+            sA0[s] = wA[s];
+            sGAe[s] = wA2[s];
+        }
+    }
+    __syncthreads();
+
+    f32x4 accA[CF::TPW_CS], accW[CF::TPW_CS], accG[CF::TPW_CS], accGA[CF::TPW_CS], accPK[CF::TPW_CS];
+    f32x4 accV[CF::TPW_CD];
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        if constexpr (CF::QKV) {
+            load_rows_bf16<C, DP, NTH, LDX, LDC, true, false>(&sX[0][0], nullptr, P.k, c.b, c.hk, t0, nv, c.tid);
+            load_rows_bf16<C, DP, NTH, LDX, LDC, true, true>(&sV[0][0], &sVt[0][0], P.v, c.b, c.hk, t0, nv, c.tid);
+            __syncthreads();
+            project<E, CF, LDX, LDU>(&sX[0][0], &sUk[0][0], pf, c, P.inv_scale);
+            __syncthreads();
+            const int R = P.R;
+            expand<CF, LDU>(&sUk[0][0], c, P.K, [&](int t, int lt, const float *, const float *pr) {
+                const bool ok = t < nv;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (r < R) {
+                        const T x = (T)(ok ? pr[r] : 0.0f);
+                        sPK[t][lt * R + r] = x;
+                        sPKt[lt * R + r][t] = x;
+                    }
+            });
+        } else {
+            load_probs<T, C, ST, NTH, LDS_, LDC, true, true>(&sPK[0][0], &sPKt[0][0], P.pK + (int64_t)c.z * P.T * P.S,
+                                                           P.S, c.s0, c.S_here, t0, nv, c.tid);
+            load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sV[0][0]),
+                                                          reinterpret_cast<float *>(&sVt[0][0]),
+                                                          P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+        }
+        // the state at this sub-chunk's start, for gW = go St^T
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < CF::NTS * CF::NTD)
+                st_rm(&sStS[0][0], LDX, (t / CF::NTD) * 16, (t % CF::NTD) * 16, c.lane, accS[i]);
+        }
+        __syncthreads();
+
+        // A = A0 + Tri pK (forward, as in the forward pass) ; carry its last row
+        float carry[CF::TPW_CS];
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            carry[i] = 0.0f;
+            accA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            accPK[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (tn < CF::NTS) {
+                const float a0 = sA0[tn * 16 + (c.lane & 15)];
+                accA[i] = f32x4{a0, a0, a0, a0};
+                mma_tile_gen<E, C>(accA[i], PredTrilIncl(), 1.0f, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
+                carry[i] = accA[i][3];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accA[i][e] = frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CD; ++i)
+            accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            if (tn < CF::NTS && tm == MTC - 1 && (c.lane >> 4) == 3)
+                sA0[tn * 16 + (c.lane & 15)] = carry[i];
+        }
+
+        const int G = CF::QKV ? P.G : 1;
+        for (int g = 0; g < G; ++g) {
+            const int hq = c.hk * P.G + g;
+            if constexpr (CF::QKV) {
+                load_rows_bf16<C, DP, NTH, LDX, LDC, true, false>(&sX[0][0], nullptr, P.q, c.b, hq, t0, nv, c.tid);
+                load_rows_bf16<C, DP, NTH, LDX, LDC, true, true>(&sGO[0][0], &sGOt[0][0], P.go, c.b, hq, t0, nv, c.tid);
+                __syncthreads();
+                project<E, CF, LDX, LDU>(&sX[0][0], &sUq[0][0], pf, c, P.inv_scale);
+                __syncthreads();
+                const int R = P.R;
+                expand<CF, LDU>(&sUq[0][0], c, P.K, [&](int t, int lt, const float *, const float *pr) {
+                    const bool ok = t < nv;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (r < R)
+                            sF[t][lt * R + r] = ok ? pr[r] : 0.0f;
+                });
+            } else {
+                load_probs<float, C, ST, NTH, LDF, LDF, true, false>(&sF[0][0], nullptr, P.pQ + (int64_t)c.z * P.T * P.S,
+                                                                   P.S, c.s0, c.S_here, t0, nv, c.tid);
+                load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sGO[0][0]),
+                                                              reinterpret_cast<float *>(&sGOt[0][0]),
+                                                              P.gO + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+            }
+            __syncthreads();
+            // W -> sW, sWt ; gW = go St^T ; Mg = tril(go V^T) -> sMg, sMv
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CS; ++i) {
+                const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+                accW[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (tn < CF::NTS) {
+                    const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accW[i][e] = sF[r + e][col] * accA[i][e];
+                    st_rm(&sW[0][0], LDS_, tm * 16, tn * 16, c.lane, accW[i]);
+                    st_cm(&sWt[0][0], LDC, tm * 16, tn * 16, c.lane, accW[i]);
+                    mma_tile<E, DP>(accG[i], &sGO[0][0], LDX, &sStS[0][0], LDX, tm * 16, tn * 16, c.lane);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CC; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int tm = t / MTC, tn = t % MTC;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_tile<E, DP>(acc, &sGO[0][0], LDX, &sV[0][0], LDX, tm * 16, tn * 16, c.lane);
+                    const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col > r + e)
+                            acc[e] = 0.0f;
+                    st_rm(&sMg[0][0], LDC, tm * 16, tn * 16, c.lane, acc);
+                    st_cm(&sMv[0][0], LDC, tm * 16, tn * 16, c.lane, acc);
+                }
+            }
+            __syncthreads();
+            // Mp = triu(pK W^T) -> sMp
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CC; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int tm = t / MTC, tn = t % MTC;  // rows tau, cols t
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_tile<E, ST>(acc, &sPK[0][0], LDS_, &sW[0][0], LDS_, tm * 16, tn * 16, c.lane);
+                    const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col < r + e)
+                            acc[e] = 0.0f;
+                    st_rm(&sMp[0][0], LDC, tm * 16, tn * 16, c.lane, acc);
+                }
+            }
+            // gW += Mg pK ; gA += -gW W/(A+eps) ; gpK += triu(V go^T) W ; dS -= W^T go
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CS; ++i) {
+                const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+                if (tn < CF::NTS) {
+                    mma_tile<E, C>(accG[i], &sMg[0][0], LDC, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accGA[i][e] -= accG[i][e] * accA[i][e] * accW[i][e];
+                    mma_tile<E, C>(accPK[i], &sMv[0][0], LDC, &sWt[0][0], LDC, tm * 16, tn * 16, c.lane);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CF::TPW_SD; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < CF::NTS * CF::NTD)
+                    mma_tile<E, C, true>(accDS[i], &sWt[0][0], LDC, &sGOt[0][0], LDC, (t / CF::NTD) * 16,
+                                         (t % CF::NTD) * 16, c.lane);
+            }
+            __syncthreads();
+            // gv += Mp go
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CD; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < MTC * CF::NTD)
+                    mma_tile<E, C>(accV[i], &sMp[0][0], LDC, &sGOt[0][0], LDC, (t / CF::NTD) * 16,
+                                   (t % CF::NTD) * 16, c.lane);
+            }
+            if (g + 1 < G)
+                __syncthreads();
+        }
+
+        // dS now holds the suffix after this sub-chunk: copies for V dS^T and pK dS;
+        // gA of this sub-chunk to sF for its suffix sums
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < CF::NTS * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                st_rm(&sdS[0][0], LDX, m0, n0, c.lane, accDS[i]);
+                st_cm(&sdSt[0][0], LDS_, m0, n0, c.lane, accDS[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            if (tn < CF::NTS)
+                st_rm(&sF[0][0], LDF, tm * 16, tn * 16, c.lane, accGA[i]);
+        }
+        __syncthreads();
+        // gAhat_t = gAhat_end + sum_{tau>=t} gA_tau with gAhat_end = gAhat_start - sum_c gA
+        for (int s = c.tid; s < ST; s += NTH) {
+            float tot = 0.0f;
+            for (int t = 0; t < C; ++t)
+                tot += sF[t][s];
+            float run = sGAe[s] - tot;
+            const float end = run;
+            for (int t = C - 1; t >= 0; --t) {
+                run += sF[t][s];
+                sF[t][s] = run;
+            }
+            sGAe[s] = end;
+        }
+        // gpK += V dS^T ; gv += pK dS  (dS = suffix after this sub-chunk)
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            if (tn < CF::NTS)
+                mma_tile<E, DP>(accPK[i], &sV[0][0], LDX, &sdS[0][0], LDX, tm * 16, tn * 16, c.lane);
+        }
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < MTC * CF::NTD)
+                mma_tile<E, ST>(accV[i], &sPK[0][0], LDS_, &sdSt[0][0], LDS_, (t / CF::NTD) * 16,
+                                (t % CF::NTD) * 16, c.lane);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i) {
+            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+            if (tn < CF::NTS) {
+                const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accPK[i][e] += sF[r + e][col];
+                if constexpr (CF::QKV)
+                    st_rm(&sF[0][0], LDF, tm * 16, tn * 16, c.lane, accPK[i]);
+                else
+                    store_probs_tile(P.gpK + (int64_t)c.z * P.T * P.S, P.S, c.s0, c.S_here, t0, nv,
+                                     tm * 16, tn * 16, c.lane, accPK[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < MTC * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                if constexpr (CF::QKV)
+                    store_out_tile(P.dv, c.b, c.hk, c.st, t0, nv, P.D, m0, n0, c.lane, accV[i]);
+                else
+                    store_out_tile(P.dv, c.z, 0, c.st, t0, nv, P.D, m0, n0, c.lane, accV[i]);
+            }
+        }
+        if constexpr (CF::QKV) {
+            // dk through the soft-hash backward (sGU aliases sUq, whose q values are dead)
+            for (int i = c.tid; i < C * LDG; i += NTH)
+                sGU[i] = (T)0.0f;
+            __syncthreads();
+            const int R = P.R, K = P.K;
+            const float scale = P.scale, inv_scale = P.inv_scale;
+            expand<CF, LDU>(&sUk[0][0], c, K, [&](int t, int lt, const float *u, const float *pr) {
+                float gp[16], gproj[4];
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    gp[r] = (r < R) ? sF[t][lt * R + r] : 0.0f;
+                softhash_bwd(u, pr, gp, K, scale, inv_scale, gproj);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k < K)
+                        sGU[t * LDG + lt * K + k] = (T)gproj[k];
+            });
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < CF::TPW_CD; ++i) {
+                const int t = c.wave + i * NW;
+                if (t < MTC * CF::NTD) {
+                    const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    const T *pa = sGU + (m0 + (c.lane & 15)) * LDG + (c.lane >> 4) * E::KPL;
+#pragma unroll
+                    for (int kb = 0; kb < CF::KB_L; ++kb)
+                        if (kb * E::KSTEP < c.LKP)
+                            E::mma(acc, E::ld(pa + kb * E::KSTEP), pf.back[i][kb]);
+                    store_out_tile(P.dk, c.b, c.hk, c.st, t0, nv, P.D, m0, n0, c.lane, acc);
+                }
+            }
+        }
+        // St += pK^T V
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i) {
+            const int t = c.wave + i * NW;
+            if (t < CF::NTS * CF::NTD)
+                mma_tile<E, C>(accS[i], &sPKt[0][0], LDC, &sVt[0][0], LDC, (t / CF::NTD) * 16,
+                               (t % CF::NTD) * 16, c.lane);
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace race

@@ -1,0 +1,127 @@
+"""Causal RACE attention on MI355X with the reference's interface
+(scaling/race_causal_cuda.py).
+
+  race_fused_fwd(probsK, probsQ, V2, eps, chunk) -> out        kernels/gpu/forward_kernel.cu:110
+  race_backward(probsK, probsQ, V2, grad_out, eps, chunk)      kernels/gpu/backward_kernels.cu:174
+      -> [gradProbsK, gradProbsQ, gradV]
+  fwd_chunk(T)                                                 race_causal_cuda.py:33-44
+  RaceCausalFn.apply(probsK, probsQ, V2, eps) -> out [N,T,D]   race_causal_cuda.py:47-69
+  race_cuda_fused(probsK, probsQ, V2, eps)                     race_causal_cuda.py:72-73
+  RaceCausalCuda(d_k, Kbits, L, M, device, share_planes, eps, seed)   race_causal_cuda.py:76-102
+
+The op-level functions run the fp32 chunked-scan HIP kernels (race_op_fwd /
+race_op_bwd). RaceCausalCuda runs the fused bf16 q/k/v kernels when its inputs
+are bf16 with a supported head dim (the soft-hash happens inside the scan and
+the [N,T,S] probabilities never reach HBM); otherwise it composes the HIP
+soft-hash with RaceCausalFn exactly as the reference does. Its output is fp32
+[B,H,T,D] in both cases, as the reference's.
+"""
+import math
+
+import torch
+import torch.nn as nn
+from torch.autograd import Function
+
+from . import _lib
+from .attention import RaceAttentionFn, fused_supported
+from .race_common import build_planes_protos, soft_hash_probs
+
+
+def fwd_chunk(T):
+    """The reference's chunk heuristic (race_causal_cuda.py:33-44), kept for callers
+    that pass it on; the HIP kernels choose their own block size when given 0 and
+    their results do not depend on it beyond fp32 rounding."""
+    if T <= 4096:
+        return int(T)
+    e = int(math.ceil(math.log2(max(1.0, T / 48.0))))
+    e = max(11, min(16, e))
+    return min(1 << e, int(T))
+
+
+def _op_inputs(probsK, probsQ, V2):
+    _lib.require_device(probsK, probsQ, V2)
+    if probsK.dim() != 3 or probsQ.shape != probsK.shape or V2.dim() != 3 or V2.shape[:2] != probsK.shape[:2]:
+        raise ValueError("shapes must be probsK/probsQ [N,T,S] and V2 [N,T,D], got "
+                         f"{tuple(probsK.shape)}, {tuple(probsQ.shape)}, {tuple(V2.shape)}")
+    return probsK.contiguous().float(), probsQ.contiguous().float(), V2.contiguous().float()
+
+
+def race_fused_fwd(probsK, probsQ, V2, eps, chunk=0):
+    """out[N,T,D] fp32 = causal RACE(probsK, probsQ, V2) (forward_kernel.cu:110-137).
+    `chunk` is the tokens per workgroup block (<= 0: automatic)."""
+    pK, pQ, V = _op_inputs(probsK, probsQ, V2)
+    N, T, S = pK.shape
+    D = V.shape[2]
+    block = max(int(chunk), 0)
+    L = _lib.lib()
+    ws = _lib.workspace(L.race_op_workspace_bytes(N, T, S, D, block, 0), pK.device)
+    out = torch.empty(N, T, D, dtype=torch.float32, device=pK.device)
+    _lib.check(L.race_op_fwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(out), N, T, S, D, float(eps),
+                             block, _lib.ptr(ws), ws.numel(), _lib.stream_of(pK)), "race_op_fwd")
+    return out
+
+
+def race_backward(probsK, probsQ, V2, grad_out, eps, chunk=0):
+    """[gradProbsK, gradProbsQ, gradV] (backward_kernels.cu:174-215), exact."""
+    pK, pQ, V = _op_inputs(probsK, probsQ, V2)
+    _lib.require_device(grad_out)
+    gO = grad_out.contiguous().float()
+    N, T, S = pK.shape
+    D = V.shape[2]
+    block = max(int(chunk), 0)
+    L = _lib.lib()
+    ws = _lib.workspace(L.race_op_workspace_bytes(N, T, S, D, block, 1), pK.device)
+    gpk = torch.empty_like(pK)
+    gpq = torch.empty_like(pQ)
+    gv = torch.empty_like(V)
+    _lib.check(L.race_op_bwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(gO), _lib.ptr(gpk), _lib.ptr(gpq),
+                             _lib.ptr(gv), N, T, S, D, float(eps), block, _lib.ptr(ws), ws.numel(),
+                             _lib.stream_of(pK)), "race_op_bwd")
+    return [gpk, gpq, gv]
+
+
+class RaceCausalFn(Function):
+    """out = causal RACE(probsK, probsQ, V2); exact grads w.r.t. probsK/probsQ/V2."""
+
+    @staticmethod
+    def forward(ctx, probsK, probsQ, V2, eps):
+        pK, pQ, V = _op_inputs(probsK, probsQ, V2)
+        out = race_fused_fwd(pK, pQ, V, eps, 0)
+        ctx.save_for_backward(pK, pQ, V)
+        ctx.eps = float(eps)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        pK, pQ, V = ctx.saved_tensors
+        gpk, gpq, gv = race_backward(pK, pQ, V, grad_out, ctx.eps, 0)
+        return gpk, gpq, gv, None
+
+
+def race_cuda_fused(probsK, probsQ, V2, eps=1e-6):
+    return RaceCausalFn.apply(probsK, probsQ, V2, eps)
+
+
+class RaceCausalCuda(nn.Module):
+    """Causal RACE over Q,K,V [B,H,T,D] -> [B,H,T,D] fp32 (race_causal_cuda.py:76-102)."""
+
+    def __init__(self, d_k, Kbits, L, M, device="cuda", share_planes=True, eps=1e-6, seed=0):
+        super().__init__()
+        self.d_k, self.Kbits, self.L, self.M = d_k, Kbits, L, M
+        self.share_planes = share_planes
+        self.eps = eps
+        planes_T, protos_T = build_planes_protos(d_k, Kbits, L, M, device=device,
+                                                 share_planes=share_planes, seed=seed)
+        self.register_buffer("planes_T", planes_T)
+        self.register_buffer("protos_T", protos_T)
+
+    def forward(self, Q, K, V):
+        B, H, T, D = Q.shape
+        if self.share_planes and fused_supported(Q, K, V, self.Kbits):
+            # the M ensemble copies share the planes, so their mean is one copy
+            return RaceAttentionFn.apply(Q, K, V, self.planes_T, self.L, self.Kbits, math.sqrt(D),
+                                         self.eps, torch.float32, 0)
+        probsK, probsQ, V2, N = soft_hash_probs(Q, K, V, self.planes_T, self.protos_T,
+                                                self.L, self.Kbits, self.M, self.share_planes)
+        out_NTD = RaceCausalFn.apply(probsK, probsQ, V2, self.eps)
+        return out_NTD.view(self.M, B, H, T, D).mean(dim=0)

@@ -1,0 +1,84 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point that
+include/race_attention.h declares, and validates arguments on the host
+(no compute call is made)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from race_attention_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "race_attention.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(race_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for must in ("race_op_fwd", "race_op_bwd", "race_qkv_fwd", "race_qkv_bwd", "race_decode_step",
+                 "race_soft_hash_fwd", "race_soft_hash_bwd", "race_qkv_final_state"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load_library()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in race_attention.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_abi_version_and_sizes():
+    lib = _lib.load_library()
+    assert lib.race_abi_version() == 1
+    sh = _lib.QKVShape(1, 4, 4, 1 << 20, 64, 8, 4, 8.0, 1e-6, 0)
+    state = lib.race_qkv_state_bytes(sh)
+    assert 40e6 < state < 200e6  # per-block states, not [T,S] probabilities
+    assert lib.race_qkv_scratch_bytes(sh, 0) == 0  # S = 128 fits one bucket tile
+    assert lib.race_qkv_scratch_bytes(sh, 1) >= state
+    assert lib.race_op_workspace_bytes(16, 2048, 128, 64, 0, 1) > 0
+
+
+@pytest.mark.parametrize("shape,msg", [
+    ((1, 4, 3, 128, 64, 8, 4), "multiple"),      # Hq not a multiple of Hkv
+    ((1, 4, 4, 128, 96, 8, 4), "head dim"),      # D not compiled in the fused path
+    ((1, 4, 4, 128, 64, 8, 5), "K = 5"),         # K > 4
+])
+def test_qkv_validation_errors(shape, msg):
+    lib = _lib.load_library()
+    sh = _lib.QKVShape(*shape, 8.0, 1e-6, 0)
+    t = _lib.Tensor4(16, 0, 0, 0)
+    rc = lib.race_qkv_fwd(sh, t, t, t, ctypes.c_void_p(16), t, 1, ctypes.c_void_p(16), 1 << 30,
+                          None, 0, None)
+    assert rc != 0
+    assert msg in lib.race_last_error().decode()
+
+
+def test_workspace_too_small_is_reported():
+    lib = _lib.load_library()
+    rc = lib.race_op_fwd(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                         2, 100, 24, 64, 1e-6, 0, ctypes.c_void_p(16), 8, None)
+    assert rc == 3 and "workspace" in lib.race_last_error().decode()
+
+
+def test_misaligned_bf16_rows_rejected():
+    lib = _lib.load_library()
+    sh = _lib.QKVShape(1, 2, 2, 64, 64, 8, 4, 8.0, 1e-6, 0)
+    bad = _lib.Tensor4(16 + 2, 64 * 64, 64 * 64, 64)
+    good = _lib.Tensor4(16, 2 * 64 * 64, 64 * 64, 64)
+    rc = lib.race_qkv_fwd(sh, bad, good, good, ctypes.c_void_p(16), good, 1, ctypes.c_void_p(16), 1 << 30,
+                          None, 0, None)
+    assert rc == 1 and "aligned" in lib.race_last_error().decode()
+
+
+def test_cpu_tensors_rejected_without_fallback():
+    import torch
+
+    from race_attention_amd import RaceCausalFn
+    x = torch.rand(1, 8, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        RaceCausalFn.apply(x, x, torch.rand(1, 8, 16), 1e-6)

@@ -1,0 +1,68 @@
+"""Op-level causal RACE on the GPU (RaceCausalFn / race_fused_fwd / race_backward)
+against the fp64 oracle. Sweeps and tolerances follow the reference's
+scaling/test_kernels.py:132-158 (fwd 2e-5, grads 3e-3, 5e-3 in the T sweep),
+extended to S = 128 and 256 (K = 4)."""
+import pytest
+import torch
+
+from race_ref import check, make_probs, oracle_op
+
+pytestmark = pytest.mark.gpu
+
+PARAM_SETS = [(2, 2), (3, 3), (4, 4), (8, 4)]  # (L, K) -> S = 8, 24, 64, 128
+EPS = 1e-6
+
+
+def run_case(dev, N, T, L, Kb, D, seed, dist="softmax", fwd_tol=2e-5, grad_tol=3e-3, blocks=(0, 64, 1024)):
+    from race_attention_amd import RaceCausalFn, race_fused_fwd
+    print(f"case N={N} T={T} L={L} K={Kb} D={D} dist={dist}", flush=True)
+    R = 1 << Kb
+    pk, pq, v, go = make_probs(N, T, L, R, D, seed, dist)
+    out_t, gpk_t, gpq_t, gv_t, _, _ = oracle_op(pk, pq, v, go, EPS)
+    pkc, pqc, vc = (x.float().to(dev) for x in (pk, pq, v))
+    for blk in blocks:
+        out = race_fused_fwd(pkc, pqc, vc, EPS, blk)
+        check(f"fwd block={blk}", out, out_t, fwd_tol)
+    a = race_fused_fwd(pkc, pqc, vc, EPS, 0)
+    b = race_fused_fwd(pkc, pqc, vc, EPS, 0)
+    assert torch.equal(a, b), "forward is not bitwise deterministic"
+    pkx, pqx, vx = (x.clone().requires_grad_(True) for x in (pkc, pqc, vc))
+    out = RaceCausalFn.apply(pkx, pqx, vx, EPS)
+    (out * go.float().to(dev)).sum().backward()
+    check("gradProbsK", pkx.grad, gpk_t, grad_tol)
+    check("gradProbsQ", pqx.grad, gpq_t, grad_tol)
+    check("gradV", vx.grad, gv_t, grad_tol)
+
+
+@pytest.mark.parametrize("L,Kb", PARAM_SETS)
+@pytest.mark.parametrize("N", [1, 2, 4])
+@pytest.mark.parametrize("D", [16, 64, 128])
+def test_shape_sweep(dev, L, Kb, N, D):
+    run_case(dev, N, 1024, L, Kb, D, seed=N + D)
+
+
+@pytest.mark.parametrize("L,Kb", PARAM_SETS)
+@pytest.mark.parametrize("T", [1, 2, 7, 64, 256, 4096, 16384])
+def test_t_sweep(dev, L, Kb, T):
+    run_case(dev, 2, T, L, Kb, 64, seed=T, grad_tol=5e-3)
+
+
+@pytest.mark.parametrize("L,Kb", [(4, 4)])
+def test_t_65536(dev, L, Kb):
+    run_case(dev, 2, 65536, L, Kb, 64, seed=65536, grad_tol=5e-3, blocks=(0,))
+
+
+@pytest.mark.parametrize("L,Kb", PARAM_SETS)
+@pytest.mark.parametrize("D", [96, 130, 256])
+def test_odd_d(dev, L, Kb, D):
+    run_case(dev, 2, 512, L, Kb, D, seed=D)
+
+
+@pytest.mark.parametrize("L,Kb", PARAM_SETS)
+def test_raw_distribution(dev, L, Kb):
+    run_case(dev, 2, 1024, L, Kb, 64, seed=7, dist="raw")
+
+
+def test_s256_tiled(dev):
+    """S = 256 > the largest bucket tile: exercises the partial-sum reduction."""
+    run_case(dev, 2, 700, 16, 4, 64, seed=11)
