@@ -125,6 +125,8 @@ int qkv_geometry(const race_qkv_shape *sh, Geo &g)
         return fail(RACE_ERR_UNSUPPORTED, "race_qkv: head dim %d, the fused path supports 64 and 128", sh->D);
     if (!(sh->eps > 0.0f) || !(sh->scale > 0.0f))
         return fail(RACE_ERR_INVALID, "race_qkv: eps and scale must be positive");
+    if ((int64_t)sh->Hq * sh->D > (1 << 20))
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv: Hq*D = %lld too large", (long long)sh->Hq * sh->D);
     const int R = 1 << sh->K;
     const int64_t S = (int64_t)sh->L * R;
     if (S > 4096)
@@ -174,6 +176,8 @@ int check_view(const race_tensor &t, const char *name, bool bf16_vec)
         if (((uintptr_t)t.data & 15) || (t.stride_b & 7) || (t.stride_h & 7) || (t.stride_t & 7))
             return fail(RACE_ERR_INVALID,
                         "%s: bf16 rows must be 16-byte aligned (pointer %% 16 == 0, strides %% 8 == 0)", name);
+        if (t.stride_t >= ((int64_t)1 << 26))
+            return fail(RACE_ERR_UNSUPPORTED, "%s: token stride %lld too large", name, (long long)t.stride_t);
     }
     return RACE_OK;
 }
@@ -508,6 +512,9 @@ static int run_scan_qkv(ScanKernel k, const Geo &g, const ScanParams &P, hipStre
 {
     ProfScope ps(RACE_PROF_QKV_FWD_TOTALS + (int)k, s);
     const dim3 grid((unsigned)g.NB, (unsigned)g.n_st, (unsigned)g.Z);
+    // kernels specialised on the hash bits where compiled (K = 2..4), generic ones otherwise
+    if (fused_variant_exists(g.ST, g.DP, P.K))
+        return hip_check(launch_fused(k, g.ST, g.DP, P.K, P, grid, s), "race_qkv fused kernel launch");
     return hip_check(launch_scan_qkv(k, g.ST, g.DP, P, grid, s), "race_qkv kernel launch");
 }
 

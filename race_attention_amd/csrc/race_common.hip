@@ -15,22 +15,42 @@ namespace race {
 // ============================================================================ block scan
 __global__ void race_block_scan(float *ws, int64_t elems, int NB, int rev)
 {
+    // Loads of a batch of blocks are issued together (they do not depend on the
+    // running sum), so each thread waits one memory latency per batch, not per block.
+    constexpr int BATCH = 16;
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= elems)
         return;
     float *base = ws + (int64_t)blockIdx.y * (NB + 1) * elems + e;
     double run = 0.0;
+    float x[BATCH];
     if (!rev) {
-        for (int b = 0; b <= NB; ++b) {
-            const float x = (b < NB) ? base[(int64_t)b * elems] : 0.0f;
-            base[(int64_t)b * elems] = (float)run;
-            run += (double)x;
+        for (int b0 = 0; b0 < NB; b0 += BATCH) {
+#pragma unroll
+            for (int i = 0; i < BATCH; ++i)
+                x[i] = (b0 + i < NB) ? base[(int64_t)(b0 + i) * elems] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < BATCH; ++i) {
+                if (b0 + i < NB) {
+                    base[(int64_t)(b0 + i) * elems] = (float)run;
+                    run += (double)x[i];
+                }
+            }
         }
+        base[(int64_t)NB * elems] = (float)run;
     } else {
         base[(int64_t)NB * elems] = 0.0f;
-        for (int b = NB - 1; b >= 0; --b) {
-            run += (double)base[(int64_t)b * elems];
-            base[(int64_t)b * elems] = (float)run;
+        for (int b1 = NB; b1 > 0; b1 -= BATCH) {
+#pragma unroll
+            for (int i = 0; i < BATCH; ++i)
+                x[i] = (b1 - 1 - i >= 0) ? base[(int64_t)(b1 - 1 - i) * elems] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < BATCH; ++i) {
+                if (b1 - 1 - i >= 0) {
+                    run += (double)x[i];
+                    base[(int64_t)(b1 - 1 - i) * elems] = (float)run;
+                }
+            }
         }
     }
 }

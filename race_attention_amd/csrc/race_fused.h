@@ -1,0 +1,1388 @@
+// Fused bf16 q/k/v kernels of the causal RACE layer, specialised for the hot path
+// (compile-time bucket tile ST, head dim DP, hash bits KB; sub-chunk C = 32 tokens).
+//
+// Same math and block decomposition as race_scan_kernels.h (see race_scan.h), with
+// the data flow arranged so that every MFMA accumulator is produced in the layout
+// its consumer needs:
+//  * the projection is computed transposed, acc[j][t] with j = table*4 + bit, so
+//    one lane holds all K soft bits of one (token, table) pair and expands its 2^K
+//    probabilities in registers (no LDS round trip of the projections);
+//  * A is scanned transposed, A^T[s][t], so W = pQ / (A + eps) is written as
+//    4-bucket vectors of one token row;
+//  * the readout is accumulated transposed, out^T[d][t], and staged through LDS
+//    for 16-byte coalesced global stores;
+//  * the next sub-chunk's k, q, v rows are loaded into registers while the current
+//    one is computed; four barriers per sub-chunk.
+#pragma once
+#include <type_traits>
+
+#include "race_scan.h"
+
+namespace race {
+
+RACE_DEV void zero_lds_bf16(__bf16 *p, int n, int tid, int nth)
+{
+    for (int i = tid; i < n; i += nth)
+        p[i] = (__bf16)0.0f;
+}
+
+template <int KB>
+RACE_DEV void expand_ct(const float *u, float *p)
+{
+    p[0] = 1.0f;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const float e = __expf(-2.0f * u[k]);
+        const float s1 = frcp(1.0f + e);
+        const float s0 = e * s1;
+        const int n = 1 << k;
+#pragma unroll
+        for (int i = n - 1; i >= 0; --i) {
+            const float pi = p[i];
+            p[2 * i + 1] = pi * s1;
+            p[2 * i] = pi * s0;
+        }
+    }
+}
+
+template <int ST, int DP, int KB, int NW>
+struct FCfg {
+    static constexpr int C = 32;
+    static constexpr int NTH = NW * 64;
+    static constexpr int R = 1 << KB;
+    static constexpr int LT = ST / R;          // tables per bucket tile
+    static constexpr int LTP = ((LT + 3) / 4) * 4;  // tables padded to whole projection tiles
+    static constexpr int LKP = 4 * LTP;        // projection rows (4 per table, bits >= KB zero)
+    static constexpr int NJT = LKP / 16;       // projection row tiles
+    static constexpr int MTC = C / 16;         // token tiles
+    static constexpr int NTS = ST / 16;
+    static constexpr int NTD = DP / 16;
+    static constexpr int NPT = NJT * MTC;      // projection tiles per tensor
+    static constexpr int LDX = DP + 8;         // bf16 rows of tokens
+    static constexpr int LDC = C + 8;          // bf16 rows of length C
+    static constexpr int LDS = ST + 8;         // bf16 rows of length ST
+    static constexpr int LDG = ((LKP + 31) / 32) * 32 + 8;  // rows of projection grads (whole MFMA k steps)
+    static constexpr int CHUNKS = C * DP / 8;  // 16-byte chunks of one token tile
+    static constexpr int PF = (CHUNKS + NTH - 1) / NTH;
+    static_assert(KB >= 2 && KB <= 4, "fused kernels: 2 <= K <= 4");
+    static_assert(ST % R == 0 && ST % 32 == 0 && DP % 32 == 0, "tile shapes");
+};
+
+// Lane-constant operand fragments (loaded once per workgroup). Projection tiles
+// are assigned to waves as t = wave + i*NW over NT tiles (k tiles, then q tiles);
+// slot i holds the planes fragment of tile t's projection rows.
+template <class CF, int DP, int NSLOT>
+struct FusedFrags {
+    bf16x8 proj[NSLOT][DP / 32];  // A operand: rows j = table*4 + bit, k = d
+    bf16x8 tri[CF::MTC];          // B operand of the A scan: col t, k = tau, (tau <= t)
+
+    RACE_DEV void load(const ScanParams &P, int l0, int Lt_valid, int lane, int wave)
+    {
+        const int LKtot = P.L * P.K;
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) {
+            const int t = wave + i * (CF::NTH / 64);
+            const int jt = (t % CF::NPT) / CF::MTC;
+            const int j = jt * 16 + (lane & 15);
+            const int table = j >> 2, bit = j & 3;
+#pragma unroll
+            for (int kb = 0; kb < DP / 32; ++kb) {
+                bf16x8 f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int d = kb * 32 + (lane >> 4) * 8 + e;
+                    float x = 0.0f;
+                    if (bit < P.K && table < Lt_valid && d < P.D)
+                        x = P.planes[d * LKtot + (l0 + table) * P.K + bit];
+                    f[e] = (__bf16)x;
+                }
+                proj[i][kb] = f;
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < CF::MTC; ++tt) {
+            const int t = tt * 16 + (lane & 15);
+            bf16x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                f[e] = (__bf16)(((lane >> 4) * 8 + e <= t) ? 1.0f : 0.0f);
+            tri[tt] = f;
+        }
+    }
+
+    RACE_DEV bf16x8 tri_of(int tt) const
+    {
+        bf16x8 r = tri[0];
+#pragma unroll
+        for (int i = 1; i < CF::MTC; ++i)
+            if (tt == i)
+                r = tri[i];
+        return r;
+    }
+};
+
+// acc[j][t] for the projection tile in slot i (rows j from registers), B = x rows t.
+template <class CF, int DP, int NSLOT>
+RACE_DEV f32x4 proj_T(const FusedFrags<CF, DP, NSLOT> &fr, int i, const __bf16 *sX, int tt, int lane)
+{
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDX + (lane >> 4) * 8;
+#pragma unroll
+    for (int kb = 0; kb < DP / 32; ++kb)
+        EngBF16::mma(acc, fr.proj[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+    return acc;
+}
+
+// acc += A[m0.., k] B[n0.., k]^T over K (bf16 LDS operands, k-contiguous rows)
+template <int K, int LDA, int LDB>
+RACE_DEV void mma_ab(f32x4 &acc, const __bf16 *A, int m0, const __bf16 *B, int n0, int lane)
+{
+    const __bf16 *pa = A + (m0 + (lane & 15)) * LDA + (lane >> 4) * 8;
+    const __bf16 *pb = B + (n0 + (lane & 15)) * LDB + (lane >> 4) * 8;
+#pragma unroll
+    for (int k = 0; k < K; k += 32)
+        EngBF16::mma(acc, *reinterpret_cast<const bf16x8 *>(pa + k), *reinterpret_cast<const bf16x8 *>(pb + k));
+}
+
+// store 4 accumulator rows (m0 + 4g + e) of column n as one vector: buf[n][m0+4g .. +3]
+RACE_DEV void st_vec4(__bf16 *p, const f32x4 &v)
+{
+    bf16x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        w[e] = (__bf16)v[e];
+    *reinterpret_cast<bf16x4 *>(p) = w;
+}
+
+// 16-byte chunk loads of one C x DP bf16 token tile (rows t0.., zero beyond nv).
+template <class CF>
+RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int nv, int tid)
+{
+    constexpr int CH = CF::CHUNKS / CF::C;  // chunks per row
+#pragma unroll
+    for (int i = 0; i < CF::PF; ++i) {
+        const int idx = tid + i * CF::NTH;
+        const int row = idx / CH, c = idx % CH;
+        r[i] = u32x4{0u, 0u, 0u, 0u};
+        if (idx < CF::CHUNKS && row < nv)
+            r[i] = *reinterpret_cast<const u32x4 *>(base + row * (int)st + c * 8);
+    }
+}
+
+template <class CF>
+RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int tid)
+{
+    constexpr int CH = CF::CHUNKS / CF::C;
+#pragma unroll
+    for (int i = 0; i < CF::PF; ++i) {
+        const int idx = tid + i * CF::NTH;
+        if (idx < CF::CHUNKS)
+            *reinterpret_cast<u32x4 *>(dst + (idx / CH) * CF::LDX + (idx % CH) * 8) = r[i];
+    }
+}
+
+template <class CF>
+RACE_DEV void tile_store_trans(__bf16 *dstT, const u32x4 (&r)[CF::PF], int tid)
+{
+    constexpr int CH = CF::CHUNKS / CF::C;
+#pragma unroll
+    for (int i = 0; i < CF::PF; ++i) {
+        const int idx = tid + i * CF::NTH;
+        if (idx < CF::CHUNKS) {
+            const int row = idx / CH, c = idx % CH;
+            const bf16x8 x = __builtin_bit_cast(bf16x8, r[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                dstT[(c * 8 + e) * CF::LDC + row] = x[e];
+        }
+    }
+}
+
+RACE_DEV const __bf16 *row_ptr(const View &v, int b, int h, int t)
+{
+    return reinterpret_cast<const __bf16 *>(v.p) + (b * v.sb + h * v.sh + (int64_t)t * v.st);
+}
+
+// ============================================================================ forward totals
+template <int ST, int DP, int KB, int NW>
+__global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParams P)
+{
+    using CF = FCfg<ST, DP, KB, NW>;
+    constexpr int C = CF::C, NTH = CF::NTH, R = CF::R;
+    __shared__ __align__(16) __bf16 sK[C][CF::LDX];
+    __shared__ __align__(16) __bf16 sVt[DP][CF::LDC];
+    __shared__ __align__(16) __bf16 sPKt[ST][CF::LDC];
+
+    const Ctx c = make_ctx(P, ST);
+    const int tid = c.tid, lane = c.lane, wave = c.wave;
+    constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
+    constexpr int TPW_A = (CF::NTS + NW - 1) / NW;
+    constexpr int TPW_P = (CF::NPT + NW - 1) / NW;
+    FusedFrags<CF, DP, TPW_P> fr;
+    fr.load(P, c.l0, c.Lt, lane, wave);
+    f32x4 accS[TPW_S], accA[TPW_A];
+#pragma unroll
+    for (int i = 0; i < TPW_S; ++i)
+        accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < TPW_A; ++i)
+        accA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        ones[e] = (__bf16)1.0f;
+
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    u32x4 pk[CF::PF], pv[CF::PF];
+    tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, min(C, c.t_end - c.t_begin), tid);
+    tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, min(C, c.t_end - c.t_begin), tid);
+    tile_store_rows<CF>(&sK[0][0], pk, tid);
+    tile_store_trans<CF>(&sVt[0][0], pv, tid);
+    __syncthreads();
+
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        if (sc + 1 < nsub) {
+            const int t1 = t0 + C;
+            tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, min(C, c.t_end - t1), tid);
+            tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, t1), P.v.st, min(C, c.t_end - t1), tid);
+        }
+        // soft-hash of k -> pK^T
+#pragma unroll
+        for (int i = 0; i < TPW_P; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NPT) {
+                const int jt = t / CF::MTC, tt = t % CF::MTC;
+                const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, &sK[0][0], tt, lane);
+                float u[4], p[R];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    u[e] = tanh_f(acc[e]) * P.inv_scale;
+                expand_ct<KB>(u, p);
+                const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                const bool ok = tok < nv && table < c.Lt;
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    sPKt[table * R + r][tok] = (__bf16)(ok ? p[r] : 0.0f);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TPW_S; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTS * CF::NTD)
+                mma_ab<C, CF::LDC, CF::LDC>(accS[i], &sPKt[0][0], (t / CF::NTD) * 16, &sVt[0][0], (t % CF::NTD) * 16, lane);
+        }
+#pragma unroll
+        for (int i = 0; i < TPW_A; ++i) {
+            const int tn = wave + i * NW;
+            if (tn < CF::NTS) {
+                const __bf16 *pb = &sPKt[0][0] + (tn * 16 + (lane & 15)) * CF::LDC + (lane >> 4) * 8;
+                EngBF16::mma(accA[i], ones, *reinterpret_cast<const bf16x8 *>(pb));
+            }
+        }
+        __syncthreads();
+        if (sc + 1 < nsub) {
+            tile_store_rows<CF>(&sK[0][0], pk, tid);
+            tile_store_trans<CF>(&sVt[0][0], pv, tid);
+        }
+        __syncthreads();
+    }
+
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+    for (int i = 0; i < TPW_S; ++i) {
+        const int t = wave + i * NW;
+        if (t < CF::NTS * CF::NTD) {
+            const int r = acc_row((t / CF::NTD) * 16, lane), col = acc_col((t % CF::NTD) * 16, lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                wB[(int64_t)(r + e) * P.DPw + col] = accS[i][e];
+        }
+    }
+    float *wA = P.wsA + slot * P.S_pad + c.s0;
+#pragma unroll
+    for (int i = 0; i < TPW_A; ++i) {
+        const int tn = wave + i * NW;
+        if (tn < CF::NTS && lane < 16)
+            wA[tn * 16 + lane] = accA[i][0];
+    }
+}
+
+// ============================================================================ forward readout
+template <int ST, int DP, int KB, int NW, bool OUT_F32>
+__global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanParams P)
+{
+    using CF = FCfg<ST, DP, KB, NW>;
+    constexpr int C = CF::C, NTH = CF::NTH, R = CF::R, MTC = CF::MTC;
+    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS;
+    using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
+    constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
+    __shared__ __align__(16) __bf16 sK[C][LDX];
+    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sVt[2][DP][LDC];
+    __shared__ __align__(16) __bf16 sPK[C][LDS];
+    __shared__ __align__(16) __bf16 sPKt[ST][LDC];
+    __shared__ __align__(16) __bf16 sPQ[C][LDS];
+    __shared__ __align__(16) __bf16 sW[C][LDS];
+    __shared__ __align__(16) __bf16 sStT[DP][LDS];
+    __shared__ __align__(16) __bf16 sPm[C][LDC];
+    __shared__ __align__(16) OT sO[C][LDO];
+    __shared__ __align__(16) float sA0[2][ST];
+
+    const Ctx c = make_ctx(P, ST);
+    const int tid = c.tid, lane = c.lane, wave = c.wave;
+    constexpr int TPW_P0 = (2 * CF::NPT + NW - 1) / NW;
+    FusedFrags<CF, DP, TPW_P0> fr;
+    fr.load(P, c.l0, c.Lt, lane, wave);
+    zero_lds_bf16(&sPK[0][0], C * LDS, tid, NTH);
+    zero_lds_bf16(&sPKt[0][0], ST * LDC, tid, NTH);
+    zero_lds_bf16(&sPQ[0][0], C * LDS, tid, NTH);
+
+    constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;  // state tiles [ST x DP]
+    constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;      // A^T tiles [ST x C]
+    constexpr int TPW_O = (CF::NTD * MTC + NW - 1) / NW;      // out^T tiles [DP x C]
+    constexpr int TPW_M = (MTC * MTC + NW - 1) / NW;          // Pm^T tiles [C x C]
+    constexpr int NPT2 = 2 * CF::NPT;                         // k and q projection tiles
+    constexpr int TPW_P = (NPT2 + NW - 1) / NW;
+
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    f32x4 accS[TPW_S];
+    {
+        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < TPW_S; ++i) {
+            const int t = wave + i * NW;
+            accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (t < CF::NTS * CF::NTD) {
+                const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
+                const int r = acc_row(m0, lane), col = acc_col(n0, lane);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accS[i][e] = wB[(int64_t)(r + e) * P.DPw + col];
+                st_vec4(&sStT[col][r], accS[i]);
+            }
+        }
+        const float *wA = P.wsA + slot * P.S_pad + c.s0;
+        for (int s = tid; s < ST; s += NTH)
+            sA0[0][s] = wA[s];
+    }
+
+    const int G = P.G;
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    u32x4 pk[CF::PF], pq[CF::PF], pv[CF::PF];
+    {
+        const int nv0 = min(C, c.t_end - c.t_begin);
+        tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, nv0, tid);
+        tile_load<CF>(pq, row_ptr(P.q, c.b, c.hk * G, c.t_begin), P.q.st, nv0, tid);
+        tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, nv0, tid);
+        tile_store_rows<CF>(&sK[0][0], pk, tid);
+        tile_store_rows<CF>(&sQ[0][0], pq, tid);
+        tile_store_trans<CF>(&sVt[0][0][0], pv, tid);
+    }
+    __syncthreads();
+
+    f32x4 accA[TPW_A];  // 1/(A+eps), transposed tiles, kept across query heads
+    int prev_t0 = -1, prev_nv = 0, prev_h = 0;
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        const int cur = sc & 1, nxt = cur ^ 1;
+        const bool more = sc + 1 < nsub;
+        if (more) {
+            const int t1 = t0 + C, nv1 = min(C, c.t_end - t1);
+            tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, nv1, tid);
+            tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, t1), P.v.st, nv1, tid);
+            if (G == 1)
+                tile_load<CF>(pq, row_ptr(P.q, c.b, c.hk, t1), P.q.st, nv1, tid);
+        }
+        for (int g = 0; g < G; ++g) {
+            const int hq = c.hk * G + g;
+            if (g > 0) {  // further query heads of the group: load q synchronously
+                u32x4 tq[CF::PF];
+                tile_load<CF>(tq, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
+                tile_store_rows<CF>(&sQ[0][0], tq, tid);
+                __syncthreads();
+            }
+            // ---- P1: soft-hash of k (first head only) and q; previous output rows to HBM
+#pragma unroll
+            for (int i = 0; i < TPW_P; ++i) {
+                const int t = wave + i * NW;
+                const bool isk = t < CF::NPT;
+                if (t < NPT2 && (isk ? g == 0 : true)) {
+                    const int tq_ = isk ? t : t - CF::NPT;
+                    const int jt = tq_ / MTC, tt = tq_ % MTC;
+                    const f32x4 acc = proj_T<CF, DP, TPW_P0>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
+                    float u[4], p[R];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        u[e] = tanh_f(acc[e]) * P.inv_scale;
+                    expand_ct<KB>(u, p);
+                    const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                    const bool ok = tok < nv && table < c.Lt;
+                    bf16x8 v8[R / 8 > 0 ? R / 8 : 1];
+                    bf16x4 v4;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const __bf16 x = (__bf16)(ok ? p[r] : 0.0f);
+                        if (R >= 8)
+                            v8[r / 8][r % 8] = x;
+                        else
+                            v4[r] = x;
+                    }
+                    __bf16 *row = isk ? &sPK[tok][table * R] : &sPQ[tok][table * R];
+                    if (table < CF::LT) {
+                        if (R >= 8) {
+#pragma unroll
+                            for (int h = 0; h < R / 8; ++h)
+                                *reinterpret_cast<bf16x8 *>(row + 8 * h) = v8[h];
+                        } else {
+                            *reinterpret_cast<bf16x4 *>(row) = v4;
+                        }
+                        if (isk) {
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+                                sPKt[table * R + r][tok] = (R >= 8) ? v8[r / 8][r % 8] : v4[r % 4];
+                        }
+                    }
+                }
+            }
+            if (prev_t0 >= 0) {
+                // coalesced store of the previous (sub-chunk, head) output from sO
+                constexpr int OCH = DP * (int)sizeof(OT) / 16;  // 16-byte chunks per row
+                for (int i = tid; i < C * OCH; i += NTH) {
+                    const int row = i / OCH, ch = i % OCH;
+                    if (row < prev_nv) {
+                        OT *dst = reinterpret_cast<OT *>(P.out.p) +
+                                  (int64_t)c.st * P.out.tile + c.b * P.out.sb + prev_h * P.out.sh +
+                                  (int64_t)(prev_t0 + row) * P.out.st + ch * (16 / (int)sizeof(OT));
+                        *reinterpret_cast<u32x4 *>(dst) =
+                            *reinterpret_cast<const u32x4 *>(&sO[row][ch * (16 / (int)sizeof(OT))]);
+                    }
+                }
+            }
+            __syncthreads();
+            // ---- P2: A^T = A0 + pK^T Tri^T (first head); W^T = pQ^T / (A + eps) -> sW
+#pragma unroll
+            for (int i = 0; i < TPW_A; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTS * MTC) {
+                    const int ts = t / MTC, tt = t % MTC;
+                    const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    if (g == 0) {
+                        f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
+                        const __bf16 *pa = &sPKt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
+                        EngBF16::mma(a, *reinterpret_cast<const bf16x8 *>(pa), fr.tri_of(tt));
+                        if (tt == MTC - 1 && (lane & 15) == 15)
+                            *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            accA[i][e] = frcp(a[e] + P.eps);
+                    }
+                    const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
+                    f32x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = (float)q4[e] * accA[i][e];
+                    st_vec4(&sW[tok][s], w);
+                }
+            }
+            __syncthreads();
+            // ---- P3: out^T = St^T W^T ; Pm^T = triu-masked pK W^T -> sPm ; St += pK^T V (first head)
+            f32x4 accO[TPW_O];
+#pragma unroll
+            for (int i = 0; i < TPW_O; ++i) {
+                const int t = wave + i * NW;
+                accO[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (t < CF::NTD * MTC)
+                    mma_ab<ST, LDS, LDS>(accO[i], &sStT[0][0], (t / MTC) * 16, &sW[0][0], (t % MTC) * 16, lane);
+            }
+#pragma unroll
+            for (int i = 0; i < TPW_M; ++i) {
+                const int t = wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int tu = t / MTC, tt = t % MTC;  // rows tau, cols t
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<ST, LDS, LDS>(acc, &sPK[0][0], tu * 16, &sW[0][0], tt * 16, lane);
+                    const int tau = tu * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (tau + e > tok)
+                            acc[e] = 0.0f;
+                    st_vec4(&sPm[tok][tau], acc);
+                }
+            }
+            if (g == G - 1) {
+#pragma unroll
+                for (int i = 0; i < TPW_S; ++i) {
+                    const int t = wave + i * NW;
+                    if (t < CF::NTS * CF::NTD)
+                        mma_ab<C, LDC, LDC>(accS[i], &sPKt[0][0], (t / CF::NTD) * 16, &sVt[cur][0][0],
+                                            (t % CF::NTD) * 16, lane);
+                }
+            }
+            __syncthreads();
+            // ---- P4: out^T += V^T Pm^T -> sO ; new St^T -> sStT ; next rows -> LDS
+#pragma unroll
+            for (int i = 0; i < TPW_O; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTD * MTC) {
+                    const int td = t / MTC, tt = t % MTC;
+                    mma_ab<C, LDC, LDC>(accO[i], &sVt[cur][0][0], td * 16, &sPm[0][0], tt * 16, lane);
+                    const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    if constexpr (OUT_F32)
+                        *reinterpret_cast<f32x4 *>(&sO[tok][d]) = accO[i];
+                    else
+                        st_vec4(&sO[tok][d], accO[i]);
+                }
+            }
+            prev_t0 = t0;
+            prev_nv = nv;
+            prev_h = hq;
+            if (g == G - 1) {
+#pragma unroll
+                for (int i = 0; i < TPW_S; ++i) {
+                    const int t = wave + i * NW;
+                    if (t < CF::NTS * CF::NTD) {
+                        const int r = acc_row((t / CF::NTD) * 16, lane), col = acc_col((t % CF::NTD) * 16, lane);
+                        st_vec4(&sStT[col][r], accS[i]);
+                    }
+                }
+                if (more) {
+                    tile_store_rows<CF>(&sK[0][0], pk, tid);
+                    tile_store_trans<CF>(&sVt[nxt][0][0], pv, tid);
+                    if (G == 1)
+                        tile_store_rows<CF>(&sQ[0][0], pq, tid);
+                    else {
+                        u32x4 tq[CF::PF];
+                        const int t1 = t0 + C;
+                        tile_load<CF>(tq, row_ptr(P.q, c.b, c.hk * G, t1), P.q.st, min(C, c.t_end - t1), tid);
+                        tile_store_rows<CF>(&sQ[0][0], tq, tid);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // last output rows
+    {
+        constexpr int OCH = DP * (int)sizeof(OT) / 16;
+        for (int i = tid; i < C * OCH; i += NTH) {
+            const int row = i / OCH, ch = i % OCH;
+            if (row < prev_nv) {
+                OT *dst = reinterpret_cast<OT *>(P.out.p) + (int64_t)c.st * P.out.tile + c.b * P.out.sb +
+                          prev_h * P.out.sh + (int64_t)(prev_t0 + row) * P.out.st + ch * (16 / (int)sizeof(OT));
+                *reinterpret_cast<u32x4 *>(dst) = *reinterpret_cast<const u32x4 *>(&sO[row][ch * (16 / (int)sizeof(OT))]);
+            }
+        }
+    }
+}
+
+
+// Planes fragments for the soft-hash backward, dx^T = P gproj^T: A operand rows d of
+// one 16-row head-dim tile, k = projection rows j (natural order, zero-padded bits).
+template <class CF, int DP, int NSLOT>
+struct BackFrags {
+    bf16x8 f[NSLOT][CF::LKP / 32 > 0 ? CF::LKP / 32 : 1];
+
+    RACE_DEV void load(const ScanParams &P, int l0, int Lt_valid, int lane, int wave, int ntiles_t)
+    {
+        const int LKtot = P.L * P.K;
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) {
+            const int t = wave + i * (CF::NTH / 64);
+            const int td = t / ntiles_t;
+            const int d = td * 16 + (lane & 15);
+#pragma unroll
+            for (int kb = 0; kb < (CF::LKP + 31) / 32; ++kb) {
+                bf16x8 v;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int j = kb * 32 + (lane >> 4) * 8 + e;
+                    const int table = j >> 2, bit = j & 3;
+                    float x = 0.0f;
+                    if (j < CF::LKP && bit < P.K && table < Lt_valid && d < P.D)
+                        x = P.planes[d * LKtot + (l0 + table) * P.K + bit];
+                    v[e] = (__bf16)x;
+                }
+                f[i][kb] = v;
+            }
+        }
+    }
+};
+
+// Soft-hash backward of one (token, table): gproj[k] = dL/dproj_k from the table's
+// probabilities p, its soft bits u and dL/dp (softmax + corner + tanh chain).
+template <int KB>
+RACE_DEV void softhash_bwd_ct(const float *u, const float *p, const float *gp, float scale, float inv_scale,
+                              float *gproj)
+{
+    constexpr int R = 1 << KB;
+    float dot = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        dot += p[r] * gp[r];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        float gu = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float gz = p[r] * (gp[r] - dot);
+            gu += ((r >> (KB - 1 - k)) & 1) ? gz : -gz;
+        }
+        const float th = u[k] * scale;
+        gproj[k] = gu * inv_scale * (1.0f - th * th);
+    }
+}
+
+// Coalesced store of a staged C x DP tile (rows < nv) to a [B][H][T][D] output view.
+template <class OT, int C, int DP, int LDO, int NTH>
+RACE_DEV void store_staged(const OutView &o, int b, int h, int st, int t0, int nv, const OT (*sO)[LDO], int tid)
+{
+    constexpr int EPC = 16 / (int)sizeof(OT);  // elements per 16-byte chunk
+    constexpr int OCH = DP / EPC;
+    for (int i = tid; i < C * OCH; i += NTH) {
+        const int row = i / OCH, ch = i % OCH;
+        if (row < nv) {
+            OT *dst = reinterpret_cast<OT *>(o.p) + (int64_t)st * o.tile + b * o.sb + h * o.sh +
+                      (int64_t)(t0 + row) * o.st + ch * EPC;
+            *reinterpret_cast<u32x4 *>(dst) = *reinterpret_cast<const u32x4 *>(&sO[row][ch * EPC]);
+        }
+    }
+}
+
+// ============================================================================ backward totals
+// Forward-order pass over a block: dq (soft-hash backward of gpQ = gW/(A+eps)) and the
+// block totals of W^T go (into ws2B) and of gA (into ws2A).
+template <int ST, int DP, int KB, int NW, bool OUT_F32>
+__global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParams P)
+{
+    using CF = FCfg<ST, DP, KB, NW>;
+    constexpr int C = CF::C, NTH = CF::NTH, R = CF::R, MTC = CF::MTC;
+    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG;
+    using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
+    constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
+    __shared__ __align__(16) __bf16 sK[C][LDX];
+    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sV[C][LDX];
+    __shared__ __align__(16) __bf16 sVt[DP][LDC];
+    __shared__ __align__(16) __bf16 sGO[C][LDX];
+    __shared__ __align__(16) __bf16 sGOt[DP][LDC];
+    __shared__ __align__(16) __bf16 sPKt[ST][LDC];
+    __shared__ __align__(16) __bf16 sPQ[C][LDS];
+    __shared__ __align__(16) __bf16 sWt[ST][LDC];
+    __shared__ __align__(16) __bf16 sMg[C][LDC];
+    __shared__ __align__(16) __bf16 sStS[ST][LDX];
+    __shared__ __align__(16) float sGP[C][ST + 4];
+    __shared__ __align__(16) __bf16 sGU[C][LDG];
+    __shared__ __align__(16) OT sO[C][LDO];
+    __shared__ __align__(16) float sA0[2][ST];
+    __shared__ float sGAred[ST];
+
+    const Ctx c = make_ctx(P, ST);
+    const int tid = c.tid, lane = c.lane, wave = c.wave;
+    constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;   // k then q projection tiles
+    constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
+    constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;
+    constexpr int TPW_O = (CF::NTD * MTC + NW - 1) / NW;
+    constexpr int TPW_M = (MTC * MTC + NW - 1) / NW;
+    FusedFrags<CF, DP, TPW_P> fr;
+    fr.load(P, c.l0, c.Lt, lane, wave);
+    BackFrags<CF, DP, TPW_O> bk;
+    bk.load(P, c.l0, c.Lt, lane, wave, MTC);
+    zero_lds_bf16(&sPKt[0][0], ST * LDC, tid, NTH);
+    zero_lds_bf16(&sPQ[0][0], C * LDS, tid, NTH);
+    zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
+    for (int i = tid; i < ST; i += NTH)
+        sGAred[i] = 0.0f;
+
+    // St^T (lane: col s, rows d) at the block start, and dS^T totals
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    f32x4 accS[TPW_S], accD[TPW_S];
+    {
+        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < TPW_S; ++i) {
+            const int t = wave + i * NW;
+            accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            accD[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (t < CF::NTS * CF::NTD) {
+                const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
+                accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + d);
+                st_vec4(&sStS[s][d], accS[i]);
+            }
+        }
+        const float *wA = P.wsA + slot * P.S_pad + c.s0;
+        for (int s = tid; s < ST; s += NTH)
+            sA0[0][s] = wA[s];
+    }
+    f32x4 accGA[TPW_A];
+#pragma unroll
+    for (int i = 0; i < TPW_A; ++i)
+        accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int G = P.G;
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    int prev_t0 = -1, prev_nv = 0, prev_h = 0;
+    f32x4 accI[TPW_A];  // 1/(A+eps), A^T tiles
+    float uq[TPW_P][4], pq_[TPW_P][R];
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        const int cur = sc & 1, nxt = cur ^ 1;
+        for (int g = 0; g < G; ++g) {
+            const int hq = c.hk * G + g;
+            // ---- P0: rows of this (sub-chunk, head) into LDS
+            {
+                u32x4 r[CF::PF];
+                if (g == 0) {
+                    tile_load<CF>(r, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, tid);
+                    tile_store_rows<CF>(&sK[0][0], r, tid);
+                    tile_load<CF>(r, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, tid);
+                    tile_store_rows<CF>(&sV[0][0], r, tid);
+                    tile_store_trans<CF>(&sVt[0][0], r, tid);
+                }
+                tile_load<CF>(r, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
+                tile_store_rows<CF>(&sQ[0][0], r, tid);
+                tile_load<CF>(r, row_ptr(P.go, c.b, hq, t0), P.go.st, nv, tid);
+                tile_store_rows<CF>(&sGO[0][0], r, tid);
+                tile_store_trans<CF>(&sGOt[0][0], r, tid);
+            }
+            __syncthreads();
+            // ---- P1: soft-hash of k (first head) -> pK^T ; of q -> pQ (kept in registers)
+#pragma unroll
+            for (int i = 0; i < TPW_P; ++i) {
+                const int t = wave + i * NW;
+                const bool isk = t < CF::NPT;
+                if (t < 2 * CF::NPT && (!isk || g == 0)) {
+                    const int tq_ = isk ? t : t - CF::NPT;
+                    const int jt = tq_ / MTC, tt = tq_ % MTC;
+                    const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
+                    float u[4], p[R];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        u[e] = tanh_f(acc[e]) * P.inv_scale;
+                    expand_ct<KB>(u, p);
+                    const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                    const bool ok = tok < nv && table < c.Lt;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        p[r] = ok ? p[r] : 0.0f;
+                    if (table < CF::LT) {
+                        if (isk) {
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+                                sPKt[table * R + r][tok] = (__bf16)p[r];
+                        } else {
+#pragma unroll
+                            for (int h = 0; h < R / 4; ++h) {
+                                bf16x4 w;
+#pragma unroll
+                                for (int e = 0; e < 4; ++e)
+                                    w[e] = (__bf16)p[4 * h + e];
+                                *reinterpret_cast<bf16x4 *>(&sPQ[tok][table * R + 4 * h]) = w;
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        uq[i][e] = u[e];
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        pq_[i][r] = p[r];
+                }
+            }
+            if (prev_t0 >= 0)
+                store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
+            __syncthreads();
+            // ---- P2: A^T scan (first head) -> 1/(A+eps); W^T -> sWt ; Mg^T -> sMg ; gW^T = St go^T
+            f32x4 accW[TPW_A], accG[TPW_A];
+#pragma unroll
+            for (int i = 0; i < TPW_A; ++i) {
+                const int t = wave + i * NW;
+                accW[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (t < CF::NTS * MTC) {
+                    const int ts = t / MTC, tt = t % MTC;
+                    const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    if (g == 0) {
+                        f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
+                        const __bf16 *pa = &sPKt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
+                        EngBF16::mma(a, *reinterpret_cast<const bf16x8 *>(pa), fr.tri_of(tt));
+                        if (tt == MTC - 1 && (lane & 15) == 15)
+                            *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            accI[i][e] = frcp(a[e] + P.eps);
+                    }
+                    const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        accW[i][e] = (float)q4[e] * accI[i][e];
+                        sWt[s + e][tok] = (__bf16)accW[i][e];
+                    }
+                    mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TPW_M; ++i) {
+                const int t = wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int tu = t / MTC, tt = t % MTC;  // rows tau, cols t
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<DP, LDX, LDX>(acc, &sV[0][0], tu * 16, &sGO[0][0], tt * 16, lane);
+                    const int tau = tu * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (tau + e > tok)
+                            acc[e] = 0.0f;
+                    st_vec4(&sMg[tok][tau], acc);
+                }
+            }
+            __syncthreads();
+            // ---- P3: gW^T += pK^T Mg^T ; gpQ^T -> sGP ; gA ; dS^T += go^T W ; St^T += V^T pK (last head)
+#pragma unroll
+            for (int i = 0; i < TPW_A; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTS * MTC) {
+                    const int ts = t / MTC, tt = t % MTC;
+                    const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    mma_ab<C, LDC, LDC>(accG[i], &sPKt[0][0], ts * 16, &sMg[0][0], tt * 16, lane);
+                    f32x4 gpq;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        gpq[e] = accG[i][e] * accI[i][e];
+                        accGA[i][e] -= gpq[e] * accW[i][e];
+                    }
+                    *reinterpret_cast<f32x4 *>(&sGP[tok][s]) = gpq;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TPW_S; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTS * CF::NTD) {
+                    const int td = t / CF::NTS, ts = t % CF::NTS;
+                    mma_ab<C, LDC, LDC>(accD[i], &sGOt[0][0], td * 16, &sWt[0][0], ts * 16, lane);
+                    if (g == G - 1)
+                        mma_ab<C, LDC, LDC>(accS[i], &sVt[0][0], td * 16, &sPKt[0][0], ts * 16, lane);
+                }
+            }
+            __syncthreads();
+            // ---- P4: soft-hash backward of q -> gproj -> sGU ; new St -> sStS (last head)
+#pragma unroll
+            for (int i = 0; i < TPW_P; ++i) {
+                const int t = wave + i * NW;
+                if (t >= CF::NPT && t < 2 * CF::NPT) {
+                    const int tq_ = t - CF::NPT;
+                    const int jt = tq_ / MTC, tt = tq_ % MTC;
+                    const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                    if (table < CF::LT) {
+                        float gp[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int h = 0; h < R / 4; ++h) {
+                            const f32x4 x = *reinterpret_cast<const f32x4 *>(&sGP[tok][table * R + 4 * h]);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                gp[4 * h + e] = x[e];
+                        }
+                        softhash_bwd_ct<KB>(uq[i], pq_[i], gp, P.scale, P.inv_scale, gproj);
+                        bf16x4 w;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
+                        *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
+                    }
+                }
+            }
+            if (g == G - 1) {
+#pragma unroll
+                for (int i = 0; i < TPW_S; ++i) {
+                    const int t = wave + i * NW;
+                    if (t < CF::NTS * CF::NTD) {
+                        const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
+                        st_vec4(&sStS[s][d], accS[i]);
+                    }
+                }
+            }
+            __syncthreads();
+            // ---- P5: dq^T = P gproj^T -> sO
+#pragma unroll
+            for (int i = 0; i < TPW_O; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTD * MTC) {
+                    const int td = t / MTC, tt = t % MTC;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    const __bf16 *pb = &sGU[0][0] + (tt * 16 + (lane & 15)) * LDG + (lane >> 4) * 8;
+#pragma unroll
+                    for (int kb = 0; kb < (CF::LKP + 31) / 32; ++kb)
+                        EngBF16::mma(acc, bk.f[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+                    const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    if constexpr (OUT_F32)
+                        *reinterpret_cast<f32x4 *>(&sO[tok][d]) = acc;
+                    else
+                        st_vec4(&sO[tok][d], acc);
+                }
+            }
+            prev_t0 = t0;
+            prev_nv = nv;
+            prev_h = hq;
+            __syncthreads();
+        }
+    }
+    store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
+
+    // block totals: dS^T -> ws2B [s][d] ; gA (sum over tokens) -> ws2A
+    float *wB = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+    for (int i = 0; i < TPW_S; ++i) {
+        const int t = wave + i * NW;
+        if (t < CF::NTS * CF::NTD) {
+            const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
+            *reinterpret_cast<f32x4 *>(wB + (int64_t)s * P.DPw + d) = accD[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TPW_A; ++i) {
+        const int t = wave + i * NW;
+        if (t < CF::NTS * MTC) {
+            const int ts = t / MTC;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = accGA[i][e];
+                v += __shfl_xor(v, 1);
+                v += __shfl_xor(v, 2);
+                v += __shfl_xor(v, 4);
+                v += __shfl_xor(v, 8);
+                if ((lane & 15) == 0)
+                    atomicAdd(&sGAred[ts * 16 + ((lane >> 4) << 2) + e], v);
+            }
+        }
+    }
+    __syncthreads();
+    float *wA = P.ws2A + slot * P.S_pad + c.s0;
+    for (int s = tid; s < ST; s += NTH)
+        wA[s] = sGAred[s];
+}
+
+
+// ============================================================================ backward main
+// Forward-order pass over a block with the suffix states (dS, gAhat) shrinking by each
+// sub-chunk's contribution (exact forward A and St, see race_scan_kernels.h):
+//   gpK^T = gAhat + dS V^T + W^T Mv^T ,   gv^T = dS^T pK^T + go^T Mp^T
+// then dk through the soft-hash backward of k and dv directly.
+template <int ST, int DP, int KB, int NW, bool OUT_F32>
+__global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams P)
+{
+    using CF = FCfg<ST, DP, KB, NW>;
+    constexpr int C = CF::C, NTH = CF::NTH, R = CF::R, MTC = CF::MTC;
+    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG, LDF = ST + 4;
+    using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
+    constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
+    // Two LDS regions are shared by arrays with disjoint lifetimes:
+    //   uKQ: k, q rows (load -> projection) and dS^T copy (last head -> gv/gpK update);
+    //   uPW: pQ, W (projection -> Mp) and the dk, dv staging (sub-chunk end -> next load).
+    constexpr int SZ_K = C * LDX * 2, SZ_DST = DP * LDS * 2;
+    constexpr int SZ_PQ = C * LDS * 2, SZ_O = C * LDO * (int)sizeof(OT);
+    constexpr int SZ_KQ = 2 * SZ_K > SZ_DST ? 2 * SZ_K : SZ_DST;
+    constexpr int SZ_PW = 2 * SZ_PQ > 2 * SZ_O ? 2 * SZ_PQ : 2 * SZ_O;
+    __shared__ __align__(16) char uKQ[SZ_KQ];
+    __shared__ __align__(16) char uPW[SZ_PW];
+    __bf16(*sK)[LDX] = reinterpret_cast<__bf16(*)[LDX]>(uKQ);
+    __bf16(*sQ)[LDX] = reinterpret_cast<__bf16(*)[LDX]>(uKQ + SZ_K);
+    __bf16(*sdSt)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uKQ);
+    __bf16(*sPQ)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uPW);
+    __bf16(*sW)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uPW + SZ_PQ);
+    OT(*sOk)[LDO] = reinterpret_cast<OT(*)[LDO]>(uPW);
+    OT(*sOv)[LDO] = reinterpret_cast<OT(*)[LDO]>(uPW + SZ_O);
+    __shared__ __align__(16) __bf16 sV[C][LDX];
+    __shared__ __align__(16) __bf16 sVt[DP][LDC];
+    __shared__ __align__(16) __bf16 sGO[C][LDX];
+    __shared__ __align__(16) __bf16 sGOt[DP][LDC];
+    __shared__ __align__(16) __bf16 sPK[C][LDS];
+    __shared__ __align__(16) __bf16 sPKt[ST][LDC];
+    __shared__ __align__(16) __bf16 sWt[ST][LDC];
+    __shared__ __align__(16) __bf16 sMg[C][LDC];   // Mg^T as [t][tau]
+    __shared__ __align__(16) __bf16 sMv[C][LDC];   // Mg   as [tau][t]
+    __shared__ __align__(16) __bf16 sMp[C][LDC];   // Mp^T as [tau][t]
+    __shared__ __align__(16) __bf16 sStS[ST][LDX];
+    __shared__ __align__(16) __bf16 sdS[ST][LDX];
+    __shared__ __align__(16) float sF[C][LDF];     // gA, then gAhat, then gpK (per token row)
+    __shared__ __align__(16) __bf16 sGU[C][LDG];
+    __shared__ __align__(16) float sA0[2][ST];
+    __shared__ float sGAe[ST];
+
+    const Ctx c = make_ctx(P, ST);
+    const int tid = c.tid, lane = c.lane, wave = c.wave;
+    constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;
+    constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
+    constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;
+    constexpr int TPW_O = (CF::NTD * MTC + NW - 1) / NW;
+    constexpr int TPW_M = (MTC * MTC + NW - 1) / NW;
+    FusedFrags<CF, DP, TPW_P> fr;
+    fr.load(P, c.l0, c.Lt, lane, wave);
+    BackFrags<CF, DP, TPW_O> bk;
+    bk.load(P, c.l0, c.Lt, lane, wave, MTC);
+    zero_lds_bf16(&sPK[0][0], C * LDS, tid, NTH);
+    zero_lds_bf16(&sPKt[0][0], ST * LDC, tid, NTH);
+    zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
+
+    // St^T at the block start (lane: col s, rows d); suffix dS from the block start in
+    // both orientations: accD (lane: col d, rows s) and accDT (lane: col s, rows d).
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    f32x4 accS[TPW_S], accD[TPW_S], accDT[TPW_S];
+    {
+        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+        const float *wB2 = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < TPW_S; ++i) {
+            const int t = wave + i * NW;
+            accS[i] = accD[i] = accDT[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (t < CF::NTS * CF::NTD) {
+                const int td = t / CF::NTS, ts = t % CF::NTS;
+                const int d = td * 16 + ((lane >> 4) << 2), s = ts * 16 + (lane & 15);
+                accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + d);
+                accDT[i] = *reinterpret_cast<const f32x4 *>(wB2 + (int64_t)s * P.DPw + d);
+                st_vec4(&sStS[s][d], accS[i]);
+                // accD: rows s2 = ts*16 + 4g + e, col d2 = td*16 + (lane & 15)
+                const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accD[i][e] = wB2[(int64_t)(s2 + e) * P.DPw + d2];
+            }
+        }
+        const float *wA = P.wsA + slot * P.S_pad + c.s0;
+        const float *wA2 = P.ws2A + slot * P.S_pad + c.s0;
+        for (int s = tid; s < ST; s += NTH) {
+            sA0[0][s] = wA[s];
+            sGAe[s] = wA2[s];
+        }
+    }
+
+    const int G = P.G;
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    int prev_t0 = -1, prev_nv = 0;
+    f32x4 accI[TPW_A], accPK[TPW_A], accV[TPW_O], accGA[TPW_A];
+    float uk[TPW_P][4], pk_[TPW_P][R];
+    for (int sc = 0; sc < nsub; ++sc) {
+        const int t0 = c.t_begin + sc * C;
+        const int nv = min(C, c.t_end - t0);
+        const int cur = sc & 1, nxt = cur ^ 1;
+#pragma unroll
+        for (int i = 0; i < TPW_A; ++i)
+            accPK[i] = accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < TPW_O; ++i)
+            accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < G; ++g) {
+            const int hq = c.hk * G + g;
+            // ---- P0: rows into LDS
+            {
+                u32x4 r[CF::PF];
+                if (g == 0) {
+                    tile_load<CF>(r, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, tid);
+                    tile_store_rows<CF>(&sK[0][0], r, tid);
+                    tile_load<CF>(r, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, tid);
+                    tile_store_rows<CF>(&sV[0][0], r, tid);
+                    tile_store_trans<CF>(&sVt[0][0], r, tid);
+                }
+                tile_load<CF>(r, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
+                tile_store_rows<CF>(&sQ[0][0], r, tid);
+                tile_load<CF>(r, row_ptr(P.go, c.b, hq, t0), P.go.st, nv, tid);
+                tile_store_rows<CF>(&sGO[0][0], r, tid);
+                tile_store_trans<CF>(&sGOt[0][0], r, tid);
+            }
+            if (g == 0 && prev_t0 >= 0) {
+                store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
+                store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
+            }
+            __syncthreads();
+            // ---- P1: soft-hash of k (first head) -> pK, pK^T ; of q -> pQ
+#pragma unroll
+            for (int i = 0; i < TPW_P; ++i) {
+                const int t = wave + i * NW;
+                const bool isk = t < CF::NPT;
+                if (t < 2 * CF::NPT && (!isk || g == 0)) {
+                    const int tq_ = isk ? t : t - CF::NPT;
+                    const int jt = tq_ / MTC, tt = tq_ % MTC;
+                    const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
+                    float u[4], p[R];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        u[e] = tanh_f(acc[e]) * P.inv_scale;
+                    expand_ct<KB>(u, p);
+                    const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                    const bool ok = tok < nv && table < c.Lt;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        p[r] = ok ? p[r] : 0.0f;
+                    if (table < CF::LT) {
+                        __bf16 *row = isk ? &sPK[tok][table * R] : &sPQ[tok][table * R];
+#pragma unroll
+                        for (int h = 0; h < R / 4; ++h) {
+                            bf16x4 w;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                w[e] = (__bf16)p[4 * h + e];
+                            *reinterpret_cast<bf16x4 *>(row + 4 * h) = w;
+                        }
+                        if (isk) {
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+                                sPKt[table * R + r][tok] = (__bf16)p[r];
+                        }
+                    }
+                    if (isk) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            uk[i][e] = u[e];
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+                            pk_[i][r] = p[r];
+                    }
+                }
+            }
+            __syncthreads();
+            // ---- P2: A^T (first head); W^T -> sW, sWt ; Mg^T -> sMg ; Mg -> sMv ; gW^T = St go^T
+            f32x4 accW[TPW_A], accG[TPW_A];
+#pragma unroll
+            for (int i = 0; i < TPW_A; ++i) {
+                const int t = wave + i * NW;
+                accW[i] = accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (t < CF::NTS * MTC) {
+                    const int ts = t / MTC, tt = t % MTC;
+                    const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    if (g == 0) {
+                        f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
+                        const __bf16 *pa = &sPKt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
+                        EngBF16::mma(a, *reinterpret_cast<const bf16x8 *>(pa), fr.tri_of(tt));
+                        if (tt == MTC - 1 && (lane & 15) == 15)
+                            *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            accI[i][e] = frcp(a[e] + P.eps);
+                    }
+                    const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        accW[i][e] = (float)q4[e] * accI[i][e];
+                        sWt[s + e][tok] = (__bf16)accW[i][e];
+                    }
+                    st_vec4(&sW[tok][s], accW[i]);
+                    mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TPW_M; ++i) {
+                const int t = wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int ta = t / MTC, tb = t % MTC;
+                    // Mg^T[tau][t] (rows tau = ta, cols t = tb) -> sMg[t][tau]
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<DP, LDX, LDX>(acc, &sV[0][0], ta * 16, &sGO[0][0], tb * 16, lane);
+                    const int r0 = ta * 16 + ((lane >> 4) << 2), c0 = tb * 16 + (lane & 15);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (r0 + e > c0)
+                            acc[e] = 0.0f;
+                    st_vec4(&sMg[c0][r0], acc);
+                    // Mg[t][tau] (rows t = ta, cols tau = tb) -> sMv[tau][t]
+                    f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<DP, LDX, LDX>(acc2, &sGO[0][0], ta * 16, &sV[0][0], tb * 16, lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (c0 > r0 + e)
+                            acc2[e] = 0.0f;
+                    st_vec4(&sMv[c0][r0], acc2);
+                }
+            }
+            __syncthreads();
+            // ---- P3: gW^T += pK^T Mg^T ; gA^T ; gpK^T += W^T Mv^T ; Mp^T -> sMp ;
+            //          dS, dS^T -= W^T go ; St^T += V^T pK (last head)
+#pragma unroll
+            for (int i = 0; i < TPW_A; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTS * MTC) {
+                    const int ts = t / MTC, tt = t % MTC;
+                    mma_ab<C, LDC, LDC>(accG[i], &sPKt[0][0], ts * 16, &sMg[0][0], tt * 16, lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accGA[i][e] -= accG[i][e] * accI[i][e] * accW[i][e];
+                    mma_ab<C, LDC, LDC>(accPK[i], &sWt[0][0], ts * 16, &sMv[0][0], tt * 16, lane);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TPW_M; ++i) {
+                const int t = wave + i * NW;
+                if (t < MTC * MTC) {
+                    const int ta = t / MTC, tb = t % MTC;  // rows t = ta, cols tau = tb
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<ST, LDS, LDS>(acc, &sW[0][0], ta * 16, &sPK[0][0], tb * 16, lane);
+                    const int r0 = ta * 16 + ((lane >> 4) << 2), c0 = tb * 16 + (lane & 15);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (r0 + e < c0)
+                            acc[e] = 0.0f;
+                    st_vec4(&sMp[c0][r0], acc);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TPW_S; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTS * CF::NTD) {
+                    const int td = t / CF::NTS, ts = t % CF::NTS;
+                    // dS[s][d] -= sum_t W[t][s] go[t][d]   (accD: rows s of tile ts, cols d of td)
+                    {
+                        const __bf16 *pa = &sWt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
+                        const __bf16 *pb = &sGOt[0][0] + (td * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
+                        EngBF16::mma(accD[i], EngBF16::neg(*reinterpret_cast<const bf16x8 *>(pa)),
+                                     *reinterpret_cast<const bf16x8 *>(pb));
+                    }
+                    {
+                        const __bf16 *pa = &sGOt[0][0] + (td * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
+                        const __bf16 *pb = &sWt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
+                        EngBF16::mma(accDT[i], EngBF16::neg(*reinterpret_cast<const bf16x8 *>(pa)),
+                                     *reinterpret_cast<const bf16x8 *>(pb));
+                    }
+                    if (g == G - 1)
+                        mma_ab<C, LDC, LDC>(accS[i], &sVt[0][0], td * 16, &sPKt[0][0], ts * 16, lane);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TPW_A; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTS * MTC && g == G - 1) {
+                    const int ts = t / MTC, tt = t % MTC;
+                    const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    *reinterpret_cast<f32x4 *>(&sF[tok][s]) = accGA[i];
+                }
+            }
+            __syncthreads();
+            // ---- P4: gv^T += go^T Mp^T ; (last head) dS copies, gAhat scan
+#pragma unroll
+            for (int i = 0; i < TPW_O; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTD * MTC)
+                    mma_ab<C, LDC, LDC>(accV[i], &sGOt[0][0], (t / MTC) * 16, &sMp[0][0], (t % MTC) * 16, lane);
+            }
+            if (g == G - 1) {
+#pragma unroll
+                for (int i = 0; i < TPW_S; ++i) {
+                    const int t = wave + i * NW;
+                    if (t < CF::NTS * CF::NTD) {
+                        const int td = t / CF::NTS, ts = t % CF::NTS;
+                        const int d = td * 16 + ((lane >> 4) << 2), s = ts * 16 + (lane & 15);
+                        st_vec4(&sdS[s][d], accDT[i]);
+                        const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
+                        st_vec4(&sdSt[d2][s2], accD[i]);
+                    }
+                }
+                // gAhat_t = gAhat_end + sum_{tau >= t} gA, gAhat_end = gAhat_start - sum_c gA
+                for (int s = tid; s < ST; s += NTH) {
+                    float tot = 0.0f;
+                    for (int t = 0; t < C; ++t)
+                        tot += sF[t][s];
+                    float run = sGAe[s] - tot;
+                    const float end = run;
+                    for (int t = C - 1; t >= 0; --t) {
+                        run += sF[t][s];
+                        sF[t][s] = run;
+                    }
+                    sGAe[s] = end;
+                }
+            }
+            if (g + 1 < G)
+                __syncthreads();
+        }
+        __syncthreads();
+        // ---- P5: gpK^T += dS V^T + gAhat -> sF ; gv^T += dS^T pK^T -> sOv ; St -> sStS
+#pragma unroll
+        for (int i = 0; i < TPW_A; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTS * MTC) {
+                const int ts = t / MTC, tt = t % MTC;
+                const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                mma_ab<DP, LDX, LDX>(accPK[i], &sdS[0][0], ts * 16, &sV[0][0], tt * 16, lane);
+                const f32x4 gh = *reinterpret_cast<const f32x4 *>(&sF[tok][s]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    accPK[i][e] += gh[e];
+                *reinterpret_cast<f32x4 *>(&sF[tok][s]) = accPK[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TPW_O; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTD * MTC) {
+                const int td = t / MTC, tt = t % MTC;
+                mma_ab<ST, LDS, LDS>(accV[i], &sdSt[0][0], td * 16, &sPK[0][0], tt * 16, lane);
+                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sOv[tok][d]) = accV[i];
+                else
+                    st_vec4(&sOv[tok][d], accV[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TPW_S; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTS * CF::NTD) {
+                const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
+                st_vec4(&sStS[s][d], accS[i]);
+            }
+        }
+        __syncthreads();
+        // ---- P6: soft-hash backward of k -> sGU
+#pragma unroll
+        for (int i = 0; i < TPW_P; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NPT) {
+                const int jt = t / MTC, tt = t % MTC;
+                const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                if (table < CF::LT) {
+                    float gp[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int h = 0; h < R / 4; ++h) {
+                        const f32x4 x = *reinterpret_cast<const f32x4 *>(&sF[tok][table * R + 4 * h]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            gp[4 * h + e] = x[e];
+                    }
+                    softhash_bwd_ct<KB>(uk[i], pk_[i], gp, P.scale, P.inv_scale, gproj);
+                    bf16x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
+                    *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
+                }
+            }
+        }
+        __syncthreads();
+        // ---- P7: dk^T = P gproj^T -> sOk
+#pragma unroll
+        for (int i = 0; i < TPW_O; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTD * MTC) {
+                const int td = t / MTC, tt = t % MTC;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                const __bf16 *pb = &sGU[0][0] + (tt * 16 + (lane & 15)) * LDG + (lane >> 4) * 8;
+#pragma unroll
+                for (int kb = 0; kb < (CF::LKP + 31) / 32; ++kb)
+                    EngBF16::mma(acc, bk.f[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sOk[tok][d]) = acc;
+                else
+                    st_vec4(&sOk[tok][d], acc);
+            }
+        }
+        prev_t0 = t0;
+        prev_nv = nv;
+        __syncthreads();
+    }
+    store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
+    store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
+}
+
+}  // namespace race
