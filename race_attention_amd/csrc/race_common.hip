@@ -13,52 +13,71 @@
 namespace race {
 
 // ============================================================================ block scan
-__global__ void race_block_scan(float *ws, int64_t elems, int NB, int rev)
+// One workgroup owns SCAN_COLS consecutive state elements of one stream and walks the
+// blocks in super-chunks of SCAN_SEGS * SCAN_SEG blocks. Each thread loads one segment
+// of SCAN_SEG blocks at once (independent loads, one memory latency per super-chunk),
+// the segment totals are combined through LDS, and each thread writes its segment's
+// running sums from its offset. Sums run in fp64 and are rounded once per output.
+//   rev = 0: slot b <- sum_{b' < b} x_b' (exclusive), slot NB <- total
+//   rev = 1: slot b <- sum_{b' >= b} x_b' (inclusive suffix), slot NB <- 0
+constexpr int SCAN_COLS = 64, SCAN_SEGS = 16, SCAN_SEG = 32;
+
+__global__ __launch_bounds__(SCAN_COLS *SCAN_SEGS) void race_block_scan(float *ws, int64_t elems, int NB, int rev)
 {
-    // Loads of a batch of blocks are issued together (they do not depend on the
-    // running sum), so each thread waits one memory latency per batch, not per block.
-    constexpr int BATCH = 16;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= elems)
-        return;
+    __shared__ double tot[SCAN_SEGS][SCAN_COLS];
+    const int col = threadIdx.x % SCAN_COLS, seg = threadIdx.x / SCAN_COLS;
+    const int64_t e = (int64_t)blockIdx.x * SCAN_COLS + col;
+    const bool live = e < elems;
     float *base = ws + (int64_t)blockIdx.y * (NB + 1) * elems + e;
-    double run = 0.0;
-    float x[BATCH];
-    if (!rev) {
-        for (int b0 = 0; b0 < NB; b0 += BATCH) {
+    constexpr int SUPER = SCAN_SEGS * SCAN_SEG;
+    double carry = 0.0;
+    for (int c0 = 0; c0 < NB; c0 += SUPER) {
+        // block index of this thread's i-th element (ascending for rev = 0, descending for rev = 1)
+        const int first = rev ? NB - 1 - c0 - seg * SCAN_SEG : c0 + seg * SCAN_SEG;
+        const int step = rev ? -1 : 1;
+        float x[SCAN_SEG];
+        double t = 0.0;
 #pragma unroll
-            for (int i = 0; i < BATCH; ++i)
-                x[i] = (b0 + i < NB) ? base[(int64_t)(b0 + i) * elems] : 0.0f;
-#pragma unroll
-            for (int i = 0; i < BATCH; ++i) {
-                if (b0 + i < NB) {
-                    base[(int64_t)(b0 + i) * elems] = (float)run;
-                    run += (double)x[i];
-                }
-            }
+        for (int i = 0; i < SCAN_SEG; ++i) {
+            const int b = first + i * step;
+            const bool ok = live && (rev ? (b >= 0 && b <= NB - 1 - c0 - seg * SCAN_SEG) : (b < NB));
+            x[i] = ok ? base[(int64_t)b * elems] : 0.0f;
         }
-        base[(int64_t)NB * elems] = (float)run;
-    } else {
-        base[(int64_t)NB * elems] = 0.0f;
-        for (int b1 = NB; b1 > 0; b1 -= BATCH) {
 #pragma unroll
-            for (int i = 0; i < BATCH; ++i)
-                x[i] = (b1 - 1 - i >= 0) ? base[(int64_t)(b1 - 1 - i) * elems] : 0.0f;
+        for (int i = 0; i < SCAN_SEG; ++i)
+            t += (double)x[i];
+        tot[seg][col] = t;
+        __syncthreads();
+        double run = carry, all = 0.0;
 #pragma unroll
-            for (int i = 0; i < BATCH; ++i) {
-                if (b1 - 1 - i >= 0) {
-                    run += (double)x[i];
-                    base[(int64_t)(b1 - 1 - i) * elems] = (float)run;
-                }
-            }
+        for (int j = 0; j < SCAN_SEGS; ++j) {
+            const double v = tot[j][col];
+            if (j < seg)
+                run += v;
+            all += v;
         }
+        carry += all;
+#pragma unroll
+        for (int i = 0; i < SCAN_SEG; ++i) {
+            const int b = first + i * step;
+            const bool ok = live && (rev ? b >= 0 : b < NB);
+            if (rev)
+                run += (double)x[i];
+            if (ok)
+                base[(int64_t)b * elems] = (float)run;
+            if (!rev)
+                run += (double)x[i];
+        }
+        __syncthreads();
     }
+    if (live && seg == 0)
+        base[(int64_t)NB * elems] = rev ? 0.0f : (float)carry;
 }
 
 hipError_t launch_block_scan(float *ws, int64_t elems, int NB, int Z, int rev, hipStream_t s)
 {
-    const dim3 grid((unsigned)((elems + 255) / 256), (unsigned)Z);
-    hipLaunchKernelGGL(race_block_scan, grid, dim3(256), 0, s, ws, elems, NB, rev);
+    const dim3 grid((unsigned)((elems + SCAN_COLS - 1) / SCAN_COLS), (unsigned)Z);
+    hipLaunchKernelGGL(race_block_scan, grid, dim3(SCAN_COLS * SCAN_SEGS), 0, s, ws, elems, NB, rev);
     return hipGetLastError();
 }
 

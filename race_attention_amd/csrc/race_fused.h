@@ -653,6 +653,36 @@ RACE_DEV void store_staged(const OutView &o, int b, int h, int st, int t0, int n
     }
 }
 
+// Register buffer for the k, v, q, go rows of the next (sub-chunk, head) step: loads are
+// issued one step ahead and land in LDS at the start of the step that uses them.
+template <class CF>
+struct RowPrefetch {
+    u32x4 k[CF::PF], v[CF::PF], q[CF::PF], g[CF::PF];
+
+    RACE_DEV void load(const ScanParams &P, const Ctx &c, int t0, int hq, bool kv, int tid)
+    {
+        const int nv = min(CF::C, c.t_end - t0);
+        if (kv) {
+            tile_load<CF>(k, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, tid);
+            tile_load<CF>(v, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, tid);
+        }
+        tile_load<CF>(q, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
+        tile_load<CF>(g, row_ptr(P.go, c.b, hq, t0), P.go.st, nv, tid);
+    }
+
+    // after storing step (t0, g): issue the loads of the following step, if any
+    RACE_DEV void advance(const ScanParams &P, const Ctx &c, int t0, int g, int tid)
+    {
+        int g2 = g + 1, t2 = t0;
+        if (g2 == P.G) {
+            g2 = 0;
+            t2 = t0 + CF::C;
+        }
+        if (t2 < c.t_end)
+            load(P, c, t2, c.hk * P.G + g2, g2 == 0, tid);
+    }
+};
+
 // ============================================================================ backward totals
 // Forward-order pass over a block: dq (soft-hash backward of gpQ = gW/(A+eps)) and the
 // block totals of W^T go (into ws2B) and of gA (into ws2A).
@@ -726,6 +756,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     const int G = P.G;
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     int prev_t0 = -1, prev_nv = 0, prev_h = 0;
+    RowPrefetch<CF> pf;
+    pf.load(P, c, c.t_begin, c.hk * G, true, tid);
     f32x4 accI[TPW_A];  // 1/(A+eps), A^T tiles
     float uq[TPW_P][4], pq_[TPW_P][R];
     for (int sc = 0; sc < nsub; ++sc) {
@@ -735,21 +767,15 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
         for (int g = 0; g < G; ++g) {
             const int hq = c.hk * G + g;
             // ---- P0: rows of this (sub-chunk, head) into LDS
-            {
-                u32x4 r[CF::PF];
-                if (g == 0) {
-                    tile_load<CF>(r, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, tid);
-                    tile_store_rows<CF>(&sK[0][0], r, tid);
-                    tile_load<CF>(r, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, tid);
-                    tile_store_rows<CF>(&sV[0][0], r, tid);
-                    tile_store_trans<CF>(&sVt[0][0], r, tid);
-                }
-                tile_load<CF>(r, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
-                tile_store_rows<CF>(&sQ[0][0], r, tid);
-                tile_load<CF>(r, row_ptr(P.go, c.b, hq, t0), P.go.st, nv, tid);
-                tile_store_rows<CF>(&sGO[0][0], r, tid);
-                tile_store_trans<CF>(&sGOt[0][0], r, tid);
+            if (g == 0) {
+                tile_store_rows<CF>(&sK[0][0], pf.k, tid);
+                tile_store_rows<CF>(&sV[0][0], pf.v, tid);
+                tile_store_trans<CF>(&sVt[0][0], pf.v, tid);
             }
+            tile_store_rows<CF>(&sQ[0][0], pf.q, tid);
+            tile_store_rows<CF>(&sGO[0][0], pf.g, tid);
+            tile_store_trans<CF>(&sGOt[0][0], pf.g, tid);
+            pf.advance(P, c, t0, g, tid);
             __syncthreads();
             // ---- P1: soft-hash of k (first head) -> pK^T ; of q -> pQ (kept in registers)
 #pragma unroll
@@ -1028,22 +1054,21 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     zero_lds_bf16(&sPKt[0][0], ST * LDC, tid, NTH);
     zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
 
-    // St^T at the block start (lane: col s, rows d); suffix dS from the block start in
-    // both orientations: accD (lane: col d, rows s) and accDT (lane: col s, rows d).
+    // St^T at the block start (lane: col s, rows d); suffix dS from the block start
+    // (accD, lane: col d, rows s).
     const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
-    f32x4 accS[TPW_S], accD[TPW_S], accDT[TPW_S];
+    f32x4 accS[TPW_S], accD[TPW_S];
     {
         const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
         const float *wB2 = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
 #pragma unroll
         for (int i = 0; i < TPW_S; ++i) {
             const int t = wave + i * NW;
-            accS[i] = accD[i] = accDT[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            accS[i] = accD[i] = f32x4{0.f, 0.f, 0.f, 0.f};
             if (t < CF::NTS * CF::NTD) {
                 const int td = t / CF::NTS, ts = t % CF::NTS;
                 const int d = td * 16 + ((lane >> 4) << 2), s = ts * 16 + (lane & 15);
                 accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + d);
-                accDT[i] = *reinterpret_cast<const f32x4 *>(wB2 + (int64_t)s * P.DPw + d);
                 st_vec4(&sStS[s][d], accS[i]);
                 // accD: rows s2 = ts*16 + 4g + e, col d2 = td*16 + (lane & 15)
                 const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
@@ -1063,8 +1088,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     const int G = P.G;
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     int prev_t0 = -1, prev_nv = 0;
+    RowPrefetch<CF> pf;
+    pf.load(P, c, c.t_begin, c.hk * G, true, tid);
     f32x4 accI[TPW_A], accPK[TPW_A], accV[TPW_O], accGA[TPW_A];
-    float uk[TPW_P][4], pk_[TPW_P][R];
+    float uk[TPW_P][4];
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -1078,21 +1105,15 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
         for (int g = 0; g < G; ++g) {
             const int hq = c.hk * G + g;
             // ---- P0: rows into LDS
-            {
-                u32x4 r[CF::PF];
-                if (g == 0) {
-                    tile_load<CF>(r, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, tid);
-                    tile_store_rows<CF>(&sK[0][0], r, tid);
-                    tile_load<CF>(r, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, tid);
-                    tile_store_rows<CF>(&sV[0][0], r, tid);
-                    tile_store_trans<CF>(&sVt[0][0], r, tid);
-                }
-                tile_load<CF>(r, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
-                tile_store_rows<CF>(&sQ[0][0], r, tid);
-                tile_load<CF>(r, row_ptr(P.go, c.b, hq, t0), P.go.st, nv, tid);
-                tile_store_rows<CF>(&sGO[0][0], r, tid);
-                tile_store_trans<CF>(&sGOt[0][0], r, tid);
+            if (g == 0) {
+                tile_store_rows<CF>(&sK[0][0], pf.k, tid);
+                tile_store_rows<CF>(&sV[0][0], pf.v, tid);
+                tile_store_trans<CF>(&sVt[0][0], pf.v, tid);
             }
+            tile_store_rows<CF>(&sQ[0][0], pf.q, tid);
+            tile_store_rows<CF>(&sGO[0][0], pf.g, tid);
+            tile_store_trans<CF>(&sGOt[0][0], pf.g, tid);
+            pf.advance(P, c, t0, g, tid);
             if (g == 0 && prev_t0 >= 0) {
                 store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
                 store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
@@ -1137,9 +1158,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             uk[i][e] = u[e];
-#pragma unroll
-                        for (int r = 0; r < R; ++r)
-                            pk_[i][r] = p[r];
                     }
                 }
             }
@@ -1239,12 +1257,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                         EngBF16::mma(accD[i], EngBF16::neg(*reinterpret_cast<const bf16x8 *>(pa)),
                                      *reinterpret_cast<const bf16x8 *>(pb));
                     }
-                    {
-                        const __bf16 *pa = &sGOt[0][0] + (td * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
-                        const __bf16 *pb = &sWt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
-                        EngBF16::mma(accDT[i], EngBF16::neg(*reinterpret_cast<const bf16x8 *>(pa)),
-                                     *reinterpret_cast<const bf16x8 *>(pb));
-                    }
                     if (g == G - 1)
                         mma_ab<C, LDC, LDC>(accS[i], &sVt[0][0], td * 16, &sPKt[0][0], ts * 16, lane);
                 }
@@ -1272,10 +1284,11 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     const int t = wave + i * NW;
                     if (t < CF::NTS * CF::NTD) {
                         const int td = t / CF::NTS, ts = t % CF::NTS;
-                        const int d = td * 16 + ((lane >> 4) << 2), s = ts * 16 + (lane & 15);
-                        st_vec4(&sdS[s][d], accDT[i]);
                         const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
                         st_vec4(&sdSt[d2][s2], accD[i]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            sdS[s2 + e][d2] = (__bf16)accD[i][e];
                     }
                 }
                 // gAhat_t = gAhat_end + sum_{tau >= t} gA, gAhat_end = gAhat_start - sum_c gA
@@ -1349,7 +1362,13 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                         for (int e = 0; e < 4; ++e)
                             gp[4 * h + e] = x[e];
                     }
-                    softhash_bwd_ct<KB>(uk[i], pk_[i], gp, P.scale, P.inv_scale, gproj);
+                    float pk[R];
+                    expand_ct<KB>(uk[i], pk);
+                    const bool ok = tok < nv && table < c.Lt;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        pk[r] = ok ? pk[r] : 0.0f;
+                    softhash_bwd_ct<KB>(uk[i], pk, gp, P.scale, P.inv_scale, gproj);
                     bf16x4 w;
 #pragma unroll
                     for (int e = 0; e < 4; ++e)

@@ -7,8 +7,11 @@ namespace race {
 template <int ST, int DP, int KB>
 static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStream_t s)
 {
-    constexpr int NW = FUSED_NW;
-    const dim3 block(NW * 64);
+    // forward kernels: 4 waves (fewer, larger per-wave tile sets measured faster);
+    // backward kernels: 8 waves (two per SIMD to overlap LDS and MFMA latency)
+    constexpr int NW = FUSED_NW_FWD;
+    constexpr int NWB = FUSED_NW_BWD;
+    const dim3 block((k == K_FWD_TOTALS || k == K_FWD_READOUT ? NW : NWB) * 64);
     if (k == K_FWD_TOTALS)
         hipLaunchKernelGGL((race_fused_fwd_totals<ST, DP, KB, NW>), grid, block, 0, s, P);
     else if (k == K_FWD_READOUT && P.out.f32)
@@ -16,15 +19,15 @@ static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStr
     else if (k == K_FWD_READOUT)
         hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, false>), grid, block, 0, s, P);
     else if (k == K_BWD_TOTALS && P.dq.f32)
-        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NW, true>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, true>), grid, block, 0, s, P);
     else if (k == K_BWD_TOTALS)
-        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NW, false>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, false>), grid, block, 0, s, P);
     else if (k == K_BWD_MAIN && P.dk.f32 != P.dv.f32)
         return hipErrorInvalidValue;
     else if (k == K_BWD_MAIN && P.dk.f32)
-        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NW, true>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, true>), grid, block, 0, s, P);
     else if (k == K_BWD_MAIN)
-        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NW, false>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, false>), grid, block, 0, s, P);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -27,7 +27,7 @@ bool qkv_variant_exists(int ST, int DP);
 // fused bf16 forward kernels specialised on the hash bits (race_fused.hip)
 hipError_t launch_fused(ScanKernel k, int ST, int DP, int KB, const ScanParams &P, dim3 grid, hipStream_t s);
 bool fused_variant_exists(int ST, int DP, int KB);
-constexpr int FUSED_NW = 4;
+constexpr int FUSED_NW_FWD = 4, FUSED_NW_BWD = 8;
 bool op_variant_exists(int ST, int DP);
 constexpr int QKV_C = 32, QKV_NW = 4;
 constexpr int OP_C = 16, OP_NW = 4;

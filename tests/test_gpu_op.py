@@ -66,3 +66,8 @@ def test_raw_distribution(dev, L, Kb):
 def test_s256_tiled(dev):
     """S = 256 > the largest bucket tile: exercises the partial-sum reduction."""
     run_case(dev, 2, 700, 16, 4, 64, seed=11)
+
+
+def test_many_blocks(dev):
+    """More blocks than one pass of the block-state scan covers (625 and 834 blocks, ragged)."""
+    run_case(dev, 1, 40000, 4, 4, 64, seed=40000, grad_tol=5e-3, blocks=(0, 48))
