@@ -994,10 +994,37 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
 
 
 // ============================================================================ backward main
+// MFMA operand fragment (row m0 + lane%16, k = k0 + 8*(lane/16) .. +7) from an LDS array
+// stored [m][k] (k contiguous): one 16-byte read.
+RACE_DEV bf16x8 ld_k(const __bf16 *X, int ld, int m0, int k0, int lane)
+{
+    return *reinterpret_cast<const bf16x8 *>(X + (m0 + (lane & 15)) * ld + k0 + (lane >> 4) * 8);
+}
+
+// The same fragment from an LDS array stored [k][m] (m contiguous), with two transposing
+// 64-bit reads (ds_read_b64_tr_b16). Within each 16-lane group, lane i receives element
+// i % 4 of the 8-byte rows read by lanes i/4 + 4e (e = 0..3); so lane s of group g reads
+// row k0 + 8g + s/4 (+4 for the second read) at columns m0 + 4*(s%4) .. +3, and lane i
+// ends up holding column m0 + i of rows k0 + 8g .. k0 + 8g + 7.
+RACE_DEV bf16x8 ld_tr(const __bf16 *X, int ld, int k0, int m0, int lane)
+{
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const int s = lane & 15;
+    const __bf16 *p = X + (k0 + 8 * (lane >> 4) + (s >> 2)) * ld + m0 + 4 * (s & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p + 4 * ld));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 r = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, r);
+}
+
 // Forward-order pass over a block with the suffix states (dS, gAhat) shrinking by each
 // sub-chunk's contribution (exact forward A and St, see race_scan_kernels.h):
-//   gpK^T = gAhat + dS V^T + W^T Mv^T ,   gv^T = dS^T pK^T + go^T Mp^T
-// then dk through the soft-hash backward of k and dv directly.
+//   gpK^T = gAhat + dS V^T + W^T Mg ,   gv^T = dS^T pK^T + go^T Mp^T
+// then dk through the soft-hash backward of k and dv directly. Each matrix is held once in
+// LDS, in the orientation its producer writes with vector stores; operands that need the
+// other orientation are read with ld_tr.
 template <int ST, int DP, int KB, int NW, bool OUT_F32>
 __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams P)
 {
@@ -1006,15 +1033,18 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG, LDF = ST + 4;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
-    // Two LDS regions are shared by arrays with disjoint lifetimes:
-    //   uKQ: k, q rows (load -> projection) and dS^T copy (last head -> gv/gpK update);
-    //   uPW: pQ, W (projection -> Mp) and the dk, dv staging (sub-chunk end -> next load).
+    // LDS regions shared by arrays with disjoint lifetimes:
+    //   uKQ: k, q rows (load -> projection) and dS^T [d][s] (last head -> gpK / gv updates);
+    //   uPW: pQ, W rows (projection -> Mp) and the dk, dv staging (sub-chunk end -> next load);
+    //   uF:  gA^T hi/lo parts as [tau][s] (last head -> suffix scan), then gpK rows in fp32.
     constexpr int SZ_K = C * LDX * 2, SZ_DST = DP * LDS * 2;
     constexpr int SZ_PQ = C * LDS * 2, SZ_O = C * LDO * (int)sizeof(OT);
     constexpr int SZ_KQ = 2 * SZ_K > SZ_DST ? 2 * SZ_K : SZ_DST;
     constexpr int SZ_PW = 2 * SZ_PQ > 2 * SZ_O ? 2 * SZ_PQ : 2 * SZ_O;
+    constexpr int SZ_F = C * LDF * 4 > 2 * SZ_PQ ? C * LDF * 4 : 2 * SZ_PQ;
     __shared__ __align__(16) char uKQ[SZ_KQ];
     __shared__ __align__(16) char uPW[SZ_PW];
+    __shared__ __align__(16) char uF[SZ_F];
     __bf16(*sK)[LDX] = reinterpret_cast<__bf16(*)[LDX]>(uKQ);
     __bf16(*sQ)[LDX] = reinterpret_cast<__bf16(*)[LDX]>(uKQ + SZ_K);
     __bf16(*sdSt)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uKQ);
@@ -1022,22 +1052,18 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     __bf16(*sW)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uPW + SZ_PQ);
     OT(*sOk)[LDO] = reinterpret_cast<OT(*)[LDO]>(uPW);
     OT(*sOv)[LDO] = reinterpret_cast<OT(*)[LDO]>(uPW + SZ_O);
+    float(*sF)[LDF] = reinterpret_cast<float(*)[LDF]>(uF);
+    __bf16(*sGAh)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uF);
+    __bf16(*sGAl)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uF + SZ_PQ);
     __shared__ __align__(16) __bf16 sV[C][LDX];
-    __shared__ __align__(16) __bf16 sVt[DP][LDC];
     __shared__ __align__(16) __bf16 sGO[C][LDX];
-    __shared__ __align__(16) __bf16 sGOt[DP][LDC];
     __shared__ __align__(16) __bf16 sPK[C][LDS];
-    __shared__ __align__(16) __bf16 sPKt[ST][LDC];
-    __shared__ __align__(16) __bf16 sWt[ST][LDC];
-    __shared__ __align__(16) __bf16 sMg[C][LDC];   // Mg^T as [t][tau]
-    __shared__ __align__(16) __bf16 sMv[C][LDC];   // Mg   as [tau][t]
-    __shared__ __align__(16) __bf16 sMp[C][LDC];   // Mp^T as [tau][t]
+    __shared__ __align__(16) __bf16 sMg[C][LDC];   // Mg as [tau][t]
+    __shared__ __align__(16) __bf16 sMp[C][LDC];   // Mp as [tau][t]
     __shared__ __align__(16) __bf16 sStS[ST][LDX];
-    __shared__ __align__(16) __bf16 sdS[ST][LDX];
-    __shared__ __align__(16) float sF[C][LDF];     // gA, then gAhat, then gpK (per token row)
     __shared__ __align__(16) __bf16 sGU[C][LDG];
     __shared__ __align__(16) float sA0[2][ST];
-    __shared__ float sGAe[ST];
+    __shared__ __align__(16) float sGAe[2][ST];
 
     const Ctx c = make_ctx(P, ST);
     const int tid = c.tid, lane = c.lane, wave = c.wave;
@@ -1046,12 +1072,16 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;
     constexpr int TPW_O = (CF::NTD * MTC + NW - 1) / NW;
     constexpr int TPW_M = (MTC * MTC + NW - 1) / NW;
+    // dv tiles live on the last GVW waves, so that the soft-hash backward of k (on the
+    // first NPT waves) and the final dv product run side by side
+    constexpr int GVW = NW - (CF::NPT < NW / 2 ? CF::NPT : NW / 2);
+    constexpr int TPW_V = (CF::NTD * MTC + GVW - 1) / GVW;
+    const int wv = wave - (NW - GVW);
     FusedFrags<CF, DP, TPW_P> fr;
     fr.load(P, c.l0, c.Lt, lane, wave);
     BackFrags<CF, DP, TPW_O> bk;
     bk.load(P, c.l0, c.Lt, lane, wave, MTC);
     zero_lds_bf16(&sPK[0][0], C * LDS, tid, NTH);
-    zero_lds_bf16(&sPKt[0][0], ST * LDC, tid, NTH);
     zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
 
     // St^T at the block start (lane: col s, rows d); suffix dS from the block start
@@ -1070,7 +1100,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 const int d = td * 16 + ((lane >> 4) << 2), s = ts * 16 + (lane & 15);
                 accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + d);
                 st_vec4(&sStS[s][d], accS[i]);
-                // accD: rows s2 = ts*16 + 4g + e, col d2 = td*16 + (lane & 15)
                 const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -1081,7 +1110,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
         const float *wA2 = P.ws2A + slot * P.S_pad + c.s0;
         for (int s = tid; s < ST; s += NTH) {
             sA0[0][s] = wA[s];
-            sGAe[s] = wA2[s];
+            sGAe[0][s] = wA2[s];
         }
     }
 
@@ -1090,7 +1119,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     int prev_t0 = -1, prev_nv = 0;
     RowPrefetch<CF> pf;
     pf.load(P, c, c.t_begin, c.hk * G, true, tid);
-    f32x4 accI[TPW_A], accPK[TPW_A], accV[TPW_O], accGA[TPW_A];
+    f32x4 accI[TPW_A], accPK[TPW_A], accV[TPW_V], accGA[TPW_A];
     float uk[TPW_P][4];
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
@@ -1100,26 +1129,23 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
         for (int i = 0; i < TPW_A; ++i)
             accPK[i] = accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < TPW_O; ++i)
+        for (int i = 0; i < TPW_V; ++i)
             accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         for (int g = 0; g < G; ++g) {
-            const int hq = c.hk * G + g;
-            // ---- P0: rows into LDS
+            // ---- P0: rows into LDS ; previous sub-chunk's dk, dv out
             if (g == 0) {
                 tile_store_rows<CF>(&sK[0][0], pf.k, tid);
                 tile_store_rows<CF>(&sV[0][0], pf.v, tid);
-                tile_store_trans<CF>(&sVt[0][0], pf.v, tid);
             }
             tile_store_rows<CF>(&sQ[0][0], pf.q, tid);
             tile_store_rows<CF>(&sGO[0][0], pf.g, tid);
-            tile_store_trans<CF>(&sGOt[0][0], pf.g, tid);
             pf.advance(P, c, t0, g, tid);
             if (g == 0 && prev_t0 >= 0) {
                 store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
                 store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
             }
             __syncthreads();
-            // ---- P1: soft-hash of k (first head) -> pK, pK^T ; of q -> pQ
+            // ---- P1: soft-hash of k (first head) -> pK ; of q -> pQ   (rows [t][s])
 #pragma unroll
             for (int i = 0; i < TPW_P; ++i) {
                 const int t = wave + i * NW;
@@ -1148,11 +1174,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                                 w[e] = (__bf16)p[4 * h + e];
                             *reinterpret_cast<bf16x4 *>(row + 4 * h) = w;
                         }
-                        if (isk) {
-#pragma unroll
-                            for (int r = 0; r < R; ++r)
-                                sPKt[table * R + r][tok] = (__bf16)p[r];
-                        }
                     }
                     if (isk) {
 #pragma unroll
@@ -1162,7 +1183,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 }
             }
             __syncthreads();
-            // ---- P2: A^T (first head); W^T -> sW, sWt ; Mg^T -> sMg ; Mg -> sMv ; gW^T = St go^T
+            // ---- P2: A^T (first head) ; W -> sW ; gW^T = St go^T ; Mg -> sMg
             f32x4 accW[TPW_A], accG[TPW_A];
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
@@ -1173,8 +1194,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
-                        const __bf16 *pa = &sPKt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
-                        EngBF16::mma(a, *reinterpret_cast<const bf16x8 *>(pa), fr.tri_of(tt));
+                        EngBF16::mma(a, ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
                         if (tt == MTC - 1 && (lane & 15) == 15)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
@@ -1183,10 +1203,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     }
                     const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
+                    for (int e = 0; e < 4; ++e)
                         accW[i][e] = (float)q4[e] * accI[i][e];
-                        sWt[s + e][tok] = (__bf16)accW[i][e];
-                    }
                     st_vec4(&sW[tok][s], accW[i]);
                     mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
                 }
@@ -1195,46 +1213,41 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             for (int i = 0; i < TPW_M; ++i) {
                 const int t = wave + i * NW;
                 if (t < MTC * MTC) {
+                    // Mg[t][tau] = go_t . v_tau (tau <= t): rows t (tile ta), cols tau (tile tb)
                     const int ta = t / MTC, tb = t % MTC;
-                    // Mg^T[tau][t] (rows tau = ta, cols t = tb) -> sMg[t][tau]
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<DP, LDX, LDX>(acc, &sV[0][0], ta * 16, &sGO[0][0], tb * 16, lane);
+                    mma_ab<DP, LDX, LDX>(acc, &sGO[0][0], ta * 16, &sV[0][0], tb * 16, lane);
                     const int r0 = ta * 16 + ((lane >> 4) << 2), c0 = tb * 16 + (lane & 15);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (r0 + e > c0)
+                        if (c0 > r0 + e)
                             acc[e] = 0.0f;
                     st_vec4(&sMg[c0][r0], acc);
-                    // Mg[t][tau] (rows t = ta, cols tau = tb) -> sMv[tau][t]
-                    f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<DP, LDX, LDX>(acc2, &sGO[0][0], ta * 16, &sV[0][0], tb * 16, lane);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (c0 > r0 + e)
-                            acc2[e] = 0.0f;
-                    st_vec4(&sMv[c0][r0], acc2);
                 }
             }
             __syncthreads();
-            // ---- P3: gW^T += pK^T Mg^T ; gA^T ; gpK^T += W^T Mv^T ; Mp^T -> sMp ;
-            //          dS, dS^T -= W^T go ; St^T += V^T pK (last head)
+            // ---- P3: gW^T += pK^T Mg^T ; gA^T ; gpK^T += W^T Mg ; Mp -> sMp ;
+            //          dS -= W^T go ; St^T += V^T pK (last head) ; gA^T hi/lo -> [tau][s]
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 const int t = wave + i * NW;
                 if (t < CF::NTS * MTC) {
                     const int ts = t / MTC, tt = t % MTC;
-                    mma_ab<C, LDC, LDC>(accG[i], &sPKt[0][0], ts * 16, &sMg[0][0], tt * 16, lane);
+                    EngBF16::mma(accG[i], ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane),
+                                 ld_tr(&sMg[0][0], LDC, 0, tt * 16, lane));
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         accGA[i][e] -= accG[i][e] * accI[i][e] * accW[i][e];
-                    mma_ab<C, LDC, LDC>(accPK[i], &sWt[0][0], ts * 16, &sMv[0][0], tt * 16, lane);
+                    EngBF16::mma(accPK[i], ld_tr(&sW[0][0], LDS, 0, ts * 16, lane),
+                                 ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
                 }
             }
 #pragma unroll
             for (int i = 0; i < TPW_M; ++i) {
                 const int t = wave + i * NW;
                 if (t < MTC * MTC) {
-                    const int ta = t / MTC, tb = t % MTC;  // rows t = ta, cols tau = tb
+                    // Mp[tau][t] = pK_tau . W_t (t >= tau): rows t (tile ta), cols tau (tile tb)
+                    const int ta = t / MTC, tb = t % MTC;
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
                     mma_ab<ST, LDS, LDS>(acc, &sW[0][0], ta * 16, &sPK[0][0], tb * 16, lane);
                     const int r0 = ta * 16 + ((lane >> 4) << 2), c0 = tb * 16 + (lane & 15);
@@ -1251,32 +1264,40 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 if (t < CF::NTS * CF::NTD) {
                     const int td = t / CF::NTS, ts = t % CF::NTS;
                     // dS[s][d] -= sum_t W[t][s] go[t][d]   (accD: rows s of tile ts, cols d of td)
-                    {
-                        const __bf16 *pa = &sWt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
-                        const __bf16 *pb = &sGOt[0][0] + (td * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
-                        EngBF16::mma(accD[i], EngBF16::neg(*reinterpret_cast<const bf16x8 *>(pa)),
-                                     *reinterpret_cast<const bf16x8 *>(pb));
-                    }
+                    EngBF16::mma(accD[i], EngBF16::neg(ld_tr(&sW[0][0], LDS, 0, ts * 16, lane)),
+                                 ld_tr(&sGO[0][0], LDX, 0, td * 16, lane));
+                    // St^T[d][s] += sum_t V[t][d] pK[t][s]
                     if (g == G - 1)
-                        mma_ab<C, LDC, LDC>(accS[i], &sVt[0][0], td * 16, &sPKt[0][0], ts * 16, lane);
+                        EngBF16::mma(accS[i], ld_tr(&sV[0][0], LDX, 0, td * 16, lane),
+                                     ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane));
                 }
             }
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 const int t = wave + i * NW;
                 if (t < CF::NTS * MTC && g == G - 1) {
+                    // gA^T as a bf16 hi/lo pair, rows [tau][s], for the suffix-scan MFMA
                     const int ts = t / MTC, tt = t % MTC;
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                    *reinterpret_cast<f32x4 *>(&sF[tok][s]) = accGA[i];
+                    f32x4 lo;
+                    bf16x4 hi;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        hi[e] = (__bf16)accGA[i][e];
+                        lo[e] = accGA[i][e] - (float)hi[e];
+                    }
+                    *reinterpret_cast<bf16x4 *>(&sGAh[tok][s]) = hi;
+                    st_vec4(&sGAl[tok][s], lo);
                 }
             }
             __syncthreads();
-            // ---- P4: gv^T += go^T Mp^T ; (last head) dS copies, gAhat scan
+            // ---- P4: gv^T += go^T Mp^T ; (last head) dS^T -> sdSt, gAhat scan
 #pragma unroll
-            for (int i = 0; i < TPW_O; ++i) {
-                const int t = wave + i * NW;
-                if (t < CF::NTD * MTC)
-                    mma_ab<C, LDC, LDC>(accV[i], &sGOt[0][0], (t / MTC) * 16, &sMp[0][0], (t % MTC) * 16, lane);
+            for (int i = 0; i < TPW_V; ++i) {
+                const int t = wv + i * GVW;
+                if (wv >= 0 && t < CF::NTD * MTC)
+                    EngBF16::mma(accV[i], ld_tr(&sGO[0][0], LDX, 0, (t / MTC) * 16, lane),
+                                 ld_k(&sMp[0][0], LDC, (t % MTC) * 16, 0, lane));
             }
             if (g == G - 1) {
 #pragma unroll
@@ -1286,55 +1307,52 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                         const int td = t / CF::NTS, ts = t % CF::NTS;
                         const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
                         st_vec4(&sdSt[d2][s2], accD[i]);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            sdS[s2 + e][d2] = (__bf16)accD[i][e];
                     }
                 }
-                // gAhat_t = gAhat_end + sum_{tau >= t} gA, gAhat_end = gAhat_start - sum_c gA
-                for (int s = tid; s < ST; s += NTH) {
-                    float tot = 0.0f;
-                    for (int t = 0; t < C; ++t)
-                        tot += sF[t][s];
-                    float run = sGAe[s] - tot;
-                    const float end = run;
-                    for (int t = C - 1; t >= 0; --t) {
-                        run += sF[t][s];
-                        sF[t][s] = run;
+                // gAhat_t = gAhat_start - sum_{tau < t} gA_tau: the inclusive sum runs on the
+                // MFMA (hi + lo parts, ~16-bit mantissa per term, fp32 accumulation) and the own
+                // term is added back in fp32; the sub-chunk total seeds the next sub-chunk.
+#pragma unroll
+                for (int i = 0; i < TPW_A; ++i) {
+                    const int t = wave + i * NW;
+                    if (t < CF::NTS * MTC) {
+                        const int ts = t / MTC, tt = t % MTC;
+                        const int s = ts * 16 + ((lane >> 4) << 2);
+                        f32x4 inc = {0.f, 0.f, 0.f, 0.f};
+                        const bf16x8 tri = fr.tri_of(tt);
+                        EngBF16::mma(inc, ld_tr(&sGAh[0][0], LDS, 0, ts * 16, lane), tri);
+                        EngBF16::mma(inc, ld_tr(&sGAl[0][0], LDS, 0, ts * 16, lane), tri);
+                        const f32x4 g0 = *reinterpret_cast<const f32x4 *>(&sGAe[cur][s]);
+                        f32x4 gend;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            gend[e] = g0[e] - inc[e];
+                            accGA[i][e] += gend[e];
+                        }
+                        if (tt == MTC - 1 && (lane & 15) == 15)
+                            *reinterpret_cast<f32x4 *>(&sGAe[nxt][s]) = gend;
                     }
-                    sGAe[s] = end;
                 }
             }
             if (g + 1 < G)
                 __syncthreads();
         }
         __syncthreads();
-        // ---- P5: gpK^T += dS V^T + gAhat -> sF ; gv^T += dS^T pK^T -> sOv ; St -> sStS
+        // ---- P5: gpK^T += dS V^T + gAhat -> sF ; St -> sStS
 #pragma unroll
         for (int i = 0; i < TPW_A; ++i) {
             const int t = wave + i * NW;
             if (t < CF::NTS * MTC) {
                 const int ts = t / MTC, tt = t % MTC;
                 const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                mma_ab<DP, LDX, LDX>(accPK[i], &sdS[0][0], ts * 16, &sV[0][0], tt * 16, lane);
-                const f32x4 gh = *reinterpret_cast<const f32x4 *>(&sF[tok][s]);
+#pragma unroll
+                for (int kd = 0; kd < DP; kd += 32)
+                    EngBF16::mma(accPK[i], ld_tr(&sdSt[0][0], LDS, kd, ts * 16, lane),
+                                 ld_k(&sV[0][0], LDX, tt * 16, kd, lane));
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    accPK[i][e] += gh[e];
+                    accPK[i][e] += accGA[i][e];
                 *reinterpret_cast<f32x4 *>(&sF[tok][s]) = accPK[i];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < TPW_O; ++i) {
-            const int t = wave + i * NW;
-            if (t < CF::NTD * MTC) {
-                const int td = t / MTC, tt = t % MTC;
-                mma_ab<ST, LDS, LDS>(accV[i], &sdSt[0][0], td * 16, &sPK[0][0], tt * 16, lane);
-                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                if constexpr (OUT_F32)
-                    *reinterpret_cast<f32x4 *>(&sOv[tok][d]) = accV[i];
-                else
-                    st_vec4(&sOv[tok][d], accV[i]);
             }
         }
 #pragma unroll
@@ -1346,7 +1364,20 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             }
         }
         __syncthreads();
-        // ---- P6: soft-hash backward of k -> sGU
+        // ---- P6: soft-hash backward of k -> sGU ; gv^T += dS^T pK^T -> sOv
+#pragma unroll
+        for (int i = 0; i < TPW_V; ++i) {
+            const int t = wv + i * GVW;
+            if (wv >= 0 && t < CF::NTD * MTC) {
+                const int td = t / MTC, tt = t % MTC;
+                mma_ab<ST, LDS, LDS>(accV[i], &sdSt[0][0], td * 16, &sPK[0][0], tt * 16, lane);
+                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sOv[tok][d]) = accV[i];
+                else
+                    st_vec4(&sOv[tok][d], accV[i]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < TPW_P; ++i) {
             const int t = wave + i * NW;
