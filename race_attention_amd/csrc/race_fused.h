@@ -154,6 +154,31 @@ RACE_DEV void st_vec4(__bf16 *p, const f32x4 &v)
     *reinterpret_cast<bf16x4 *>(p) = w;
 }
 
+// MFMA operand fragment (row m0 + lane%16, k = k0 + 8*(lane/16) .. +7) from an LDS array
+// stored [m][k] (k contiguous): one 16-byte read.
+RACE_DEV bf16x8 ld_k(const __bf16 *X, int ld, int m0, int k0, int lane)
+{
+    return *reinterpret_cast<const bf16x8 *>(X + (m0 + (lane & 15)) * ld + k0 + (lane >> 4) * 8);
+}
+
+// The same fragment from an LDS array stored [k][m] (m contiguous), with two transposing
+// 64-bit reads (ds_read_b64_tr_b16). Within each 16-lane group, lane i receives element
+// i % 4 of the 8-byte rows read by lanes i/4 + 4e (e = 0..3); so lane s of group g reads
+// row k0 + 8g + s/4 (+4 for the second read) at columns m0 + 4*(s%4) .. +3, and lane i
+// ends up holding column m0 + i of rows k0 + 8g .. k0 + 8g + 7.
+RACE_DEV bf16x8 ld_tr(const __bf16 *X, int ld, int k0, int m0, int lane)
+{
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const int s = lane & 15;
+    const __bf16 *p = X + (k0 + 8 * (lane >> 4) + (s >> 2)) * ld + m0 + 4 * (s & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p + 4 * ld));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 r = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, r);
+}
+
 // 16-byte chunk loads of one C x DP bf16 token tile (rows t0.., zero beyond nv).
 template <class CF>
 RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int nv, int tid)
@@ -181,23 +206,6 @@ RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int tid)
     }
 }
 
-template <class CF>
-RACE_DEV void tile_store_trans(__bf16 *dstT, const u32x4 (&r)[CF::PF], int tid)
-{
-    constexpr int CH = CF::CHUNKS / CF::C;
-#pragma unroll
-    for (int i = 0; i < CF::PF; ++i) {
-        const int idx = tid + i * CF::NTH;
-        if (idx < CF::CHUNKS) {
-            const int row = idx / CH, c = idx % CH;
-            const bf16x8 x = __builtin_bit_cast(bf16x8, r[i]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                dstT[(c * 8 + e) * CF::LDC + row] = x[e];
-        }
-    }
-}
-
 RACE_DEV const __bf16 *row_ptr(const View &v, int b, int h, int t)
 {
     return reinterpret_cast<const __bf16 *>(v.p) + (b * v.sb + h * v.sh + (int64_t)t * v.st);
@@ -210,8 +218,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     using CF = FCfg<ST, DP, KB, NW>;
     constexpr int C = CF::C, NTH = CF::NTH, R = CF::R;
     __shared__ __align__(16) __bf16 sK[C][CF::LDX];
-    __shared__ __align__(16) __bf16 sVt[DP][CF::LDC];
-    __shared__ __align__(16) __bf16 sPKt[ST][CF::LDC];
+    __shared__ __align__(16) __bf16 sV[C][CF::LDX];
+    __shared__ __align__(16) __bf16 sPK[C][CF::LDS];  // rows [t][s]
 
     const Ctx c = make_ctx(P, ST);
     const int tid = c.tid, lane = c.lane, wave = c.wave;
@@ -237,7 +245,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, min(C, c.t_end - c.t_begin), tid);
     tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, min(C, c.t_end - c.t_begin), tid);
     tile_store_rows<CF>(&sK[0][0], pk, tid);
-    tile_store_trans<CF>(&sVt[0][0], pv, tid);
+    tile_store_rows<CF>(&sV[0][0], pv, tid);
     __syncthreads();
 
     for (int sc = 0; sc < nsub; ++sc) {
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
             tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, min(C, c.t_end - t1), tid);
             tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, t1), P.v.st, min(C, c.t_end - t1), tid);
         }
-        // soft-hash of k -> pK^T
+        // soft-hash of k -> pK rows
 #pragma unroll
         for (int i = 0; i < TPW_P; ++i) {
             const int t = wave + i * NW;
@@ -262,9 +270,16 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
                 expand_ct<KB>(u, p);
                 const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                 const bool ok = tok < nv && table < c.Lt;
+                if (table < CF::LT) {
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    sPKt[table * R + r][tok] = (__bf16)(ok ? p[r] : 0.0f);
+                    for (int h = 0; h < R / 4; ++h) {
+                        bf16x4 w;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            w[e] = (__bf16)(ok ? p[4 * h + e] : 0.0f);
+                        *reinterpret_cast<bf16x4 *>(&sPK[tok][table * R + 4 * h]) = w;
+                    }
+                }
             }
         }
         __syncthreads();
@@ -272,20 +287,19 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
         for (int i = 0; i < TPW_S; ++i) {
             const int t = wave + i * NW;
             if (t < CF::NTS * CF::NTD)
-                mma_ab<C, CF::LDC, CF::LDC>(accS[i], &sPKt[0][0], (t / CF::NTD) * 16, &sVt[0][0], (t % CF::NTD) * 16, lane);
+                EngBF16::mma(accS[i], ld_tr(&sPK[0][0], CF::LDS, 0, (t / CF::NTD) * 16, lane),
+                             ld_tr(&sV[0][0], CF::LDX, 0, (t % CF::NTD) * 16, lane));
         }
 #pragma unroll
         for (int i = 0; i < TPW_A; ++i) {
             const int tn = wave + i * NW;
-            if (tn < CF::NTS) {
-                const __bf16 *pb = &sPKt[0][0] + (tn * 16 + (lane & 15)) * CF::LDC + (lane >> 4) * 8;
-                EngBF16::mma(accA[i], ones, *reinterpret_cast<const bf16x8 *>(pb));
-            }
+            if (tn < CF::NTS)
+                EngBF16::mma(accA[i], ones, ld_tr(&sPK[0][0], CF::LDS, 0, tn * 16, lane));
         }
         __syncthreads();
         if (sc + 1 < nsub) {
             tile_store_rows<CF>(&sK[0][0], pk, tid);
-            tile_store_trans<CF>(&sVt[0][0], pv, tid);
+            tile_store_rows<CF>(&sV[0][0], pv, tid);
         }
         __syncthreads();
     }
@@ -322,9 +336,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
     __shared__ __align__(16) __bf16 sK[C][LDX];
     __shared__ __align__(16) __bf16 sQ[C][LDX];
-    __shared__ __align__(16) __bf16 sVt[2][DP][LDC];
-    __shared__ __align__(16) __bf16 sPK[C][LDS];
-    __shared__ __align__(16) __bf16 sPKt[ST][LDC];
+    __shared__ __align__(16) __bf16 sV[2][C][LDX];   // v rows, double buffered
+    __shared__ __align__(16) __bf16 sPK[C][LDS];     // rows [t][s]
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
     __shared__ __align__(16) __bf16 sW[C][LDS];
     __shared__ __align__(16) __bf16 sStT[DP][LDS];
@@ -338,7 +351,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
     FusedFrags<CF, DP, TPW_P0> fr;
     fr.load(P, c.l0, c.Lt, lane, wave);
     zero_lds_bf16(&sPK[0][0], C * LDS, tid, NTH);
-    zero_lds_bf16(&sPKt[0][0], ST * LDC, tid, NTH);
     zero_lds_bf16(&sPQ[0][0], C * LDS, tid, NTH);
 
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;  // state tiles [ST x DP]
@@ -380,7 +392,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
         tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, nv0, tid);
         tile_store_rows<CF>(&sK[0][0], pk, tid);
         tile_store_rows<CF>(&sQ[0][0], pq, tid);
-        tile_store_trans<CF>(&sVt[0][0][0], pv, tid);
+        tile_store_rows<CF>(&sV[0][0][0], pv, tid);
     }
     __syncthreads();
 
@@ -441,11 +453,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
                         } else {
                             *reinterpret_cast<bf16x4 *>(row) = v4;
                         }
-                        if (isk) {
-#pragma unroll
-                            for (int r = 0; r < R; ++r)
-                                sPKt[table * R + r][tok] = (R >= 8) ? v8[r / 8][r % 8] : v4[r % 4];
-                        }
                     }
                 }
             }
@@ -473,8 +480,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
-                        const __bf16 *pa = &sPKt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
-                        EngBF16::mma(a, *reinterpret_cast<const bf16x8 *>(pa), fr.tri_of(tt));
+                        EngBF16::mma(a, ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
                         if (tt == MTC - 1 && (lane & 15) == 15)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
@@ -519,8 +525,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
                 for (int i = 0; i < TPW_S; ++i) {
                     const int t = wave + i * NW;
                     if (t < CF::NTS * CF::NTD)
-                        mma_ab<C, LDC, LDC>(accS[i], &sPKt[0][0], (t / CF::NTD) * 16, &sVt[cur][0][0],
-                                            (t % CF::NTD) * 16, lane);
+                        EngBF16::mma(accS[i], ld_tr(&sPK[0][0], LDS, 0, (t / CF::NTD) * 16, lane),
+                                     ld_tr(&sV[cur][0][0], LDX, 0, (t % CF::NTD) * 16, lane));
                 }
             }
             __syncthreads();
@@ -530,7 +536,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
                 const int t = wave + i * NW;
                 if (t < CF::NTD * MTC) {
                     const int td = t / MTC, tt = t % MTC;
-                    mma_ab<C, LDC, LDC>(accO[i], &sVt[cur][0][0], td * 16, &sPm[0][0], tt * 16, lane);
+                    EngBF16::mma(accO[i], ld_tr(&sV[cur][0][0], LDX, 0, td * 16, lane),
+                                 ld_k(&sPm[0][0], LDC, tt * 16, 0, lane));
                     const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if constexpr (OUT_F32)
                         *reinterpret_cast<f32x4 *>(&sO[tok][d]) = accO[i];
@@ -552,7 +559,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
                 }
                 if (more) {
                     tile_store_rows<CF>(&sK[0][0], pk, tid);
-                    tile_store_trans<CF>(&sVt[nxt][0][0], pv, tid);
+                    tile_store_rows<CF>(&sV[nxt][0][0], pv, tid);
                     if (G == 1)
                         tile_store_rows<CF>(&sQ[0][0], pq, tid);
                     else {
@@ -697,13 +704,11 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     __shared__ __align__(16) __bf16 sK[C][LDX];
     __shared__ __align__(16) __bf16 sQ[C][LDX];
     __shared__ __align__(16) __bf16 sV[C][LDX];
-    __shared__ __align__(16) __bf16 sVt[DP][LDC];
     __shared__ __align__(16) __bf16 sGO[C][LDX];
-    __shared__ __align__(16) __bf16 sGOt[DP][LDC];
-    __shared__ __align__(16) __bf16 sPKt[ST][LDC];
+    __shared__ __align__(16) __bf16 sPK[C][LDS];   // rows [t][s]
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
-    __shared__ __align__(16) __bf16 sWt[ST][LDC];
-    __shared__ __align__(16) __bf16 sMg[C][LDC];
+    __shared__ __align__(16) __bf16 sW[C][LDS];
+    __shared__ __align__(16) __bf16 sMg[C][LDC];   // Mg as [t][tau]
     __shared__ __align__(16) __bf16 sStS[ST][LDX];
     __shared__ __align__(16) float sGP[C][ST + 4];
     __shared__ __align__(16) __bf16 sGU[C][LDG];
@@ -722,7 +727,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     fr.load(P, c.l0, c.Lt, lane, wave);
     BackFrags<CF, DP, TPW_O> bk;
     bk.load(P, c.l0, c.Lt, lane, wave, MTC);
-    zero_lds_bf16(&sPKt[0][0], ST * LDC, tid, NTH);
+    zero_lds_bf16(&sPK[0][0], C * LDS, tid, NTH);
     zero_lds_bf16(&sPQ[0][0], C * LDS, tid, NTH);
     zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
     for (int i = tid; i < ST; i += NTH)
@@ -770,11 +775,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             if (g == 0) {
                 tile_store_rows<CF>(&sK[0][0], pf.k, tid);
                 tile_store_rows<CF>(&sV[0][0], pf.v, tid);
-                tile_store_trans<CF>(&sVt[0][0], pf.v, tid);
             }
             tile_store_rows<CF>(&sQ[0][0], pf.q, tid);
             tile_store_rows<CF>(&sGO[0][0], pf.g, tid);
-            tile_store_trans<CF>(&sGOt[0][0], pf.g, tid);
             pf.advance(P, c, t0, g, tid);
             __syncthreads();
             // ---- P1: soft-hash of k (first head) -> pK^T ; of q -> pQ (kept in registers)
@@ -797,19 +800,14 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     for (int r = 0; r < R; ++r)
                         p[r] = ok ? p[r] : 0.0f;
                     if (table < CF::LT) {
-                        if (isk) {
+                        __bf16 *row = isk ? &sPK[tok][table * R] : &sPQ[tok][table * R];
 #pragma unroll
-                            for (int r = 0; r < R; ++r)
-                                sPKt[table * R + r][tok] = (__bf16)p[r];
-                        } else {
+                        for (int h = 0; h < R / 4; ++h) {
+                            bf16x4 w;
 #pragma unroll
-                            for (int h = 0; h < R / 4; ++h) {
-                                bf16x4 w;
-#pragma unroll
-                                for (int e = 0; e < 4; ++e)
-                                    w[e] = (__bf16)p[4 * h + e];
-                                *reinterpret_cast<bf16x4 *>(&sPQ[tok][table * R + 4 * h]) = w;
-                            }
+                            for (int e = 0; e < 4; ++e)
+                                w[e] = (__bf16)p[4 * h + e];
+                            *reinterpret_cast<bf16x4 *>(row + 4 * h) = w;
                         }
                     }
 #pragma unroll
@@ -823,7 +821,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             if (prev_t0 >= 0)
                 store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
             __syncthreads();
-            // ---- P2: A^T scan (first head) -> 1/(A+eps); W^T -> sWt ; Mg^T -> sMg ; gW^T = St go^T
+            // ---- P2: A^T scan (first head) -> 1/(A+eps); W -> sW ; Mg -> sMg ; gW^T = St go^T
             f32x4 accW[TPW_A], accG[TPW_A];
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
@@ -835,8 +833,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
-                        const __bf16 *pa = &sPKt[0][0] + (ts * 16 + (lane & 15)) * LDC + (lane >> 4) * 8;
-                        EngBF16::mma(a, *reinterpret_cast<const bf16x8 *>(pa), fr.tri_of(tt));
+                        EngBF16::mma(a, ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
                         if (tt == MTC - 1 && (lane & 15) == 15)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
@@ -845,10 +842,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     }
                     const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
+                    for (int e = 0; e < 4; ++e)
                         accW[i][e] = (float)q4[e] * accI[i][e];
-                        sWt[s + e][tok] = (__bf16)accW[i][e];
-                    }
+                    st_vec4(&sW[tok][s], accW[i]);
                     mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
                 }
             }
@@ -875,7 +871,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                 if (t < CF::NTS * MTC) {
                     const int ts = t / MTC, tt = t % MTC;
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                    mma_ab<C, LDC, LDC>(accG[i], &sPKt[0][0], ts * 16, &sMg[0][0], tt * 16, lane);
+                    EngBF16::mma(accG[i], ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane),
+                                 ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
                     f32x4 gpq;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -890,9 +887,11 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                 const int t = wave + i * NW;
                 if (t < CF::NTS * CF::NTD) {
                     const int td = t / CF::NTS, ts = t % CF::NTS;
-                    mma_ab<C, LDC, LDC>(accD[i], &sGOt[0][0], td * 16, &sWt[0][0], ts * 16, lane);
+                    EngBF16::mma(accD[i], ld_tr(&sGO[0][0], LDX, 0, td * 16, lane),
+                                 ld_tr(&sW[0][0], LDS, 0, ts * 16, lane));
                     if (g == G - 1)
-                        mma_ab<C, LDC, LDC>(accS[i], &sVt[0][0], td * 16, &sPKt[0][0], ts * 16, lane);
+                        EngBF16::mma(accS[i], ld_tr(&sV[0][0], LDX, 0, td * 16, lane),
+                                     ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane));
                 }
             }
             __syncthreads();
@@ -994,31 +993,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
 
 
 // ============================================================================ backward main
-// MFMA operand fragment (row m0 + lane%16, k = k0 + 8*(lane/16) .. +7) from an LDS array
-// stored [m][k] (k contiguous): one 16-byte read.
-RACE_DEV bf16x8 ld_k(const __bf16 *X, int ld, int m0, int k0, int lane)
-{
-    return *reinterpret_cast<const bf16x8 *>(X + (m0 + (lane & 15)) * ld + k0 + (lane >> 4) * 8);
-}
-
-// The same fragment from an LDS array stored [k][m] (m contiguous), with two transposing
-// 64-bit reads (ds_read_b64_tr_b16). Within each 16-lane group, lane i receives element
-// i % 4 of the 8-byte rows read by lanes i/4 + 4e (e = 0..3); so lane s of group g reads
-// row k0 + 8g + s/4 (+4 for the second read) at columns m0 + 4*(s%4) .. +3, and lane i
-// ends up holding column m0 + i of rows k0 + 8g .. k0 + 8g + 7.
-RACE_DEV bf16x8 ld_tr(const __bf16 *X, int ld, int k0, int m0, int lane)
-{
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-    const int s = lane & 15;
-    const __bf16 *p = X + (k0 + 8 * (lane >> 4) + (s >> 2)) * ld + m0 + 4 * (s & 3);
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p + 4 * ld));
-    typedef short s16x8 __attribute__((ext_vector_type(8)));
-    const s16x8 r = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    return __builtin_bit_cast(bf16x8, r);
-}
-
 // Forward-order pass over a block with the suffix states (dS, gAhat) shrinking by each
 // sub-chunk's contribution (exact forward A and St, see race_scan_kernels.h):
 //   gpK^T = gAhat + dS V^T + W^T Mg ,   gv^T = dS^T pK^T + go^T Mp^T
