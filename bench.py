@@ -44,6 +44,14 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-T", type=int, default=8192)
+    ap.add_argument("--sweep", action="store_true",
+                    help="cfg3 long-context sweep instead of the headline line: tokens/s for "
+                         "T = 2^20 .. --sweep-max, GPU and CPU-path memory per token and the "
+                         "largest T each fits")
+    ap.add_argument("--sweep-max", type=int, default=1 << 24)
+    ap.add_argument("--workload", default="cfg3", choices=["cfg3", "cfg5"],
+                    help="cfg5: Llama-3.2-1B-shaped hybrid LM (random init), B=8, T=8192 prefill "
+                         "forward+backward, then 256-token greedy decode through the RACE state cache")
     return ap.parse_args()
 
 
@@ -80,6 +88,12 @@ def main():
     from race_attention_amd import RaceDecodeState, build_planes_protos, race_causal_attention
     from race_attention_amd import _lib
 
+    if args.sweep:
+        print(json.dumps(bench_sweep(torch, args, build_planes_protos, race_causal_attention)))
+        return
+    if args.workload == "cfg5":
+        print(json.dumps(bench_hybrid(torch, args)))
+        return
     dev = torch.device("cuda:0")
     B, H, T, D, L, K = args.B, args.H, args.T, 64, args.L, 4
     S = L << K
@@ -162,6 +176,117 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = bench_cpu(torch, args.cpu_T, H, D, L, K)
     print(json.dumps(result))
+
+
+def bench_sweep(torch, args, build_planes_protos, race_causal_attention):
+    """cfg3 over T = 2^20 .. sweep_max (B=1, H=4, D=64, L=8, K=4): tokens/s of one layer
+    fwd+bwd and peak HBM per token; the largest T that fits in this GPU's memory at that
+    rate; the CPU path's (oracle/race_cpu_port.py) peak host memory per token at a small
+    T and the largest T the host memory would hold."""
+    import resource
+    dev = torch.device("cuda:0")
+    B, H, D, L, K = 1, args.H, 64, args.L, 4
+    planes_T, _ = build_planes_protos(D, K, L, 1, device=dev, seed=0)
+    rows = []
+    T = 1 << 20
+    per_tok = None
+    while T <= args.sweep_max:
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        g = torch.Generator(device=dev).manual_seed(1)
+        std = 1.0 / math.sqrt(D)
+        q, k, v = ((torch.randn(B, H, T, D, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(True)
+                   for _ in range(3))
+        go = torch.randn(B, H, T, D, generator=g, device=dev).to(torch.bfloat16)
+
+        def step():
+            q.grad = k.grad = v.grad = None
+            race_causal_attention(q, k, v, planes_T, L, K).backward(go)
+
+        step()
+        torch.cuda.synchronize()
+        reps = 3
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / reps * 1e3
+        peak = torch.cuda.max_memory_allocated(dev) - base
+        per_tok = peak / (B * T)
+        rows.append({"T": T, "ms_per_step": round(ms, 3), "tokens_per_s": round(B * T / (ms / 1e3), 1),
+                     "peak_hbm_bytes": peak, "hbm_bytes_per_token": round(per_tok, 1)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        del q, k, v, go
+        T *= 2
+    total = torch.cuda.get_device_properties(dev).total_memory
+    gpu_max_T = int(total // per_tok)
+    # CPU path: peak resident memory of one layer fwd+bwd at a small T
+    from oracle import race_cpu_port
+    from oracle import race_oracle as orc
+    planes_c, protos_c = orc.build_planes_protos(D, K, L, seed=0)
+    Tc = args.cpu_T
+    rss0 = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss * 1024
+    gc = torch.Generator().manual_seed(1)
+    qc, kc, vc = ((torch.randn(1, H, Tc, D, generator=gc) / math.sqrt(D)).requires_grad_(True) for _ in range(3))
+    race_cpu_port.race_layer_cpu(qc, kc, vc, planes_c, protos_c, L, K).backward(torch.randn(1, H, Tc, D, generator=gc))
+    rss1 = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss * 1024
+    cpu_per_tok = max(rss1 - rss0, 1) / Tc
+    host = os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES")
+    return {"workload": "cfg3 long-context sweep (one layer fwd+bwd, B=1, H=4, D=64, L=8, K=4, bf16)",
+            "sweep": rows, "gpu_total_bytes": total, "gpu_max_T_estimate": gpu_max_T,
+            "cpu_path": {"T": Tc, "peak_rss_growth_bytes": rss1 - rss0, "bytes_per_token": round(cpu_per_tok, 1),
+                         "host_bytes": host, "cpu_max_T_estimate": int(host // cpu_per_tok)}}
+
+
+def bench_hybrid(torch, args, B=8, T=8192, n_new=256):
+    """cfg5: HybridLM (16 layers, hidden 2048, 32/8 heads of 64, SwiGLU 8192, vocab 128256,
+    RACE L=8 K=4), bf16 random-init weights, uniform synthetic token ids (seed 1).
+    prefill: forward + cross-entropy backward over B x T tokens; decode: prefill the
+    RACE state cache with the B x T prompt, then n_new greedy tokens, one fused decode
+    kernel per layer per token."""
+    from race_attention_amd.hybrid import HybridConfig, HybridLM
+    dev = torch.device("cuda:0")
+    cfg = HybridConfig()
+    model = HybridLM(cfg).to(dev).init_weights(seed=0)
+    g = torch.Generator(device=dev).manual_seed(1)
+    idx = torch.randint(0, cfg.vocab_size, (B, T + 1), generator=g, device=dev)
+
+    def train_step():
+        model.zero_grad(set_to_none=True)
+        model(idx[:, :-1], targets=idx[:, 1:]).backward()
+
+    for _ in range(max(1, args.warmup)):
+        train_step()
+    torch.cuda.synchronize()
+    steps = max(1, min(args.steps, 3))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        train_step()
+    torch.cuda.synchronize()
+    train_s = (time.perf_counter() - t0) / steps
+    model.zero_grad(set_to_none=True)
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        cache = model.make_cache(B)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits = model(idx[:, :T], cache)[:, -1]
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for i in range(n_new):
+            nxt = logits.argmax(-1, keepdim=True)
+            logits = model(nxt, cache)[:, -1]
+        torch.cuda.synchronize()
+        decode_s = time.perf_counter() - t0
+    return {"metric": "cfg5 hybrid LM tokens/sec", "workload": "cfg5", "B": B, "T": T, "params": sum(
+                p.numel() for p in model.parameters()),
+            "train_fwd_bwd": {"value": round(B * T / train_s, 1), "unit": "tokens/s", "seconds": round(train_s, 4)},
+            "prefill_fwd": {"value": round(B * T / prefill_s, 1), "unit": "tokens/s", "seconds": round(prefill_s, 4)},
+            "greedy_decode": {"value": round(B * n_new / decode_s, 1), "unit": "tokens/s", "steps": n_new,
+                              "ms_per_token_step": round(decode_s / n_new * 1e3, 3)},
+            "dtype": "bf16", "data": "synthetic uniform token ids, random-init weights"}
 
 
 def bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, steps):
