@@ -72,6 +72,15 @@ int race_soft_hash_bwd(const race_hash_shape *sh, race_tensor x, int x_dtype,
                        const float *planes_T, const float *gprobs, race_tensor dx,
                        race_stream stream);
 
+/* As race_soft_hash_bwd, and also the temperature gradient of a learnable scale
+ * (scaling/benchmark_time.py:104,111, logits = tanh(proj) / scale): gscale_partials
+ * receives race_soft_hash_bwd_partials(sh) per-workgroup sums of (dL/du) * u with
+ * u = tanh(proj) / scale, so dL/dscale = -(sum of the partials) / scale. */
+int race_soft_hash_bwd_partials(const race_hash_shape *sh);
+int race_soft_hash_bwd_scale(const race_hash_shape *sh, race_tensor x, int x_dtype,
+                             const float *planes_T, const float *gprobs, race_tensor dx,
+                             float *gscale_partials, race_stream stream);
+
 /* ---------------------------------------------------------------- op-level scan */
 /* pK, pQ [N][T][S], V / out / gO / gV [N][T][D], gpK / gpQ [N][T][S]; fp32,
  * contiguous. `block` = tokens per workgroup (0: automatic; results do not depend
@@ -84,6 +93,21 @@ int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, in
 int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK,
                 float *gpQ, float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps,
                 int64_t block, void *workspace, size_t workspace_bytes, race_stream stream);
+
+/* ---------------------------------------------------------------- non-causal op */
+/* Non-causal RACE of BatchedACE (scaling/benchmark_time.py:139-160), replacing its
+ * torch bmm sequence: E = (pK^T V) / (sum_t pK + eps), out = pQ E; the backward
+ * gives gpK, gpQ, gV as the autograd of that sequence. Same layouts and workspace
+ * convention as race_op_*. */
+size_t race_nc_op_workspace_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block,
+                                  int backward);
+int race_nc_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N,
+                   int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
+                   size_t workspace_bytes, race_stream stream);
+int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO,
+                   float *gpK, float *gpQ, float *gV, int64_t N, int64_t T, int64_t S,
+                   int64_t D, float eps, int64_t block, void *workspace,
+                   size_t workspace_bytes, race_stream stream);
 
 /* ---------------------------------------------------------------- fused layer */
 typedef struct {
@@ -142,7 +166,9 @@ enum {
     RACE_PROF_SOFTHASH_FWD = 10,
     RACE_PROF_SOFTHASH_BWD = 11,
     RACE_PROF_DECODE = 12,
-    RACE_PROF_KERNELS = 13
+    RACE_PROF_NC_FWD = 13,
+    RACE_PROF_NC_BWD = 14,
+    RACE_PROF_KERNELS = 15
 };
 int race_profile_enable(int on);
 int race_profile_read(int kernel, double *total_ms, int64_t *launches);

@@ -17,6 +17,10 @@ float64 torch on the CPU (the reference itself is torch code):
   race_module_ref       scaling/race_causal_cuda.py:94-102 / race_torch_cumsum.py:27-36
   decode_ref            state semantics of race_prefix_ref's (A_final, B_final)
                         (the reference has no decode: chat/nanochat/gpt.py:143-146)
+  race_noncausal_ref    scaling/benchmark_time.py:139-160 (non-causal bmm sequence)
+  race_noncausal_brute  O(T^2) loop of the same definition, tiny T only
+  batched_ace_nc_ref    scaling/benchmark_time.py:111-166 (BatchedACE.forward with
+                        the learnable temperature, shared or per-ensemble planes)
 
 How each is pinned (tests/test_oracle.py):
   build_planes_protos : committed fixture of the planes for the seeds used;
@@ -32,6 +36,14 @@ How each is pinned (tests/test_oracle.py):
                         torch.autograd.gradcheck (finite differences) and by the
                         C restatement of the explicit backward in race_pref.cpp.
   decode_ref          : equals race_module_ref at every position.
+  race_noncausal_ref  : equals race_noncausal_brute; its last row equals
+                        race_prefix_ref's last row (the causal prefix at T-1 is the
+                        whole sequence); planes=0 known answer
+                        out_t = L * sum_tau v_tau / (T + R*eps); gradients by
+                        torch.autograd.gradcheck.
+  batched_ace_nc_ref  : built from soft_hash_probs' formula with a tensor scale;
+                        pinned through race_noncausal_ref and by gradcheck in the
+                        temperature.
 """
 import itertools
 import math
@@ -201,6 +213,55 @@ def decode_ref(K_hist, V_hist, q_new, k_new, v_new, planes_T, L, Kbits, eps=1e-6
     out, A, Bst = race_prefix_ref(pK, pQ, V2, eps)
     Bb, H = q_new.shape[0], q_new.shape[1]
     return out[:, -1].reshape(Bb, H, -1), A, Bst
+
+
+def race_noncausal_ref(probsK, probsQ, V2, eps=1e-6):
+    """Non-causal bucket summaries (scaling/benchmark_time.py:139-160):
+    A = sum_t pK, B = pK^T V, E = B / (A + eps), out = pQ E. [N,T,S] x2, [N,T,D] -> [N,T,D]."""
+    A = probsK.sum(dim=1)
+    Bsum = probsK.transpose(1, 2) @ V2
+    E = Bsum / (A.unsqueeze(-1) + eps)
+    return probsQ @ E
+
+
+def race_noncausal_brute(probsK, probsQ, V2, eps=1e-6):
+    """O(N T^2 S) loops of out[t] = sum_s pQ[t,s] sum_tau pK[tau,s] v_tau / (sum_tau pK[tau,s] + eps)."""
+    N, T, S = probsK.shape
+    out = torch.zeros(N, T, V2.shape[-1], dtype=F64)
+    for n in range(N):
+        for s in range(S):
+            a = float(probsK[n, :, s].sum())
+            b = (probsK[n, :, s].to(F64).unsqueeze(-1) * V2[n].to(F64)).sum(0)
+            for t in range(T):
+                out[n, t] += float(probsQ[n, t, s]) * b / (a + eps)
+    return out
+
+
+def batched_ace_nc_ref(Khf, Vhf, Qhf, planes_T, protos_T, L, Kbits, share_planes, logit_temp, eps=1e-6):
+    """BatchedACE.forward of scaling/benchmark_time.py:111-166 in fp64.
+
+    Khf, Vhf, Qhf [M,B,T,H,dk]; planes_T [dk, L*K] (shared) or [M, dk, L*K];
+    logit_temp a 0-d tensor: scale = exp(logit_temp).clamp(1e-2, 10) divides the
+    tanh'd projections. Differentiable in the inputs and logit_temp."""
+    M, B, T, H, dk = Khf.shape
+    N = M * B * H
+    S = L << Kbits
+    scale = logit_temp.to(F64).exp().clamp(1e-2, 10.0)
+
+    def flat(X):
+        return X.to(F64).permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
+
+    Kh, Qh, Vh = flat(Khf), flat(Qhf), flat(Vhf)
+    P = planes_T.to(F64)
+    pr = protos_T.to(F64)
+
+    def probs(Xh):
+        proj = Xh @ P if share_planes else torch.einsum("mbtd,mds->mbts", Xh, P)
+        logits = (proj.reshape(N, T, L, Kbits).tanh() / scale) @ pr
+        return torch.softmax(logits, dim=-1).reshape(N, T, S)
+
+    out = race_noncausal_ref(probs(Kh), probs(Qh), Vh.reshape(N, T, dk), eps)
+    return out.view(M, B, H, T, dk).permute(0, 1, 3, 2, 4)
 
 
 def relerr(got, ref):

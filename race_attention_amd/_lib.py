@@ -49,6 +49,14 @@ SIGNATURES = {
     "race_soft_hash_fwd": (ctypes.c_int, [ctypes.POINTER(HashShape), Tensor4, ctypes.c_int, _vp, _vp, _vp]),
     "race_soft_hash_bwd": (ctypes.c_int, [ctypes.POINTER(HashShape), Tensor4, ctypes.c_int, _vp, _vp,
                                           Tensor4, _vp]),
+    "race_soft_hash_bwd_partials": (ctypes.c_int, [ctypes.POINTER(HashShape)]),
+    "race_soft_hash_bwd_scale": (ctypes.c_int, [ctypes.POINTER(HashShape), Tensor4, ctypes.c_int, _vp, _vp,
+                                                Tensor4, _vp, _vp]),
+    "race_nc_op_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, ctypes.c_int]),
+    "race_nc_op_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
+                                      ctypes.c_size_t, _vp]),
+    "race_nc_op_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float,
+                                      _i64, _vp, ctypes.c_size_t, _vp]),
     "race_op_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, ctypes.c_int]),
     "race_op_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
                                    ctypes.c_size_t, _vp]),
@@ -72,7 +80,8 @@ SIGNATURES = {
 # kernel ids of race_profile_read (include/race_attention.h)
 PROF_KERNELS = ["qkv_fwd_totals", "qkv_fwd_readout", "qkv_bwd_totals", "qkv_bwd_main",
                 "op_fwd_totals", "op_fwd_readout", "op_bwd_totals", "op_bwd_main",
-                "block_scan", "reduce_partials", "softhash_fwd", "softhash_bwd", "decode_step"]
+                "block_scan", "reduce_partials", "softhash_fwd", "softhash_bwd", "decode_step",
+                "nc_readout", "nc_backward"]
 
 _LIB = None
 

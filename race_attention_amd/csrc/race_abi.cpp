@@ -13,6 +13,7 @@
 #include "../../include/race_attention.h"
 #include "race_decode.h"
 #include "race_launch.h"
+#include "race_noncausal.h"
 #include "race_softhash.h"
 
 using namespace race;
@@ -325,6 +326,27 @@ int race_soft_hash_bwd(const race_hash_shape *sh, race_tensor x, int x_dtype, co
     return hip_check(prof_softhash(P, x_dtype == RACE_BF16, 1, hs(stream)), "race_soft_hash_bwd");
 }
 
+int race_soft_hash_bwd_partials(const race_hash_shape *sh)
+{
+    if (!sh || sh->T <= 0 || sh->B <= 0 || sh->H <= 0)
+        return 0;
+    return (int)(cdiv(sh->T, SH_TT) * sh->B * sh->H);
+}
+
+int race_soft_hash_bwd_scale(const race_hash_shape *sh, race_tensor x, int x_dtype, const float *planes_T,
+                             const float *gprobs, race_tensor dx, float *gscale_partials, race_stream stream)
+{
+    SoftHashParams P;
+    RACE_TRY(hash_common(sh, x, x_dtype, planes_T, P));
+    if (!gprobs || !gscale_partials)
+        return fail(RACE_ERR_INVALID, "race_soft_hash_bwd_scale: null gprobs or partials");
+    RACE_TRY(check_view(dx, "race_soft_hash_bwd_scale: dx", false));
+    P.gprobs = gprobs;
+    P.dx = to_view(dx);
+    P.gscale = gscale_partials;
+    return hip_check(prof_softhash(P, x_dtype == RACE_BF16, 1, hs(stream)), "race_soft_hash_bwd_scale");
+}
+
 // ============================================================================ op-level scan
 static size_t op_bytes(const Geo &g, int64_t T, int64_t D, int backward)
 {
@@ -451,6 +473,98 @@ int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *g
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{gV, T * D, 0, D, 0, 1},
                                                   (int)N, 1, (int)T, (int)D, s), "reduce partials"));
     return RACE_OK;
+}
+
+// ============================================================================ non-causal op
+static size_t nc_bytes(const Geo &g, int backward)
+{
+    return (backward ? 2 : 1) * (align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4));
+}
+
+size_t race_nc_op_workspace_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block, int backward)
+{
+    Geo g;
+    if (op_geometry(N, T, S, D, block, g) != RACE_OK)
+        return 0;
+    return nc_bytes(g, backward);
+}
+
+// whole-sequence totals of (w, x): per-block sums then the forward block scan (slot NB)
+static int nc_totals(const Geo &g, ScanParams P, const float *w, const float *x, float *wsB, float *wsA,
+                     hipStream_t s)
+{
+    P.pK = w;
+    P.V = x;
+    P.wsB = wsB;
+    P.wsA = wsA;
+    RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
+    RACE_TRY(hip_check(prof_block_scan(wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    return hip_check(prof_block_scan(wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan");
+}
+
+static NcParams nc_params(const Geo &g, int64_t T, int64_t S, int64_t D, float eps)
+{
+    NcParams Q;
+    std::memset(&Q, 0, sizeof(Q));
+    Q.T = (int)T;
+    Q.S = (int)S;
+    Q.D = (int)D;
+    Q.NB = (int)g.NB;
+    Q.S_pad = g.S_pad;
+    Q.DPw = g.DP;
+    Q.eps = eps;
+    return Q;
+}
+
+int race_nc_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T, int64_t S,
+                   int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes, race_stream stream)
+{
+    Geo g;
+    RACE_TRY(op_geometry(N, T, S, D, block, g));
+    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, nc_bytes(g, 0), "race_nc_op_fwd"));
+    if (!out)
+        return fail(RACE_ERR_INVALID, "race_nc_op_fwd: null out");
+    Carver cv(workspace, workspace_bytes);
+    float *wsB = cv.take(g.state_elems_B), *wsA = cv.take(g.state_elems_A);
+    const hipStream_t s = hs(stream);
+    RACE_TRY(nc_totals(g, op_params(g, T, S, D, eps), pK, V, wsB, wsA, s));
+    NcParams Q = nc_params(g, T, S, D, eps);
+    Q.pQ = pQ;
+    Q.out = out;
+    Q.totB = wsB;
+    Q.totA = wsA;
+    ProfScope ps(RACE_PROF_NC_FWD, s);
+    return hip_check(launch_noncausal(0, g.DP, Q, (int)N, s), "race_nc_op_fwd readout");
+}
+
+int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                   float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                   void *workspace, size_t workspace_bytes, race_stream stream)
+{
+    Geo g;
+    RACE_TRY(op_geometry(N, T, S, D, block, g));
+    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, nc_bytes(g, 1), "race_nc_op_bwd"));
+    if (!gO || !gpK || !gpQ || !gV)
+        return fail(RACE_ERR_INVALID, "race_nc_op_bwd: null gradient pointer");
+    Carver cv(workspace, workspace_bytes);
+    float *wsB = cv.take(g.state_elems_B), *wsA = cv.take(g.state_elems_A);
+    float *ws2B = cv.take(g.state_elems_B), *ws2A = cv.take(g.state_elems_A);
+    const hipStream_t s = hs(stream);
+    const ScanParams P = op_params(g, T, S, D, eps);
+    RACE_TRY(nc_totals(g, P, pK, V, wsB, wsA, s));
+    RACE_TRY(nc_totals(g, P, pQ, gO, ws2B, ws2A, s));
+    NcParams Q = nc_params(g, T, S, D, eps);
+    Q.pK = pK;
+    Q.V = V;
+    Q.gO = gO;
+    Q.gpK = gpK;
+    Q.gpQ = gpQ;
+    Q.gV = gV;
+    Q.totB = wsB;
+    Q.totA = wsA;
+    Q.totGE = ws2B;
+    ProfScope ps(RACE_PROF_NC_BWD, s);
+    return hip_check(launch_noncausal(1, g.DP, Q, (int)N, s), "race_nc_op_bwd backward");
 }
 
 // ============================================================================ fused layer

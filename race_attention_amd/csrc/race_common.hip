@@ -196,6 +196,7 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
     float gx[MAXO];
     for (int o = 0; o < MAXO; ++o)
         gx[o] = 0.0f;
+    float gsu = 0.0f;  // sum of gu * u over this thread's (token, table) items
     for (int m = 0; m < P.M; ++m) {
         const float *planes = P.planes + (int64_t)(P.unshared ? m : 0) * P.plane_stride;
         __syncthreads();
@@ -229,6 +230,8 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
                     for (int k = 0; k < P.K; ++k)
                         gu[k] += ((c >> (P.K - 1 - k)) & 1) ? gz : -gz;
                 }
+                for (int k = 0; k < P.K; ++k)
+                    gsu += gu[k] * u[k];
             }
             for (int k = 0; k < P.K; ++k) {
                 const float th = u[k] * P.scale;
@@ -255,6 +258,17 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
             if (r < nv)
                 dx[b * P.dx.sb + h * P.dx.sh + (int64_t)(t0 + r) * P.dx.st + d] = (TX)gx[o];
         }
+    }
+    if (P.gscale) {
+        // workgroup sum of gu * u: d loss / d scale = -(1/scale) * (sum over all workgroups)
+        __shared__ float red[4];
+        for (int o = 32; o > 0; o >>= 1)
+            gsu += __shfl_xor(gsu, o);
+        if ((threadIdx.x & 63) == 0)
+            red[threadIdx.x >> 6] = gsu;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            P.gscale[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
     }
 }
 

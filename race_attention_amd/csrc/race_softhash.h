@@ -20,6 +20,7 @@ struct SoftHashParams {
     int unshared;         // 1: planes differ per ensemble member
     int round_planes;     // 1: round planes to bf16 (bf16 inputs, as race_common.py:54)
     float scale, inv_scale;
+    float *gscale;        // backward, optional: per-workgroup sums of gu * u (temperature grad)
 };
 
 size_t softhash_smem(int D, int LK, bool bwd);

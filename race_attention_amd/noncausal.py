@@ -1,0 +1,160 @@
+"""Non-causal RACE (BatchedACE of scaling/benchmark_time.py:77-176) on the MI355X kernels.
+
+The reference computes, per stream n = (m, b, h), the whole-sequence bucket summaries
+A = sum_t pK, B = pK^T V, E = B / (A + eps) and reads them out with out = pQ E
+(benchmark_time.py:139-160), through torch bmm in fp32, with a learnable softmax
+temperature scale = exp(logit_temp).clamp(1e-2, 10) (benchmark_time.py:104,111).
+
+Here the summaries are the per-block totals of the causal scan machinery (one totals
+kernel and the block scan, whose last slot is the whole-sequence sum) and the readout
+and its backward are HIP kernels (race_nc_op_fwd / race_nc_op_bwd). The soft-hash runs
+in the HIP soft-hash kernels; with a learnable temperature its backward also returns
+d loss / d scale from per-workgroup partial sums (race_soft_hash_bwd_scale).
+"""
+import itertools
+
+import torch
+import torch.nn as nn
+from torch.autograd import Function
+
+from . import _lib
+from .race_causal_cuda import _op_inputs
+from .race_common import _hash_shape
+
+
+def race_nc_fwd(probsK, probsQ, V2, eps, block=0):
+    pK, pQ, V = _op_inputs(probsK, probsQ, V2)
+    N, T, S = pK.shape
+    D = V.shape[2]
+    lib = _lib.lib()
+    ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, block, 0), pK.device)
+    out = torch.empty(N, T, D, dtype=torch.float32, device=pK.device)
+    _lib.check(lib.race_nc_op_fwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(out), N, T, S, D, float(eps),
+                                  block, _lib.ptr(ws), ws.numel(), _lib.stream_of(pK)), "race_nc_op_fwd")
+    return out
+
+
+def race_nc_bwd(probsK, probsQ, V2, grad_out, eps, block=0):
+    pK, pQ, V = _op_inputs(probsK, probsQ, V2)
+    N, T, S = pK.shape
+    D = V.shape[2]
+    gO = grad_out.float().contiguous()
+    lib = _lib.lib()
+    ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, block, 1), pK.device)
+    gpK, gpQ, gV = torch.empty_like(pK), torch.empty_like(pQ), torch.empty_like(V)
+    _lib.check(lib.race_nc_op_bwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(gO), _lib.ptr(gpK),
+                                  _lib.ptr(gpQ), _lib.ptr(gV), N, T, S, D, float(eps), block, _lib.ptr(ws),
+                                  ws.numel(), _lib.stream_of(pK)), "race_nc_op_bwd")
+    return gpK, gpQ, gV
+
+
+class RaceNonCausalFn(Function):
+    """out [N,T,D] fp32 = pQ (pK^T V) / (sum_t pK + eps) for probsK/probsQ [N,T,S], V2 [N,T,D]."""
+
+    @staticmethod
+    def forward(ctx, probsK, probsQ, V2, eps):
+        ctx.save_for_backward(probsK, probsQ, V2)
+        ctx.eps = float(eps)
+        return race_nc_fwd(probsK, probsQ, V2, eps)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        pK, pQ, V2 = ctx.saved_tensors
+        gpK, gpQ, gV = race_nc_bwd(pK, pQ, V2, grad_out, ctx.eps)
+        return gpK, gpQ, gV.to(V2.dtype), None
+
+
+class SoftHashTempFn(Function):
+    """Soft-hash probabilities [Mp*B*H, T, L*2^K] of X [B,H,T,D] with a tensor scale;
+    the backward returns d loss / d X and d loss / d scale."""
+
+    @staticmethod
+    def forward(ctx, X, planes_T, L, Kbits, M, unshared, scale):
+        _lib.require_device(X, planes_T)
+        B, H, T, D = X.shape
+        s = float(scale)
+        planes = planes_T.detach().float().contiguous()
+        xv, Xc = _lib.view4(X)
+        Mp = M if unshared else 1
+        probs = torch.empty(Mp * B * H, T, L << Kbits, dtype=torch.float32, device=X.device)
+        sh = _hash_shape(X, L, Kbits, M, unshared, s)
+        _lib.check(_lib.lib().race_soft_hash_fwd(sh, xv, _lib.dtype_code(X.dtype), _lib.ptr(planes),
+                                                 _lib.ptr(probs), _lib.stream_of(X)), "race_soft_hash_fwd")
+        ctx.save_for_backward(Xc, planes)
+        ctx.cfg = (L, Kbits, M, unshared, s)
+        return probs
+
+    @staticmethod
+    def backward(ctx, gprobs):
+        Xc, planes = ctx.saved_tensors
+        L, Kbits, M, unshared, s = ctx.cfg
+        B, H, T, D = Xc.shape
+        Mp = M if unshared else 1
+        g = gprobs.float().contiguous().view(Mp, B * H, T, -1)
+        dX = torch.empty(B, H, T, D, dtype=Xc.dtype, device=Xc.device)
+        xv, _ = _lib.view4(Xc)
+        dv, _ = _lib.view4(dX)
+        sh = _hash_shape(Xc, L, Kbits, Mp, unshared, s)
+        lib = _lib.lib()
+        part = torch.empty(lib.race_soft_hash_bwd_partials(sh), dtype=torch.float32, device=Xc.device)
+        _lib.check(lib.race_soft_hash_bwd_scale(sh, xv, _lib.dtype_code(Xc.dtype), _lib.ptr(planes), _lib.ptr(g),
+                                                dv, _lib.ptr(part), _lib.stream_of(Xc)), "race_soft_hash_bwd_scale")
+        dscale = -part.double().sum() / s
+        return dX, None, None, None, None, None, dscale.to(torch.float32)
+
+
+class BatchedACE(nn.Module):
+    """Non-causal BatchedACE (scaling/benchmark_time.py:77-166): Khf, Vhf, Qhf
+    [M,B,T,H,d_k] -> [M,B,T,H,d_k], planes from the global RNG as the reference,
+    learnable temperature logit_temp (scale = exp(logit_temp).clamp(1e-2, 10))."""
+
+    def __init__(self, d_k, K, L, M, device="cpu", share_planes: bool = False):
+        super().__init__()
+        self.d_k, self.K, self.L, self.M = d_k, K, L, M
+        self.R = 1 << K
+        self.share_planes = share_planes
+        if share_planes:
+            planes = torch.randn(L, K, d_k, device=device)
+            self.register_buffer("planes_T", planes.view(L * K, d_k).T)
+        else:
+            planes = torch.randn(M, L, K, d_k, device=device)
+            self.register_buffer("planes_T", planes.view(M, L * K, d_k).transpose(1, 2))
+        corners = torch.tensor(list(itertools.product([-1.0, 1.0], repeat=K)), device=device)
+        self.register_buffer("protos_T", corners.T)
+        self.logit_temp = nn.Parameter(torch.log(torch.tensor(1.0, device=device)))
+
+    def forward(self, Khf, Vhf, Qhf, eps: float = 1e-6):
+        M, B, T, H, dk = Khf.shape
+        if M != self.M or dk != self.d_k:
+            raise ValueError(f"expected [M={self.M},B,T,H,{self.d_k}] inputs, got {tuple(Khf.shape)}")
+        scale = self.logit_temp.exp().clamp(1e-2, 10.0)
+        # streams ordered (M, B, H) as benchmark_time.py:121-131; one row of planes per m
+        def bhtd(X):  # [M,B,T,H,dk] -> [M*B, H, T, dk] view
+            return X.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, dk)
+
+        if self.share_planes:
+            pK = SoftHashTempFn.apply(bhtd(Khf), self.planes_T, self.L, self.K, 1, False, scale)
+            pQ = SoftHashTempFn.apply(bhtd(Qhf), self.planes_T, self.L, self.K, 1, False, scale)
+        else:
+            # per-ensemble planes [M, dk, L*K]: member m hashes its own B*H rows
+            Kx = Khf.permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
+            Qx = Qhf.permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
+            pK = torch.cat([SoftHashTempFn.apply(Kx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale)
+                            for m in range(M)], 0)
+            pQ = torch.cat([SoftHashTempFn.apply(Qx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale)
+                            for m in range(M)], 0)
+        V2 = Vhf.permute(0, 1, 3, 2, 4).reshape(M * B * H, T, dk)
+        out2 = RaceNonCausalFn.apply(pK, pQ, V2, eps)
+        return out2.view(M, B, H, T, dk).permute(0, 1, 3, 2, 4)
+
+
+def race_attention(Q, K, V, ace_module: BatchedACE, eps=1e-6):
+    """[B,H,T,D] wrapper of BatchedACE (scaling/benchmark_time.py:168-176): pack to
+    [M,B,T,H,D], run, average over M, return [B,H,T,D]."""
+    M = ace_module.M
+
+    def pack(Z):
+        return Z.permute(0, 2, 1, 3).unsqueeze(0).expand(M, -1, -1, -1, -1)
+
+    out = ace_module(pack(K), pack(V), pack(Q), eps)
+    return out.mean(dim=0).permute(0, 2, 1, 3)

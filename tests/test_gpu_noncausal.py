@@ -1,0 +1,83 @@
+"""Non-causal RACE (BatchedACE, scaling/benchmark_time.py:77-176) on the GPU against the
+fp64 oracle: the probability-level op (RaceNonCausalFn over race_nc_op_fwd/bwd) and the
+module with its learnable temperature (soft-hash backward with d loss / d scale).
+fp32 throughout: tolerance 1e-4 (max-normalised, scaling/test_kernels.py:30-31)."""
+import pytest
+import torch
+
+from oracle import race_oracle as orc
+from race_ref import check
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _probs(N, T, S, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    pk = torch.softmax(torch.randn(N, T, S, generator=g) * 2, -1)
+    pq = torch.softmax(torch.randn(N, T, S, generator=g) * 2, -1)
+    v = torch.randn(N, T, D, generator=g)
+    go = torch.randn(N, T, D, generator=g)
+    return pk, pq, v, go
+
+
+@pytest.mark.parametrize("N,T,S,D", [(1, 1, 8, 16), (2, 7, 24, 64), (3, 300, 128, 64), (1, 4096, 256, 128),
+                                     (2, 1000, 64, 100), (1, 513, 300, 256), (4, 2000, 16, 32)])
+def test_noncausal_op(dev, N, T, S, D):
+    from race_attention_amd.noncausal import RaceNonCausalFn
+    print(f"nc op N={N} T={T} S={S} D={D}", flush=True)
+    pk, pq, v, go = _probs(N, T, S, D, seed=T + S + D)
+    eps = 1e-6
+    pkr, pqr, vr = (x.double().requires_grad_(True) for x in (pk, pq, v))
+    ref = orc.race_noncausal_ref(pkr, pqr, vr, eps)
+    ref.backward(go.double())
+    pkx, pqx, vx = (x.to(dev).requires_grad_(True) for x in (pk, pq, v))
+    out = RaceNonCausalFn.apply(pkx, pqx, vx, eps)
+    out.backward(go.to(dev))
+    check("out", out, ref, TOL)
+    check("gpK", pkx.grad, pkr.grad, TOL)
+    check("gpQ", pqx.grad, pqr.grad, TOL)
+    check("gV", vx.grad, vr.grad, TOL)
+
+
+def test_noncausal_block_invariance(dev):
+    from race_attention_amd.noncausal import race_nc_fwd
+    pk, pq, v, _ = _probs(2, 3000, 64, 64, seed=9)
+    a = race_nc_fwd(pk.to(dev), pq.to(dev), v.to(dev), 1e-6, 0)
+    for blk in (16, 256, 3000):
+        b = race_nc_fwd(pk.to(dev), pq.to(dev), v.to(dev), 1e-6, blk)
+        check(f"block {blk}", b, a.double(), 1e-6)
+
+
+@pytest.mark.parametrize("share", [True, False])
+@pytest.mark.parametrize("M", [1, 2])
+def test_batched_ace_noncausal_module(dev, share, M):
+    from race_attention_amd.noncausal import BatchedACE, race_attention
+    torch.manual_seed(0)
+    B, T, H, dk, L, K = 2, 200, 3, 64, 4, 3
+    ace = BatchedACE(dk, K, L, M, device=dev, share_planes=share)
+    with torch.no_grad():
+        ace.logit_temp.fill_(0.4)
+    g = torch.Generator().manual_seed(1)
+    Kh, Vh, Qh = (torch.randn(M, B, T, H, dk, generator=g) for _ in range(3))
+    go = torch.randn(M, B, T, H, dk, generator=g)
+    lt = torch.tensor(0.4, dtype=torch.float64, requires_grad=True)
+    refs = [x.double().requires_grad_(True) for x in (Kh, Vh, Qh)]
+    ref = orc.batched_ace_nc_ref(*refs, ace.planes_T.cpu(), ace.protos_T.cpu(), L, K, share, lt)
+    ref.backward(go.double())
+    xs = [x.to(dev).requires_grad_(True) for x in (Kh, Vh, Qh)]
+    out = ace(*xs)
+    out.backward(go.to(dev))
+    check("out", out, ref, TOL)
+    for name, a, r in zip(("dK", "dV", "dQ"), xs, refs):
+        check(name, a.grad, r.grad, TOL)
+    check("dlogit_temp", ace.logit_temp.grad.reshape(1), lt.grad.reshape(1), TOL)
+    # [B,H,T,D] wrapper: mean over the M copies of the same inputs
+    Q4, K4, V4 = (torch.randn(B, H, T, dk, generator=g).to(dev) for _ in range(3))
+    with torch.no_grad():
+        o4 = race_attention(Q4, K4, V4, ace)
+        pack = lambda Z: Z.permute(0, 2, 1, 3).unsqueeze(0).expand(M, -1, -1, -1, -1).double().cpu()
+        r4 = orc.batched_ace_nc_ref(pack(K4), pack(V4), pack(Q4), ace.planes_T.cpu(), ace.protos_T.cpu(), L, K,
+                                    share, lt.detach()).mean(0).permute(0, 2, 1, 3)
+    check("race_attention", o4, r4, TOL)

@@ -232,3 +232,70 @@ def test_gqa_ref_is_repeated_kv():
         one = orc.race_module_ref(Q[:, h:h + 1], K[:, h // 2:h // 2 + 1], V[:, h // 2:h // 2 + 1],
                                   planes_T, protos, L, Kb)
         assert (out[:, h:h + 1] - one).abs().max().item() < 1e-14
+
+
+# ------------------------------------------------------------------ non-causal restatement
+def _nc_inputs(N, T, S, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    pk = torch.softmax(torch.randn(N, T, S, generator=g, dtype=torch.float64), -1)
+    pq = torch.softmax(torch.randn(N, T, S, generator=g, dtype=torch.float64), -1)
+    v = torch.randn(N, T, D, generator=g, dtype=torch.float64)
+    return pk, pq, v
+
+
+def test_noncausal_matches_brute_force():
+    pk, pq, v = _nc_inputs(2, 9, 6, 5, 0)
+    assert torch.allclose(orc.race_noncausal_ref(pk, pq, v), orc.race_noncausal_brute(pk, pq, v),
+                          rtol=1e-12, atol=1e-12)
+
+
+def test_noncausal_last_row_is_causal_last_row():
+    pk, pq, v = _nc_inputs(3, 40, 16, 8, 1)
+    nc = orc.race_noncausal_ref(pk, pq, v)
+    ca, _, _ = orc.race_prefix_ref(pk, pq, v)
+    assert torch.allclose(nc[:, -1], ca[:, -1], rtol=1e-12, atol=1e-12)
+    assert not torch.allclose(nc[:, 0], ca[:, 0])  # earlier rows see the whole sequence
+
+
+def test_noncausal_uniform_hash_closed_form():
+    B, H, T, D, L, K, eps = 1, 2, 50, 8, 3, 2, 1e-3
+    planes = torch.zeros(D, L * K, dtype=torch.float64)
+    _, protos = orc.build_planes_protos(D, K, L)
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(B, H, T, D, generator=g, dtype=torch.float64) for _ in range(3))
+    pk, pq, v2, _ = orc.soft_hash_probs(q, k, v, planes, protos, L, K)
+    out = orc.race_noncausal_ref(pk, pq, v2, eps)
+    R = 1 << K
+    want = L * v2.sum(1, keepdim=True) / (T + R * eps)
+    assert torch.allclose(out, want.expand_as(out), rtol=1e-12, atol=1e-12)
+
+
+def test_noncausal_single_token_closed_form():
+    pk, pq, v = _nc_inputs(2, 1, 12, 4, 3)
+    eps = 1e-2
+    want = (pq * pk / (pk + eps)).sum(-1, keepdim=True) * v
+    assert torch.allclose(orc.race_noncausal_ref(pk, pq, v, eps), want, rtol=1e-12, atol=1e-12)
+
+
+def test_noncausal_gradcheck():
+    pk, pq, v = _nc_inputs(1, 5, 4, 3, 4)
+    for x in (pk, pq, v):
+        x.requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda a, b, c: orc.race_noncausal_ref(a, b, c, 1e-3), (pk, pq, v))
+
+
+def test_batched_ace_nc_temperature_gradcheck():
+    g = torch.Generator().manual_seed(5)
+    M, B, T, H, dk, L, K = 2, 1, 6, 2, 4, 2, 2
+    Kh, Vh, Qh = (torch.randn(M, B, T, H, dk, generator=g, dtype=torch.float64) for _ in range(3))
+    planes = torch.randn(M, dk, L * K, generator=g, dtype=torch.float64)
+    _, protos = orc.build_planes_protos(dk, K, L)
+    lt = torch.tensor(0.3, dtype=torch.float64, requires_grad=True)
+    Kh.requires_grad_(True)
+    f = lambda t, kk: orc.batched_ace_nc_ref(kk, Vh, Qh, planes, protos, L, K, False, t)
+    assert torch.autograd.gradcheck(f, (lt, Kh))
+    # shared planes equal per-member planes when every member gets the same matrix
+    shared = planes[0]
+    a = orc.batched_ace_nc_ref(Kh, Vh, Qh, shared, protos, L, K, True, lt)
+    b = orc.batched_ace_nc_ref(Kh, Vh, Qh, shared.expand(M, -1, -1), protos, L, K, False, lt)
+    assert torch.allclose(a, b, rtol=1e-12, atol=1e-12)
