@@ -94,6 +94,21 @@ int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *g
                 float *gpQ, float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps,
                 int64_t block, void *workspace, size_t workspace_bytes, race_stream stream);
 
+/* ---------------------------------------------------------------- causal linear attention */
+/* Katharopoulos causal linear attention, the reference's comparison kernel
+ * (kernels/cpu/linear_pref.cpp:87-213, causal_dot_product / causal_dot_backward):
+ * out_l = Q_l . sum_{s<=l} K_s (x) V_s, with Q, K [N][L][E], V / out / gO / gV [N][L][M]
+ * and gQ, gK [N][L][E] fp32 contiguous (N = batch * heads). Runs on the causal scan
+ * kernels with the normalisation removed; workspace from race_op_workspace_bytes(N, L,
+ * E, M, block, backward). */
+int race_causal_dot_product(const float *Q, const float *K, const float *V, float *out,
+                            int64_t N, int64_t L, int64_t E, int64_t M, int64_t block,
+                            void *workspace, size_t workspace_bytes, race_stream stream);
+int race_causal_dot_backward(const float *Q, const float *K, const float *V, const float *gO,
+                             float *gQ, float *gK, float *gV, int64_t N, int64_t L, int64_t E,
+                             int64_t M, int64_t block, void *workspace, size_t workspace_bytes,
+                             race_stream stream);
+
 /* ---------------------------------------------------------------- non-causal op */
 /* Non-causal RACE of BatchedACE (scaling/benchmark_time.py:139-160), replacing its
  * torch bmm sequence: E = (pK^T V) / (sum_t pK + eps), out = pQ E; the backward

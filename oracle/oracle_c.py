@@ -90,14 +90,23 @@ def race_bwd(pK, pQ, V, gO, eps):
     return gpK, gpQ, gV
 
 
-def ref_ext():
-    """The reference's own race_pref.cpp compiled into oracle/_ref (None if not built)."""
-    path = os.path.join(_HERE, "_ref", "race_pref_ref.so")
+def _load_ref(name):
+    path = os.path.join(_HERE, "_ref", name + ".so")
     if not os.path.exists(path):
         return None
     import importlib.util
-    spec = importlib.util.spec_from_file_location("race_pref_ref", path)
+    spec = importlib.util.spec_from_file_location(name, path)
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
     return mod
+
+
+def ref_ext():
+    """The reference's own race_pref.cpp compiled into oracle/_ref (None if not built)."""
+    return _load_ref("race_pref_ref")
+
+
+def ref_linear_ext():
+    """The reference's own linear_pref.cpp compiled into oracle/_ref (None if not built)."""
+    return _load_ref("linear_pref_ref")
 

@@ -21,6 +21,9 @@ float64 torch on the CPU (the reference itself is torch code):
   race_noncausal_brute  O(T^2) loop of the same definition, tiny T only
   batched_ace_nc_ref    scaling/benchmark_time.py:111-166 (BatchedACE.forward with
                         the learnable temperature, shared or per-ensemble planes)
+  causal_linear_ref     kernels/cpu/linear_pref.cpp:87-130 (causal_dot_product), as
+                        kernels/cpu/test_cpu_kernels.py:94-97 states it
+  causal_linear_brute   O(L^2) loop of out_l = sum_{s<=l} (Q_l . K_s) V_s
 
 How each is pinned (tests/test_oracle.py):
   build_planes_protos : committed fixture of the planes for the seeds used;
@@ -41,6 +44,9 @@ How each is pinned (tests/test_oracle.py):
                         whole sequence); planes=0 known answer
                         out_t = L * sum_tau v_tau / (T + R*eps); gradients by
                         torch.autograd.gradcheck.
+  causal_linear_ref   : equals causal_linear_brute and the compiled reference
+                        linear_pref.cpp (oracle/_ref) where built; gradients by
+                        gradcheck and against the reference's causal_dot_backward.
   batched_ace_nc_ref  : built from soft_hash_probs' formula with a tensor scale;
                         pinned through race_noncausal_ref and by gradcheck in the
                         temperature.
@@ -262,6 +268,22 @@ def batched_ace_nc_ref(Khf, Vhf, Qhf, planes_T, protos_T, L, Kbits, share_planes
 
     out = race_noncausal_ref(probs(Kh), probs(Qh), Vh.reshape(N, T, dk), eps)
     return out.view(M, B, H, T, dk).permute(0, 1, 3, 2, 4)
+
+
+def causal_linear_ref(Q, K, V):
+    """Causal linear attention (kernels/cpu/linear_pref.cpp:87-130): out_l = Q_l .
+    sum_{s<=l} K_s (x) V_s. Q, K [N,H,L,E], V [N,H,L,M] -> [N,H,L,M], fp64."""
+    KV = (K.to(F64).unsqueeze(-1) * V.to(F64).unsqueeze(-2)).cumsum(2)
+    return (Q.to(F64).unsqueeze(-1) * KV).sum(-2)
+
+
+def causal_linear_brute(Q, K, V):
+    N, H, L, _ = Q.shape
+    out = torch.zeros(N, H, L, V.shape[-1], dtype=F64)
+    for l in range(L):
+        for s in range(l + 1):
+            out[:, :, l] += (Q[:, :, l].to(F64) * K[:, :, s].to(F64)).sum(-1, keepdim=True) * V[:, :, s].to(F64)
+    return out
 
 
 def relerr(got, ref):

@@ -408,17 +408,18 @@ static int op_check(const float *pK, const float *pQ, const float *V, float eps,
     return RACE_OK;
 }
 
-int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
-                int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
-                race_stream stream)
+static int op_fwd_impl(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
+                       int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
+                       race_stream stream, int linear, const char *who)
 {
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
-    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, op_bytes(g, T, D, 0), "race_op_fwd"));
+    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, op_bytes(g, T, D, 0), who));
     if (!out)
-        return fail(RACE_ERR_INVALID, "race_op_fwd: null out");
+        return fail(RACE_ERR_INVALID, "%s: null out", who);
     Carver cv(workspace, workspace_bytes);
     ScanParams P = op_params(g, T, S, D, eps);
+    P.linear = linear;
     P.pK = pK;
     P.pQ = pQ;
     P.V = V;
@@ -437,17 +438,26 @@ int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, in
     return RACE_OK;
 }
 
-int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
-                float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
-                void *workspace, size_t workspace_bytes, race_stream stream)
+int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
+                int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
+                race_stream stream)
+{
+    return op_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, 0,
+                       "race_op_fwd");
+}
+
+static int op_bwd_impl(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                       float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                       void *workspace, size_t workspace_bytes, race_stream stream, int linear, const char *who)
 {
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
-    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, op_bytes(g, T, D, 1), "race_op_bwd"));
+    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, op_bytes(g, T, D, 1), who));
     if (!gO || !gpK || !gpQ || !gV)
-        return fail(RACE_ERR_INVALID, "race_op_bwd: null gradient pointer");
+        return fail(RACE_ERR_INVALID, "%s: null gradient pointer", who);
     Carver cv(workspace, workspace_bytes);
     ScanParams P = op_params(g, T, S, D, eps);
+    P.linear = linear;
     P.pK = pK;
     P.pQ = pQ;
     P.V = V;
@@ -473,6 +483,32 @@ int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *g
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{gV, T * D, 0, D, 0, 1},
                                                   (int)N, 1, (int)T, (int)D, s), "reduce partials"));
     return RACE_OK;
+}
+
+int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                void *workspace, size_t workspace_bytes, race_stream stream)
+{
+    return op_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream, 0,
+                       "race_op_bwd");
+}
+
+// ============================================================================ causal linear attention
+// Unnormalised causal linear attention on the same chunked scan (W = Q, no 1/(A+eps)).
+int race_causal_dot_product(const float *Q, const float *K, const float *V, float *out, int64_t N, int64_t L,
+                            int64_t E, int64_t M, int64_t block, void *workspace, size_t workspace_bytes,
+                            race_stream stream)
+{
+    return op_fwd_impl(K, Q, V, out, N, L, E, M, 0.0f, block, workspace, workspace_bytes, stream, 1,
+                       "race_causal_dot_product");
+}
+
+int race_causal_dot_backward(const float *Q, const float *K, const float *V, const float *gO, float *gQ,
+                             float *gK, float *gV, int64_t N, int64_t L, int64_t E, int64_t M, int64_t block,
+                             void *workspace, size_t workspace_bytes, race_stream stream)
+{
+    return op_bwd_impl(K, Q, V, gO, gK, gQ, gV, N, L, E, M, 0.0f, block, workspace, workspace_bytes, stream, 1,
+                       "race_causal_dot_backward");
 }
 
 // ============================================================================ non-causal op

@@ -282,7 +282,7 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
                     const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        sW[r + e][col] = (T)(sF[r + e][col] * frcp(accA[i][e] + P.eps));
+                        sW[r + e][col] = (T)(P.linear ? sF[r + e][col] : sF[r + e][col] * frcp(accA[i][e] + P.eps));
                 }
             }
             __syncthreads();
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
                 carry[i] = accA[i][3];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    accA[i][e] = frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
+                    accA[i][e] = P.linear ? 1.0f : frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
             }
         }
         __syncthreads();
@@ -522,6 +522,8 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
                         gpq[e] = accG[i][e] * accA[i][e];
                         colsum -= gpq[e] * accW[i][e];
                     }
+                    if (P.linear)
+                        colsum = 0.0f;
                     accG[i] = gpq;
                     dGA[i / MTC] += colsum;  // reduced across lanes at the end
                     if constexpr (!CF::QKV)
@@ -747,7 +749,7 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
                 carry[i] = accA[i][3];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    accA[i][e] = frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
+                    accA[i][e] = P.linear ? 1.0f : frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
             }
         }
 #pragma unroll
@@ -843,7 +845,7 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
                     mma_tile<E, C>(accG[i], &sMg[0][0], LDC, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        accGA[i][e] -= accG[i][e] * accA[i][e] * accW[i][e];
+                        accGA[i][e] -= P.linear ? 0.0f : accG[i][e] * accA[i][e] * accW[i][e];
                     mma_tile<E, C>(accPK[i], &sMv[0][0], LDC, &sWt[0][0], LDC, tm * 16, tn * 16, c.lane);
                 }
             }

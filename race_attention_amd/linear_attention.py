@@ -1,0 +1,78 @@
+"""Causal linear attention (Katharopoulos et al.), the reference's comparison kernel
+(kernels/cpu/linear_pref.cpp:87-213, bound in kernels/cpu/race_ext.py:57-66):
+
+  causal_dot_product(Q, K, V, out):   out_l = Q_l . sum_{s<=l} K_s (x) V_s
+  causal_dot_backward(Q, K, V, g, gQ, gK, gV)
+
+Q, K [N,H,L,E], V [N,H,L,M] fp32. On MI355X this is the causal RACE scan with the
+1/(A+eps) normalisation removed (race_causal_dot_product / race_causal_dot_backward):
+K plays the bucket probabilities of keys, Q those of queries, E the bucket count.
+"""
+import torch
+from torch.autograd import Function
+
+from . import _lib
+
+
+def _flat(x):
+    N, H, L, F = x.shape
+    return x.detach().float().contiguous().view(N * H, L, F)
+
+
+def causal_dot_product(queries, keys, values, product):
+    """Writes out = causal linear attention into `product` [N,H,L,M] (as the reference)."""
+    _lib.require_device(queries, keys, values, product)
+    N, H, L, E = queries.shape
+    M = values.shape[3]
+    if keys.shape != queries.shape or values.shape[:3] != queries.shape[:3] or product.shape != values.shape:
+        raise ValueError("expected Q, K [N,H,L,E], V and product [N,H,L,M]")
+    Q, K, V = _flat(queries), _flat(keys), _flat(values)
+    out = torch.empty(N * H, L, M, dtype=torch.float32, device=Q.device)
+    lib = _lib.lib()
+    ws = _lib.workspace(lib.race_op_workspace_bytes(N * H, L, E, M, 0, 0), Q.device)
+    _lib.check(lib.race_causal_dot_product(_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(out), N * H, L, E, M, 0,
+                                           _lib.ptr(ws), ws.numel(), _lib.stream_of(Q)), "race_causal_dot_product")
+    product.copy_(out.view(N, H, L, M))
+    return product
+
+
+def causal_dot_backward(queries, keys, values, grad_out, grad_queries, grad_keys, grad_values):
+    """Writes the gradients of causal_dot_product into grad_queries / grad_keys / grad_values."""
+    _lib.require_device(queries, keys, values, grad_out)
+    N, H, L, E = queries.shape
+    M = values.shape[3]
+    Q, K, V, G = _flat(queries), _flat(keys), _flat(values), _flat(grad_out)
+    gQ, gK = torch.empty_like(Q), torch.empty_like(K)
+    gV = torch.empty_like(V)
+    lib = _lib.lib()
+    ws = _lib.workspace(lib.race_op_workspace_bytes(N * H, L, E, M, 0, 1), Q.device)
+    _lib.check(lib.race_causal_dot_backward(_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(G), _lib.ptr(gQ),
+                                            _lib.ptr(gK), _lib.ptr(gV), N * H, L, E, M, 0, _lib.ptr(ws), ws.numel(),
+                                            _lib.stream_of(Q)), "race_causal_dot_backward")
+    grad_queries.copy_(gQ.view(N, H, L, E))
+    grad_keys.copy_(gK.view(N, H, L, E))
+    grad_values.copy_(gV.view(N, H, L, M))
+
+
+class CausalLinearFn(Function):
+    """Autograd wrapper (the reference test's LinFn, kernels/cpu/test_cpu_kernels.py:110-124)."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V):
+        out = torch.empty(Q.shape[0], Q.shape[1], Q.shape[2], V.shape[3], dtype=torch.float32, device=Q.device)
+        causal_dot_product(Q, K, V, out)
+        ctx.save_for_backward(Q, K, V)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        Q, K, V = ctx.saved_tensors
+        gQ = torch.empty(Q.shape, dtype=torch.float32, device=Q.device)
+        gK = torch.empty(K.shape, dtype=torch.float32, device=K.device)
+        gV = torch.empty(V.shape, dtype=torch.float32, device=V.device)
+        causal_dot_backward(Q, K, V, g, gQ, gK, gV)
+        return gQ.to(Q.dtype), gK.to(K.dtype), gV.to(V.dtype)
+
+
+def causal_linear_attention(Q, K, V):
+    return CausalLinearFn.apply(Q, K, V)

@@ -299,3 +299,40 @@ def test_batched_ace_nc_temperature_gradcheck():
     a = orc.batched_ace_nc_ref(Kh, Vh, Qh, shared, protos, L, K, True, lt)
     b = orc.batched_ace_nc_ref(Kh, Vh, Qh, shared.expand(M, -1, -1), protos, L, K, False, lt)
     assert torch.allclose(a, b, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------ causal linear attention
+def _lin_inputs(N, H, L, E, M, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(N, H, L, E, generator=g), torch.randn(N, H, L, E, generator=g),
+            torch.randn(N, H, L, M, generator=g))
+
+
+def test_causal_linear_matches_brute_force():
+    Q, K, V = _lin_inputs(2, 2, 9, 4, 3, 0)
+    assert torch.allclose(orc.causal_linear_ref(Q, K, V), orc.causal_linear_brute(Q, K, V), rtol=1e-12, atol=1e-12)
+
+
+def test_causal_linear_gradcheck():
+    Q, K, V = (x.double().requires_grad_(True) for x in _lin_inputs(1, 1, 5, 3, 2, 1))
+    assert torch.autograd.gradcheck(orc.causal_linear_ref, (Q, K, V))
+
+
+def test_causal_linear_matches_compiled_reference():
+    """The reference's own linear_pref.cpp (compiled into oracle/_ref from its source)."""
+    from oracle import oracle_c
+    ext = oracle_c.ref_linear_ext()
+    if ext is None:
+        pytest.skip("oracle/_ref/linear_pref_ref.so not built (reference tree absent)")
+    for (N, H, L, E, M) in [(1, 1, 1, 4, 4), (2, 2, 16, 8, 8), (2, 4, 256, 32, 32)]:
+        Q, K, V = _lin_inputs(N, H, L, E, M, L)
+        out = torch.zeros(N, H, L, M)
+        ext.causal_dot_product(Q.contiguous(), K.contiguous(), V.contiguous(), out)
+        assert orc.relerr(out, orc.causal_linear_ref(Q, K, V)) < 1e-5
+        g = torch.randn(N, H, L, M)
+        gQ, gK, gV = torch.zeros_like(Q), torch.zeros_like(K), torch.zeros_like(V)
+        ext.causal_dot_backward(Q, K, V, g, gQ, gK, gV)
+        q1, k1, v1 = (x.double().requires_grad_(True) for x in (Q, K, V))
+        (orc.causal_linear_ref(q1, k1, v1) * g.double()).sum().backward()
+        for a, b in ((gQ, q1.grad), (gK, k1.grad), (gV, v1.grad)):
+            assert orc.relerr(a, b) < 1e-5
