@@ -49,6 +49,9 @@ def parse():
                          "T = 2^20 .. --sweep-max, GPU and CPU-path memory per token and the "
                          "largest T each fits")
     ap.add_argument("--sweep-max", type=int, default=1 << 24)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device copy (x3), the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
     ap.add_argument("--workload", default="cfg3", choices=["cfg3", "cfg5"],
                     help="cfg5: Llama-3.2-1B-shaped hybrid LM (random init), B=8, T=8192 prefill "
                          "forward+backward, then 256-token greedy decode through the RACE state cache")
@@ -76,6 +79,20 @@ def kernel_bytes(name, Hq, Hkv, D, elt=2):
     }.get(name)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` at the default cfg3 shape, measured with rocprofv3
+    FETCH_SIZE / WRITE_SIZE (calibrated on a plain copy) and recorded in
+    profiles/race_layer_cfg3_T1M_hbm_traffic.md; None when not recorded."""
+    path = os.path.join(ROOT, "profiles", "race_layer_cfg3_T1M_hbm_traffic.md")
+    try:
+        for line in open(path):
+            if line.strip().startswith("traffic_bytes_per_launch"):
+                return json.loads(line.split("traffic_bytes_per_launch", 1)[1]).get(kernel)
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -88,6 +105,14 @@ def main():
     from race_attention_amd import RaceDecodeState, build_planes_protos, race_causal_attention
     from race_attention_amd import _lib
 
+    if args.copy_calibration:
+        a = torch.empty(1 << 28, device="cuda").uniform_()
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_launch": a.numel() * 4, "launches": 3}))
+        return
     if args.sweep:
         print(json.dumps(bench_sweep(torch, args, build_planes_protos, race_causal_attention)))
         return
@@ -138,8 +163,10 @@ def main():
     if per_tok is not None:
         traffic_bytes = per_tok * B * H * T
         achieved = traffic_bytes / (dom_ms / 1e3) / 1e9
+        default_shape = (B, H, T, L) == (1, 4, 1 << 20, 8)
         roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
-                    "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4),
+                    "traffic": measured_traffic(dom) if default_shape else None,
                     "algorithmic_bytes_per_launch": traffic_bytes, "avg_launch_ms": round(dom_ms, 4)}
     f_alg, b_alg = layer_counts(S, D, L, K)
     n_tok = B * H * T
