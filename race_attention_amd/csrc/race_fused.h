@@ -154,6 +154,37 @@ RACE_DEV void st_vec4(__bf16 *p, const f32x4 &v)
     *reinterpret_cast<bf16x4 *>(p) = w;
 }
 
+// Operand pairs for MFMA chains whose reduction index k is a bucket or head-dim index held
+// by accumulator tiles: the reduction order of an MFMA is free, so lane group g may supply
+// k = k0 + 4g .. +3 and k0 + 16 + 4g .. +3 (the rows of two 16-row accumulator tiles) as
+// its 8 consecutive k, as long as both operands use the same order.
+// A operand from two accumulator tiles (rows k, col m = lane%16), converted to bf16.
+RACE_DEV bf16x8 acc_pair(const f32x4 &lo, const f32x4 &hi)
+{
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[e] = (__bf16)lo[e];
+        f[4 + e] = (__bf16)hi[e];
+    }
+    return f;
+}
+
+// The matching operand from an LDS array stored [n][k] (k contiguous): row n0 + lane%16.
+RACE_DEV bf16x8 ld_pair(const __bf16 *X, int ld, int n0, int k0, int lane)
+{
+    const __bf16 *p = X + (n0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+    const bf16x4 a = *reinterpret_cast<const bf16x4 *>(p);
+    const bf16x4 b = *reinterpret_cast<const bf16x4 *>(p + 16);
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[e] = a[e];
+        f[4 + e] = b[e];
+    }
+    return f;
+}
+
 // MFMA operand fragment (row m0 + lane%16, k = k0 + 8*(lane/16) .. +7) from an LDS array
 // stored [m][k] (k contiguous): one 16-byte read.
 RACE_DEV bf16x8 ld_k(const __bf16 *X, int ld, int m0, int k0, int lane)
@@ -340,7 +371,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
     __shared__ __align__(16) __bf16 sPK[C][LDS];     // rows [t][s]
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
     __shared__ __align__(16) __bf16 sW[C][LDS];
-    __shared__ __align__(16) __bf16 sStT[DP][LDS];
     __shared__ __align__(16) __bf16 sPm[C][LDC];
     __shared__ __align__(16) OT sO[C][LDO];
     __shared__ __align__(16) float sA0[2][ST];
@@ -355,7 +385,12 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
 
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;  // state tiles [ST x DP]
     constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;      // A^T tiles [ST x C]
-    constexpr int TPW_O = (CF::NTD * MTC + NW - 1) / NW;      // out^T tiles [DP x C]
+    // out^T tiles [DP x C]: wave w owns head-dim tiles w + NW*j (j < NDW) for both token
+    // tiles, the same head-dim tiles as its state tiles accS, so out^T = St^T W^T takes its A
+    // operand straight from the state accumulators
+    static_assert(CF::NTD % NW == 0, "head-dim tiles must split evenly over the waves");
+    constexpr int NDW = CF::NTD / NW;
+    constexpr int TPW_O = NDW * MTC;
     constexpr int TPW_M = (MTC * MTC + NW - 1) / NW;          // Pm^T tiles [C x C]
     constexpr int NPT2 = 2 * CF::NPT;                         // k and q projection tiles
     constexpr int TPW_P = (NPT2 + NW - 1) / NW;
@@ -374,7 +409,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     accS[i][e] = wB[(int64_t)(r + e) * P.DPw + col];
-                st_vec4(&sStT[col][r], accS[i]);
             }
         }
         const float *wA = P.wsA + slot * P.S_pad + c.s0;
@@ -496,14 +530,17 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
                 }
             }
             __syncthreads();
-            // ---- P3: out^T = St^T W^T ; Pm^T = triu-masked pK W^T -> sPm ; St += pK^T V (first head)
+            // ---- P3: out^T = St^T W^T (state operand from registers) ; Pm^T = triu-masked pK W^T
+            //          -> sPm ; St += pK^T V (last head)
             f32x4 accO[TPW_O];
 #pragma unroll
             for (int i = 0; i < TPW_O; ++i) {
-                const int t = wave + i * NW;
+                const int j = i / MTC, tt = i % MTC;
                 accO[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (t < CF::NTD * MTC)
-                    mma_ab<ST, LDS, LDS>(accO[i], &sStT[0][0], (t / MTC) * 16, &sW[0][0], (t % MTC) * 16, lane);
+#pragma unroll
+                for (int ks = 0; ks < ST / 32; ++ks)
+                    EngBF16::mma(accO[i], acc_pair(accS[(2 * ks) * NDW + j], accS[(2 * ks + 1) * NDW + j]),
+                                 ld_pair(&sW[0][0], LDS, tt * 16, 32 * ks, lane));
             }
 #pragma unroll
             for (int i = 0; i < TPW_M; ++i) {
@@ -530,33 +567,22 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
                 }
             }
             __syncthreads();
-            // ---- P4: out^T += V^T Pm^T -> sO ; new St^T -> sStT ; next rows -> LDS
+            // ---- P4: out^T += V^T Pm^T -> sO ; next rows -> LDS
 #pragma unroll
             for (int i = 0; i < TPW_O; ++i) {
-                const int t = wave + i * NW;
-                if (t < CF::NTD * MTC) {
-                    const int td = t / MTC, tt = t % MTC;
-                    EngBF16::mma(accO[i], ld_tr(&sV[cur][0][0], LDX, 0, td * 16, lane),
-                                 ld_k(&sPm[0][0], LDC, tt * 16, 0, lane));
-                    const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                    if constexpr (OUT_F32)
-                        *reinterpret_cast<f32x4 *>(&sO[tok][d]) = accO[i];
-                    else
-                        st_vec4(&sO[tok][d], accO[i]);
-                }
+                const int td = wave + NW * (i / MTC), tt = i % MTC;
+                EngBF16::mma(accO[i], ld_tr(&sV[cur][0][0], LDX, 0, td * 16, lane),
+                             ld_k(&sPm[0][0], LDC, tt * 16, 0, lane));
+                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sO[tok][d]) = accO[i];
+                else
+                    st_vec4(&sO[tok][d], accO[i]);
             }
             prev_t0 = t0;
             prev_nv = nv;
             prev_h = hq;
             if (g == G - 1) {
-#pragma unroll
-                for (int i = 0; i < TPW_S; ++i) {
-                    const int t = wave + i * NW;
-                    if (t < CF::NTS * CF::NTD) {
-                        const int r = acc_row((t / CF::NTD) * 16, lane), col = acc_col((t % CF::NTD) * 16, lane);
-                        st_vec4(&sStT[col][r], accS[i]);
-                    }
-                }
                 if (more) {
                     tile_store_rows<CF>(&sK[0][0], pk, tid);
                     tile_store_rows<CF>(&sV[nxt][0][0], pv, tid);
@@ -709,7 +735,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
     __shared__ __align__(16) __bf16 sW[C][LDS];
     __shared__ __align__(16) __bf16 sMg[C][LDC];   // Mg as [t][tau]
-    __shared__ __align__(16) __bf16 sStS[ST][LDX];
+    __shared__ __align__(16) __bf16 sStS[CF::NTS == NW ? 1 : ST][LDX];  // St rows when not in registers
     __shared__ __align__(16) float sGP[C][ST + 4];
     __shared__ __align__(16) __bf16 sGU[C][LDG];
     __shared__ __align__(16) OT sO[C][LDO];
@@ -721,6 +747,13 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;   // k then q projection tiles
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
     constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;
+    // A-tiles [ST x C] (A^T, W, gW, gA per bucket tile ts and token tile tt). When the waves
+    // and the bucket tiles match one to one (REG_ST), wave w owns bucket tile w for every token
+    // tile and every head-dim tile of the state, so gW = go St^T takes St from registers.
+    constexpr bool REG_ST = CF::NTS == NW;
+    auto a_ts = [&](int i) { return REG_ST ? wave : (wave + i * NW) / MTC; };
+    auto a_tt = [&](int i) { return REG_ST ? i : (wave + i * NW) % MTC; };
+    auto a_ok = [&](int i) { return REG_ST || (wave + i * NW) < CF::NTS * MTC; };
     constexpr int TPW_O = (CF::NTD * MTC + NW - 1) / NW;
     constexpr int TPW_M = (MTC * MTC + NW - 1) / NW;
     FusedFrags<CF, DP, TPW_P> fr;
@@ -746,7 +779,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             if (t < CF::NTS * CF::NTD) {
                 const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
                 accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + d);
-                st_vec4(&sStS[s][d], accS[i]);
+                if constexpr (!REG_ST)
+                    st_vec4(&sStS[s][d], accS[i]);
             }
         }
         const float *wA = P.wsA + slot * P.S_pad + c.s0;
@@ -828,8 +862,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                 const int t = wave + i * NW;
                 accW[i] = f32x4{0.f, 0.f, 0.f, 0.f};
                 accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (t < CF::NTS * MTC) {
-                    const int ts = t / MTC, tt = t % MTC;
+                if (a_ok(i)) {
+                    const int ts = a_ts(i), tt = a_tt(i);
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
@@ -845,7 +879,14 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     for (int e = 0; e < 4; ++e)
                         accW[i][e] = (float)q4[e] * accI[i][e];
                     st_vec4(&sW[tok][s], accW[i]);
-                    mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
+                    if constexpr (REG_ST) {
+#pragma unroll
+                        for (int kd = 0; kd < DP / 32; ++kd)
+                            EngBF16::mma(accG[i], acc_pair(accS[2 * kd], accS[2 * kd + 1]),
+                                         ld_pair(&sGO[0][0], LDX, tt * 16, 32 * kd, lane));
+                    } else {
+                        mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
+                    }
                 }
             }
 #pragma unroll
@@ -868,8 +909,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 const int t = wave + i * NW;
-                if (t < CF::NTS * MTC) {
-                    const int ts = t / MTC, tt = t % MTC;
+                if (a_ok(i)) {
+                    const int ts = a_ts(i), tt = a_tt(i);
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     EngBF16::mma(accG[i], ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane),
                                  ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
@@ -927,7 +968,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     const int t = wave + i * NW;
                     if (t < CF::NTS * CF::NTD) {
                         const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
-                        st_vec4(&sStS[s][d], accS[i]);
+                        if constexpr (!REG_ST)
+                    st_vec4(&sStS[s][d], accS[i]);
                     }
                 }
             }
@@ -970,9 +1012,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     }
 #pragma unroll
     for (int i = 0; i < TPW_A; ++i) {
-        const int t = wave + i * NW;
-        if (t < CF::NTS * MTC) {
-            const int ts = t / MTC;
+        if (a_ok(i)) {
+            const int ts = a_ts(i);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float v = accGA[i][e];
@@ -1034,7 +1075,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     __shared__ __align__(16) __bf16 sPK[C][LDS];
     __shared__ __align__(16) __bf16 sMg[C][LDC];   // Mg as [tau][t]
     __shared__ __align__(16) __bf16 sMp[C][LDC];   // Mp as [tau][t]
-    __shared__ __align__(16) __bf16 sStS[ST][LDX];
+    __shared__ __align__(16) __bf16 sStS[CF::NTS == NW ? 1 : ST][LDX];  // St rows when not in registers
     __shared__ __align__(16) __bf16 sGU[C][LDG];
     __shared__ __align__(16) float sA0[2][ST];
     __shared__ __align__(16) float sGAe[2][ST];
@@ -1044,6 +1085,13 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
     constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;
+    // A-tiles [ST x C] (A^T, W, gW, gA per bucket tile ts and token tile tt). When the waves
+    // and the bucket tiles match one to one (REG_ST), wave w owns bucket tile w for every token
+    // tile and every head-dim tile of the state, so gW = go St^T takes St from registers.
+    constexpr bool REG_ST = CF::NTS == NW;
+    auto a_ts = [&](int i) { return REG_ST ? wave : (wave + i * NW) / MTC; };
+    auto a_tt = [&](int i) { return REG_ST ? i : (wave + i * NW) % MTC; };
+    auto a_ok = [&](int i) { return REG_ST || (wave + i * NW) < CF::NTS * MTC; };
     constexpr int TPW_O = (CF::NTD * MTC + NW - 1) / NW;
     constexpr int TPW_M = (MTC * MTC + NW - 1) / NW;
     // dv tiles live on the last GVW waves, so that the soft-hash backward of k (on the
@@ -1073,7 +1121,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 const int td = t / CF::NTS, ts = t % CF::NTS;
                 const int d = td * 16 + ((lane >> 4) << 2), s = ts * 16 + (lane & 15);
                 accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + d);
-                st_vec4(&sStS[s][d], accS[i]);
+                if constexpr (!REG_ST)
+                    st_vec4(&sStS[s][d], accS[i]);
                 const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -1163,8 +1212,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             for (int i = 0; i < TPW_A; ++i) {
                 const int t = wave + i * NW;
                 accW[i] = accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (t < CF::NTS * MTC) {
-                    const int ts = t / MTC, tt = t % MTC;
+                if (a_ok(i)) {
+                    const int ts = a_ts(i), tt = a_tt(i);
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
@@ -1180,7 +1229,14 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     for (int e = 0; e < 4; ++e)
                         accW[i][e] = (float)q4[e] * accI[i][e];
                     st_vec4(&sW[tok][s], accW[i]);
-                    mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
+                    if constexpr (REG_ST) {
+#pragma unroll
+                        for (int kd = 0; kd < DP / 32; ++kd)
+                            EngBF16::mma(accG[i], acc_pair(accS[2 * kd], accS[2 * kd + 1]),
+                                         ld_pair(&sGO[0][0], LDX, tt * 16, 32 * kd, lane));
+                    } else {
+                        mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
+                    }
                 }
             }
 #pragma unroll
@@ -1205,8 +1261,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 const int t = wave + i * NW;
-                if (t < CF::NTS * MTC) {
-                    const int ts = t / MTC, tt = t % MTC;
+                if (a_ok(i)) {
+                    const int ts = a_ts(i), tt = a_tt(i);
                     EngBF16::mma(accG[i], ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane),
                                  ld_tr(&sMg[0][0], LDC, 0, tt * 16, lane));
 #pragma unroll
@@ -1249,9 +1305,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 const int t = wave + i * NW;
-                if (t < CF::NTS * MTC && g == G - 1) {
+                if (a_ok(i) && g == G - 1) {
                     // gA^T as a bf16 hi/lo pair, rows [tau][s], for the suffix-scan MFMA
-                    const int ts = t / MTC, tt = t % MTC;
+                    const int ts = a_ts(i), tt = a_tt(i);
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     f32x4 lo;
                     bf16x4 hi;
@@ -1289,8 +1345,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
 #pragma unroll
                 for (int i = 0; i < TPW_A; ++i) {
                     const int t = wave + i * NW;
-                    if (t < CF::NTS * MTC) {
-                        const int ts = t / MTC, tt = t % MTC;
+                    if (a_ok(i)) {
+                        const int ts = a_ts(i), tt = a_tt(i);
                         const int s = ts * 16 + ((lane >> 4) << 2);
                         f32x4 inc = {0.f, 0.f, 0.f, 0.f};
                         const bf16x8 tri = fr.tri_of(tt);
@@ -1316,8 +1372,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
 #pragma unroll
         for (int i = 0; i < TPW_A; ++i) {
             const int t = wave + i * NW;
-            if (t < CF::NTS * MTC) {
-                const int ts = t / MTC, tt = t % MTC;
+            if (a_ok(i)) {
+                const int ts = a_ts(i), tt = a_tt(i);
                 const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
 #pragma unroll
                 for (int kd = 0; kd < DP; kd += 32)
@@ -1334,7 +1390,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             const int t = wave + i * NW;
             if (t < CF::NTS * CF::NTD) {
                 const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
-                st_vec4(&sStS[s][d], accS[i]);
+                if constexpr (!REG_ST)
+                    st_vec4(&sStS[s][d], accS[i]);
             }
         }
         __syncthreads();
