@@ -54,13 +54,15 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Tokens per workgroup: enough blocks for ~2048 workgroups in total, at least
 // four sub-chunks per block; an explicit request is rounded to the sub-chunk.
-int64_t resolve_block(int64_t T, int64_t streams, int C, int64_t req)
+// Tokens per workgroup: `req` rounded to the sub-chunk, or (req = 0) about `target`
+// workgroups per launch with at least 4 sub-chunks each.
+int64_t resolve_block(int64_t T, int64_t streams, int C, int64_t req, int64_t target)
 {
     int64_t cb;
     if (req > 0) {
         cb = rup(req, C);
     } else {
-        const int64_t nb = std::max<int64_t>(1, cdiv(2048, std::max<int64_t>(1, streams)));
+        const int64_t nb = std::max<int64_t>(1, cdiv(target, std::max<int64_t>(1, streams)));
         cb = std::max<int64_t>(4 * C, rup(cdiv(T, nb), C));
     }
     return std::min(cb, rup(T, C));
@@ -106,7 +108,7 @@ int op_geometry(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block, Geo &
     g.n_st = (int)cdiv(S, g.ST);
     g.S_pad = g.n_st * g.ST;
     g.Z = N;
-    g.CB = resolve_block(T, N * g.n_st, g.C, block);
+    g.CB = resolve_block(T, N * g.n_st, g.C, block, 2048);
     g.NB = cdiv(T, g.CB);
     fill_ws_sizes(g);
     return RACE_OK;
@@ -148,7 +150,9 @@ int qkv_geometry(const race_qkv_shape *sh, Geo &g)
     g.Z = (int64_t)sh->B * sh->Hkv;
     if (g.Z > 65535)
         return fail(RACE_ERR_UNSUPPORTED, "race_qkv: B*Hkv = %lld exceeds 65535", (long long)g.Z);
-    g.CB = resolve_block(sh->T, g.Z * g.n_st, g.C, sh->block);
+    // the fused backward kernels hold one workgroup per CU: ~1024 workgroups (4 rounds) keep the
+    // block-state traffic and per-block set-up low while filling the chip
+    g.CB = resolve_block(sh->T, g.Z * g.n_st, g.C, sh->block, 1024);
     g.NB = cdiv(sh->T, g.CB);
     fill_ws_sizes(g);
     return RACE_OK;
@@ -234,10 +238,11 @@ struct ProfScope {
     }
 };
 
-hipError_t prof_block_scan(float *ws, int64_t elems, int NB, int Z, int rev, hipStream_t s)
+hipError_t prof_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB, int Z, int rev,
+                           hipStream_t s)
 {
     ProfScope ps(RACE_PROF_BLOCK_SCAN, s);
-    return launch_block_scan(ws, elems, NB, Z, rev, s);
+    return launch_block_scan(wsB, elemsB, wsA, elemsA, NB, Z, rev, s);
 }
 hipError_t prof_reduce(const float *part, int n_st, int64_t tile, const OutView &out, int B, int H, int T, int D,
                        hipStream_t s)
@@ -429,8 +434,7 @@ static int op_fwd_impl(const float *pK, const float *pQ, const float *V, float *
     P.out = part ? OutView{part, T * D, 0, D, N * T * D, 1} : OutView{out, T * D, 0, D, 0, 1};
     const hipStream_t s = hs(stream);
     RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
-    RACE_TRY(hip_check(prof_block_scan(P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
     RACE_TRY(run_scan_op(K_FWD_READOUT, g, P, s));
     if (part)
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{out, T * D, 0, D, 0, 1},
@@ -473,11 +477,9 @@ static int op_bwd_impl(const float *pK, const float *pQ, const float *V, const f
     const hipStream_t s = hs(stream);
     // forward block states (the backward recomputes them; nothing is saved between calls)
     RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
-    RACE_TRY(hip_check(prof_block_scan(P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
     RACE_TRY(run_scan_op(K_BWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 1, s), "block scan"));
-    RACE_TRY(hip_check(prof_block_scan(P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
     RACE_TRY(run_scan_op(K_BWD_MAIN, g, P, s));
     if (part)
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{gV, T * D, 0, D, 0, 1},
@@ -534,8 +536,7 @@ static int nc_totals(const Geo &g, ScanParams P, const float *w, const float *x,
     P.wsB = wsB;
     P.wsA = wsA;
     RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
-    return hip_check(prof_block_scan(wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan");
+    return hip_check(prof_block_scan(wsB, (int64_t)g.S_pad * g.DP, wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan");
 }
 
 static NcParams nc_params(const Geo &g, int64_t T, int64_t S, int64_t D, float eps)
@@ -717,8 +718,7 @@ int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     }
     const hipStream_t s = hs(stream);
     RACE_TRY(run_scan_qkv(K_FWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 0, s), "block scan"));
-    RACE_TRY(hip_check(prof_block_scan(P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
     RACE_TRY(run_scan_qkv(K_FWD_READOUT, g, P, s));
     if (part)
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, q_elems, to_out(out, out_dtype == RACE_F32), sh->B,
@@ -773,8 +773,7 @@ int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     }
     const hipStream_t s = hs(stream);
     RACE_TRY(run_scan_qkv(K_BWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, (int)g.NB, (int)g.Z, 1, s), "block scan"));
-    RACE_TRY(hip_check(prof_block_scan(P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
     RACE_TRY(run_scan_qkv(K_BWD_MAIN, g, P, s));
     if (g.n_st > 1) {
         RACE_TRY(hip_check(prof_reduce(pq, g.n_st, q_elems, to_out(dq, 0), sh->B, sh->Hq, sh->T, sh->D, s),

@@ -22,27 +22,38 @@ namespace race {
 //   rev = 1: slot b <- sum_{b' >= b} x_b' (inclusive suffix), slot NB <- 0
 constexpr int SCAN_COLS = 64, SCAN_SEGS = 16, SCAN_SEG = 32;
 
-__global__ __launch_bounds__(SCAN_COLS *SCAN_SEGS) void race_block_scan(float *ws, int64_t elems, int NB, int rev)
+// One launch scans two workspaces of the same block count: (wsB, elemsB) with the first
+// ceil(elemsB / SCAN_COLS) workgroups along x, (wsA, elemsA) with the rest.
+template <bool REV>
+__global__ __launch_bounds__(SCAN_COLS *SCAN_SEGS) void race_block_scan(float *wsB, int64_t elemsB, float *wsA,
+                                                                         int64_t elemsA, int NB)
 {
     __shared__ double tot[SCAN_SEGS][SCAN_COLS];
     const int col = threadIdx.x % SCAN_COLS, seg = threadIdx.x / SCAN_COLS;
-    const int64_t e = (int64_t)blockIdx.x * SCAN_COLS + col;
+    const int nbB = (int)((elemsB + SCAN_COLS - 1) / SCAN_COLS);
+    const bool isB = (int)blockIdx.x < nbB;
+    float *ws = isB ? wsB : wsA;
+    const int64_t elems = isB ? elemsB : elemsA;
+    const int64_t e = (int64_t)(isB ? blockIdx.x : blockIdx.x - nbB) * SCAN_COLS + col;
     const bool live = e < elems;
-    float *base = ws + (int64_t)blockIdx.y * (NB + 1) * elems + e;
+    // loads use a clamped column and block index (always inside this stream's workspace), so
+    // they are unconditional and all SCAN_SEG of them are in flight together
+    const int64_t ec = live ? e : elems - 1;
+    float *base = ws + (int64_t)blockIdx.y * (NB + 1) * elems;
     constexpr int SUPER = SCAN_SEGS * SCAN_SEG;
     double carry = 0.0;
     for (int c0 = 0; c0 < NB; c0 += SUPER) {
-        // block index of this thread's i-th element (ascending for rev = 0, descending for rev = 1)
-        const int first = rev ? NB - 1 - c0 - seg * SCAN_SEG : c0 + seg * SCAN_SEG;
-        const int step = rev ? -1 : 1;
+        // block index of this thread's i-th element (ascending, or descending when REV)
+        const int first = REV ? NB - 1 - c0 - seg * SCAN_SEG : c0 + seg * SCAN_SEG;
         float x[SCAN_SEG];
-        double t = 0.0;
 #pragma unroll
         for (int i = 0; i < SCAN_SEG; ++i) {
-            const int b = first + i * step;
-            const bool ok = live && (rev ? (b >= 0 && b <= NB - 1 - c0 - seg * SCAN_SEG) : (b < NB));
-            x[i] = ok ? base[(int64_t)b * elems] : 0.0f;
+            const int b = REV ? first - i : first + i;
+            const bool ok = REV ? b >= 0 : b < NB;
+            const float v = base[(int64_t)(ok ? b : 0) * elems + ec];
+            x[i] = ok ? v : 0.0f;
         }
+        double t = 0.0;
 #pragma unroll
         for (int i = 0; i < SCAN_SEG; ++i)
             t += (double)x[i];
@@ -59,25 +70,32 @@ __global__ __launch_bounds__(SCAN_COLS *SCAN_SEGS) void race_block_scan(float *w
         carry += all;
 #pragma unroll
         for (int i = 0; i < SCAN_SEG; ++i) {
-            const int b = first + i * step;
-            const bool ok = live && (rev ? b >= 0 : b < NB);
-            if (rev)
+            const int b = REV ? first - i : first + i;
+            const bool ok = live && (REV ? b >= 0 : b < NB);
+            if (REV)
                 run += (double)x[i];
             if (ok)
-                base[(int64_t)b * elems] = (float)run;
-            if (!rev)
+                base[(int64_t)b * elems + e] = (float)run;
+            if (!REV)
                 run += (double)x[i];
         }
         __syncthreads();
     }
     if (live && seg == 0)
-        base[(int64_t)NB * elems] = rev ? 0.0f : (float)carry;
+        base[(int64_t)NB * elems + e] = REV ? 0.0f : (float)carry;
 }
 
-hipError_t launch_block_scan(float *ws, int64_t elems, int NB, int Z, int rev, hipStream_t s)
+hipError_t launch_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB, int Z, int rev,
+                             hipStream_t s)
 {
-    const dim3 grid((unsigned)((elems + SCAN_COLS - 1) / SCAN_COLS), (unsigned)Z);
-    hipLaunchKernelGGL(race_block_scan, grid, dim3(SCAN_COLS * SCAN_SEGS), 0, s, ws, elems, NB, rev);
+    const dim3 grid((unsigned)((elemsB + SCAN_COLS - 1) / SCAN_COLS + (elemsA + SCAN_COLS - 1) / SCAN_COLS),
+                    (unsigned)Z);
+    if (rev)
+        hipLaunchKernelGGL(race_block_scan<true>, grid, dim3(SCAN_COLS * SCAN_SEGS), 0, s, wsB, elemsB, wsA, elemsA,
+                           NB);
+    else
+        hipLaunchKernelGGL(race_block_scan<false>, grid, dim3(SCAN_COLS * SCAN_SEGS), 0, s, wsB, elemsB, wsA, elemsA,
+                           NB);
     return hipGetLastError();
 }
 

@@ -33,7 +33,9 @@ constexpr int QKV_C = 32, QKV_NW = 4;
 constexpr int OP_C = 16, OP_NW = 4;
 
 // race_common.hip
-hipError_t launch_block_scan(float *ws, int64_t elems, int NB, int Z, int rev, hipStream_t s);
+// scans wsB [Z][NB+1][elemsB] and wsA [Z][NB+1][elemsA] over the block axis in one launch
+hipError_t launch_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB, int Z, int rev,
+                             hipStream_t s);
 // out[i] (view, f32 or bf16) = sum_{st < n_st} part[st * tile + i] over a [B][H][T][D] box
 hipError_t launch_reduce_partials(const float *part, int n_st, int64_t tile, const OutView &out,
                                   int B, int H, int T, int D, hipStream_t s);
