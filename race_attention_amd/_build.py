@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librace_amd.so")
 ARCH = os.environ.get("RACE_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["race_scan_qkv.hip", "race_fused.hip", "race_scan_op.hip", "race_common.hip", "race_noncausal.hip", "race_abi.cpp"]
+SOURCES = ["race_scan_qkv.hip", "race_fused.hip", "race_fused_gqa.hip", "race_scan_op.hip", "race_common.hip", "race_noncausal.hip", "race_abi.cpp"]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]

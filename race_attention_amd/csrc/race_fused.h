@@ -49,6 +49,9 @@ template <int ST, int DP, int KB, int NW>
 struct FCfg {
     static constexpr int C = 32;
     static constexpr int NTH = NW * 64;
+    // readout waves per SIMD asked of the register allocator: three workgroups of four waves
+    // fit a CU's LDS at the bf16-output tile set of the 128-bucket, 64-dim variant
+    static constexpr int RO_WAVES = (ST == 128 && DP == 64 && NW == 4 && KB >= 3) ? 3 : 1;
     static constexpr int R = 1 << KB;
     static constexpr int LT = ST / R;          // tables per bucket tile
     static constexpr int LTP = ((LT + 3) / 4) * 4;  // tables padded to whole projection tiles
@@ -210,7 +213,10 @@ RACE_DEV bf16x8 ld_tr(const __bf16 *X, int ld, int k0, int m0, int lane)
     return __builtin_bit_cast(bf16x8, r);
 }
 
-// 16-byte chunk loads of one C x DP bf16 token tile (rows t0.., zero beyond nv).
+// 16-byte chunk loads of one C x DP bf16 token tile (rows t0.., nv >= 1 valid rows). Rows at
+// and beyond nv re-read row nv - 1 and are zeroed when stored: the destination registers are
+// never written before the load, so issuing the next tile's loads needs no wait on earlier
+// memory operations.
 template <class CF>
 RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int nv, int tid)
 {
@@ -218,23 +224,34 @@ RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int 
 #pragma unroll
     for (int i = 0; i < CF::PF; ++i) {
         const int idx = tid + i * CF::NTH;
-        const int row = idx / CH, c = idx % CH;
-        r[i] = u32x4{0u, 0u, 0u, 0u};
-        if (idx < CF::CHUNKS && row < nv)
+        const int row = min(idx / CH, nv - 1), c = idx % CH;
+        if (idx < CF::CHUNKS)
             r[i] = *reinterpret_cast<const u32x4 *>(base + row * (int)st + c * 8);
     }
 }
 
+// Tile rows into LDS, rows at and beyond nv as zeros.
 template <class CF>
-RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int tid)
+RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int tid)
 {
     constexpr int CH = CF::CHUNKS / CF::C;
 #pragma unroll
     for (int i = 0; i < CF::PF; ++i) {
         const int idx = tid + i * CF::NTH;
-        if (idx < CF::CHUNKS)
-            *reinterpret_cast<u32x4 *>(dst + (idx / CH) * CF::LDX + (idx % CH) * 8) = r[i];
+        if (idx < CF::CHUNKS) {
+            const bool ok = idx / CH < nv;
+            const u32x4 x = {ok ? r[i][0] : 0u, ok ? r[i][1] : 0u, ok ? r[i][2] : 0u, ok ? r[i][3] : 0u};
+            *reinterpret_cast<u32x4 *>(dst + (idx / CH) * CF::LDX + (idx % CH) * 8) = x;
+        }
     }
+}
+
+// s_waitcnt vmcnt(0): every vector-memory operation of the wave has completed. Issued once
+// after a kernel's prologue loads, so that the uses of those registers inside the sub-chunk
+// loop need no wait there (such a wait would also cover the loop's own prefetch loads).
+RACE_DEV void wait_vmem_all()
+{
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt 0, expcnt 7 (none), lgkmcnt 15 (none)
 }
 
 RACE_DEV const __bf16 *row_ptr(const View &v, int b, int h, int t)
@@ -275,8 +292,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     u32x4 pk[CF::PF], pv[CF::PF];
     tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, min(C, c.t_end - c.t_begin), tid);
     tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, min(C, c.t_end - c.t_begin), tid);
-    tile_store_rows<CF>(&sK[0][0], pk, tid);
-    tile_store_rows<CF>(&sV[0][0], pv, tid);
+    tile_store_rows<CF>(&sK[0][0], pk, min(C, c.t_end - c.t_begin), tid);
+    tile_store_rows<CF>(&sV[0][0], pv, min(C, c.t_end - c.t_begin), tid);
+    wait_vmem_all();
     __syncthreads();
 
     for (int sc = 0; sc < nsub; ++sc) {
@@ -328,9 +346,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
                 EngBF16::mma(accA[i], ones, ld_tr(&sPK[0][0], CF::LDS, 0, tn * 16, lane));
         }
         __syncthreads();
+        wait_vmem_all();
         if (sc + 1 < nsub) {
-            tile_store_rows<CF>(&sK[0][0], pk, tid);
-            tile_store_rows<CF>(&sV[0][0], pv, tid);
+            tile_store_rows<CF>(&sK[0][0], pk, min(C, c.t_end - t0 - C), tid);
+            tile_store_rows<CF>(&sV[0][0], pv, min(C, c.t_end - t0 - C), tid);
         }
         __syncthreads();
     }
@@ -357,8 +376,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
 }
 
 // ============================================================================ forward readout
-template <int ST, int DP, int KB, int NW, bool OUT_F32>
-__global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanParams P)
+template <int ST, int DP, int KB, int NW, bool OUT_F32, bool G1>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(FCfg<ST, DP, KB, NW>::RO_WAVES)))
+void race_fused_fwd_readout(const ScanParams P)
 {
     using CF = FCfg<ST, DP, KB, NW>;
     constexpr int C = CF::C, NTH = CF::NTH, R = CF::R, MTC = CF::MTC;
@@ -416,7 +436,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
             sA0[0][s] = wA[s];
     }
 
-    const int G = P.G;
+    const int G = G1 ? 1 : P.G;  // G1: one query head per kv head, the head loop folds away
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     u32x4 pk[CF::PF], pq[CF::PF], pv[CF::PF];
     {
@@ -424,10 +444,11 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
         tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, nv0, tid);
         tile_load<CF>(pq, row_ptr(P.q, c.b, c.hk * G, c.t_begin), P.q.st, nv0, tid);
         tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, nv0, tid);
-        tile_store_rows<CF>(&sK[0][0], pk, tid);
-        tile_store_rows<CF>(&sQ[0][0], pq, tid);
-        tile_store_rows<CF>(&sV[0][0][0], pv, tid);
+        tile_store_rows<CF>(&sK[0][0], pk, nv0, tid);
+        tile_store_rows<CF>(&sQ[0][0], pq, nv0, tid);
+        tile_store_rows<CF>(&sV[0][0][0], pv, nv0, tid);
     }
+    wait_vmem_all();
     __syncthreads();
 
     f32x4 accA[TPW_A];  // 1/(A+eps), transposed tiles, kept across query heads
@@ -449,7 +470,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
             if (g > 0) {  // further query heads of the group: load q synchronously
                 u32x4 tq[CF::PF];
                 tile_load<CF>(tq, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
-                tile_store_rows<CF>(&sQ[0][0], tq, tid);
+                tile_store_rows<CF>(&sQ[0][0], tq, nv, tid);
                 __syncthreads();
             }
             // ---- P1: soft-hash of k (first head only) and q; previous output rows to HBM
@@ -582,17 +603,18 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_readout(const ScanPara
             prev_t0 = t0;
             prev_nv = nv;
             prev_h = hq;
+            wait_vmem_all();
             if (g == G - 1) {
                 if (more) {
-                    tile_store_rows<CF>(&sK[0][0], pk, tid);
-                    tile_store_rows<CF>(&sV[nxt][0][0], pv, tid);
+                    const int nv1 = min(C, c.t_end - t0 - C);
+                    tile_store_rows<CF>(&sK[0][0], pk, nv1, tid);
+                    tile_store_rows<CF>(&sV[nxt][0][0], pv, nv1, tid);
                     if (G == 1)
-                        tile_store_rows<CF>(&sQ[0][0], pq, tid);
+                        tile_store_rows<CF>(&sQ[0][0], pq, nv1, tid);
                     else {
                         u32x4 tq[CF::PF];
-                        const int t1 = t0 + C;
-                        tile_load<CF>(tq, row_ptr(P.q, c.b, c.hk * G, t1), P.q.st, min(C, c.t_end - t1), tid);
-                        tile_store_rows<CF>(&sQ[0][0], tq, tid);
+                        tile_load<CF>(tq, row_ptr(P.q, c.b, c.hk * G, t0 + C), P.q.st, nv1, tid);
+                        tile_store_rows<CF>(&sQ[0][0], tq, nv1, tid);
                     }
                 }
             }
@@ -719,7 +741,7 @@ struct RowPrefetch {
 // ============================================================================ backward totals
 // Forward-order pass over a block: dq (soft-hash backward of gpQ = gW/(A+eps)) and the
 // block totals of W^T go (into ws2B) and of gA (into ws2A).
-template <int ST, int DP, int KB, int NW, bool OUT_F32>
+template <int ST, int DP, int KB, int NW, bool OUT_F32, bool G1>
 __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParams P)
 {
     using CF = FCfg<ST, DP, KB, NW>;
@@ -792,11 +814,12 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     for (int i = 0; i < TPW_A; ++i)
         accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int G = P.G;
+    const int G = G1 ? 1 : P.G;  // G1: one query head per kv head, the head loop folds away
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     int prev_t0 = -1, prev_nv = 0, prev_h = 0;
     RowPrefetch<CF> pf;
     pf.load(P, c, c.t_begin, c.hk * G, true, tid);
+    wait_vmem_all();
     f32x4 accI[TPW_A];  // 1/(A+eps), A^T tiles
     float uq[TPW_P][4], pq_[TPW_P][R];
     for (int sc = 0; sc < nsub; ++sc) {
@@ -805,13 +828,14 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
         const int cur = sc & 1, nxt = cur ^ 1;
         for (int g = 0; g < G; ++g) {
             const int hq = c.hk * G + g;
-            // ---- P0: rows of this (sub-chunk, head) into LDS
+            // ---- P0: rows of this (sub-chunk, head) into LDS (their loads were issued a step ago)
+            wait_vmem_all();
             if (g == 0) {
-                tile_store_rows<CF>(&sK[0][0], pf.k, tid);
-                tile_store_rows<CF>(&sV[0][0], pf.v, tid);
+                tile_store_rows<CF>(&sK[0][0], pf.k, nv, tid);
+                tile_store_rows<CF>(&sV[0][0], pf.v, nv, tid);
             }
-            tile_store_rows<CF>(&sQ[0][0], pf.q, tid);
-            tile_store_rows<CF>(&sGO[0][0], pf.g, tid);
+            tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
+            tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
             pf.advance(P, c, t0, g, tid);
             __syncthreads();
             // ---- P1: soft-hash of k (first head) -> pK^T ; of q -> pQ (kept in registers)
@@ -1040,7 +1064,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
 // then dk through the soft-hash backward of k and dv directly. Each matrix is held once in
 // LDS, in the orientation its producer writes with vector stores; operands that need the
 // other orientation are read with ld_tr.
-template <int ST, int DP, int KB, int NW, bool OUT_F32>
+template <int ST, int DP, int KB, int NW, bool OUT_F32, bool G1>
 __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams P)
 {
     using CF = FCfg<ST, DP, KB, NW>;
@@ -1137,11 +1161,12 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
         }
     }
 
-    const int G = P.G;
+    const int G = G1 ? 1 : P.G;  // G1: one query head per kv head, the head loop folds away
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     int prev_t0 = -1, prev_nv = 0;
     RowPrefetch<CF> pf;
     pf.load(P, c, c.t_begin, c.hk * G, true, tid);
+    wait_vmem_all();
     f32x4 accI[TPW_A], accPK[TPW_A], accV[TPW_V], accGA[TPW_A];
     float uk[TPW_P][4];
     for (int sc = 0; sc < nsub; ++sc) {
@@ -1155,13 +1180,14 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
         for (int i = 0; i < TPW_V; ++i)
             accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         for (int g = 0; g < G; ++g) {
-            // ---- P0: rows into LDS ; previous sub-chunk's dk, dv out
+            // ---- P0: rows into LDS (their loads were issued a step ago) ; previous sub-chunk's dk, dv out
+            wait_vmem_all();
             if (g == 0) {
-                tile_store_rows<CF>(&sK[0][0], pf.k, tid);
-                tile_store_rows<CF>(&sV[0][0], pf.v, tid);
+                tile_store_rows<CF>(&sK[0][0], pf.k, nv, tid);
+                tile_store_rows<CF>(&sV[0][0], pf.v, nv, tid);
             }
-            tile_store_rows<CF>(&sQ[0][0], pf.q, tid);
-            tile_store_rows<CF>(&sGO[0][0], pf.g, tid);
+            tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
+            tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
             pf.advance(P, c, t0, g, tid);
             if (g == 0 && prev_t0 >= 0) {
                 store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);

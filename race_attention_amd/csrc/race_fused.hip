@@ -1,42 +1,8 @@
-// Instantiations and launch of the fused bf16 q/k/v kernels (race_fused.h).
-#include "race_fused.h"
-#include "race_launch.h"
+// Instantiations of the fused bf16 q/k/v kernels for one query head per kv head, and the
+// variant dispatch (grouped query heads go to race_fused_gqa.hip).
+#include "race_fused_launch.h"
 
 namespace race {
-
-template <int ST, int DP, int KB>
-static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStream_t s)
-{
-    // forward kernels: 4 waves (fewer, larger per-wave tile sets measured faster);
-    // backward kernels: 8 waves (two per SIMD to overlap LDS and MFMA latency)
-    constexpr int NW = FUSED_NW_FWD;
-    constexpr int NWB = FUSED_NW_BWD;
-    const dim3 block((k == K_FWD_TOTALS || k == K_FWD_READOUT ? NW : NWB) * 64);
-    if (k == K_FWD_TOTALS)
-        hipLaunchKernelGGL((race_fused_fwd_totals<ST, DP, KB, NW>), grid, block, 0, s, P);
-    else if (k == K_FWD_READOUT && P.out.f32)
-        hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, true>), grid, block, 0, s, P);
-    else if (k == K_FWD_READOUT)
-        hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, false>), grid, block, 0, s, P);
-    else if (k == K_BWD_TOTALS && P.dq.f32)
-        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, true>), grid, block, 0, s, P);
-    else if (k == K_BWD_TOTALS)
-        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, false>), grid, block, 0, s, P);
-    else if (k == K_BWD_MAIN && P.dk.f32 != P.dv.f32)
-        return hipErrorInvalidValue;
-    else if (k == K_BWD_MAIN && P.dk.f32)
-        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, true>), grid, block, 0, s, P);
-    else if (k == K_BWD_MAIN)
-        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, false>), grid, block, 0, s, P);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-
-#define RACE_FUSED_VARIANTS(X) \
-    X(32, 64, 2) X(32, 64, 3) X(32, 64, 4) X(64, 64, 2) X(64, 64, 3) X(64, 64, 4) \
-    X(128, 64, 2) X(128, 64, 3) X(128, 64, 4) X(32, 128, 2) X(32, 128, 3) X(32, 128, 4) \
-    X(64, 128, 2) X(64, 128, 3) X(64, 128, 4)
 
 bool fused_variant_exists(int ST, int DP, int KB)
 {
@@ -48,7 +14,9 @@ bool fused_variant_exists(int ST, int DP, int KB)
 
 hipError_t launch_fused(ScanKernel k, int ST, int DP, int KB, const ScanParams &P, dim3 grid, hipStream_t s)
 {
-#define X(a, b, c) if (ST == a && DP == b && KB == c) return launch_fv<a, b, c>(k, P, grid, s);
+    if (P.G != 1 && k != K_FWD_TOTALS)
+        return launch_fused_gqa(k, ST, DP, KB, P, grid, s);
+#define X(a, b, c) if (ST == a && DP == b && KB == c) return launch_fv<a, b, c, true>(k, P, grid, s);
     RACE_FUSED_VARIANTS(X)
 #undef X
     return hipErrorInvalidValue;

@@ -1,0 +1,51 @@
+// Launch of one compiled variant of the fused bf16 q/k/v kernels (race_fused.h). Included by
+// race_fused.hip (one query head per kv head) and race_fused_gqa.hip (grouped query heads),
+// which compile the two specialisations in separate translation units.
+#pragma once
+#include "race_fused.h"
+#include "race_launch.h"
+
+namespace race {
+
+#define RACE_FUSED_VARIANTS(X) \
+    X(32, 64, 2) X(32, 64, 3) X(32, 64, 4) X(64, 64, 2) X(64, 64, 3) X(64, 64, 4) \
+    X(128, 64, 2) X(128, 64, 3) X(128, 64, 4) X(32, 128, 2) X(32, 128, 3) X(32, 128, 4) \
+    X(64, 128, 2) X(64, 128, 3) X(64, 128, 4)
+
+template <int ST, int DP, int KB, bool G1>
+static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStream_t s)
+{
+    // forward kernels: 4 waves (fewer, larger per-wave tile sets measured faster);
+    // backward kernels: 8 waves (two per SIMD to overlap LDS and MFMA latency)
+    constexpr int NW = FUSED_NW_FWD;
+    constexpr int NWB = FUSED_NW_BWD;
+    const dim3 block((k == K_FWD_TOTALS || k == K_FWD_READOUT ? NW : NWB) * 64);
+    if (k == K_FWD_TOTALS) {
+        // no query heads involved: compiled once, in the single-head unit
+        if constexpr (G1)
+            hipLaunchKernelGGL((race_fused_fwd_totals<ST, DP, KB, NW>), grid, block, 0, s, P);
+        else
+            return hipErrorInvalidValue;
+    } else if (k == K_FWD_READOUT && P.out.f32)
+        hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, true, G1>), grid, block, 0, s, P);
+    else if (k == K_FWD_READOUT)
+        hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, false, G1>), grid, block, 0, s, P);
+    else if (k == K_BWD_TOTALS && P.dq.f32)
+        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, true, G1>), grid, block, 0, s, P);
+    else if (k == K_BWD_TOTALS)
+        hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, false, G1>), grid, block, 0, s, P);
+    else if (k == K_BWD_MAIN && P.dk.f32 != P.dv.f32)
+        return hipErrorInvalidValue;
+    else if (k == K_BWD_MAIN && P.dk.f32)
+        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, true, G1>), grid, block, 0, s, P);
+    else if (k == K_BWD_MAIN)
+        hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, false, G1>), grid, block, 0, s, P);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// grouped-query-head variants (race_fused_gqa.hip)
+hipError_t launch_fused_gqa(ScanKernel k, int ST, int DP, int KB, const ScanParams &P, dim3 grid, hipStream_t s);
+
+}  // namespace race
