@@ -1064,6 +1064,12 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
 // then dk through the soft-hash backward of k and dv directly. Each matrix is held once in
 // LDS, in the orientation its producer writes with vector stores; operands that need the
 // other orientation are read with ld_tr.
+//
+// Software pipeline over sub-chunks: each sub-chunk is a head (H0 rows, H1 soft-hash, H2
+// A/W/gW/Mg, H3, H4) and a tail (T5 gpK, T6 soft-hash backward of k and dv, T7 dk). The
+// tail of sub-chunk i runs in the barrier phases of H0, H1, H2 of sub-chunk i+1, so a
+// sub-chunk costs five barrier phases. Arrays that both sides touch are double buffered by
+// sub-chunk parity (v rows, pK) or kept apart (dS^T, the dk and dv staging).
 template <int ST, int DP, int KB, int NW, bool OUT_F32, bool G1>
 __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams P)
 {
@@ -1072,35 +1078,27 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG, LDF = ST + 4;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
-    // LDS regions shared by arrays with disjoint lifetimes:
-    //   uKQ: k, q rows (load -> projection) and dS^T [d][s] (last head -> gpK / gv updates);
-    //   uPW: pQ, W rows (projection -> Mp) and the dk, dv staging (sub-chunk end -> next load);
-    //   uF:  gA^T hi/lo parts as [tau][s] (last head -> suffix scan), then gpK rows in fp32.
-    constexpr int SZ_K = C * LDX * 2, SZ_DST = DP * LDS * 2;
-    constexpr int SZ_PQ = C * LDS * 2, SZ_O = C * LDO * (int)sizeof(OT);
-    constexpr int SZ_KQ = 2 * SZ_K > SZ_DST ? 2 * SZ_K : SZ_DST;
-    constexpr int SZ_PW = 2 * SZ_PQ > 2 * SZ_O ? 2 * SZ_PQ : 2 * SZ_O;
+    // uF holds gpK rows in fp32 (T5 -> T6) and the gA^T hi/lo parts (H3 -> H4): disjoint phases
+    constexpr int SZ_PQ = C * LDS * 2;
     constexpr int SZ_F = C * LDF * 4 > 2 * SZ_PQ ? C * LDF * 4 : 2 * SZ_PQ;
-    __shared__ __align__(16) char uKQ[SZ_KQ];
-    __shared__ __align__(16) char uPW[SZ_PW];
     __shared__ __align__(16) char uF[SZ_F];
-    __bf16(*sK)[LDX] = reinterpret_cast<__bf16(*)[LDX]>(uKQ);
-    __bf16(*sQ)[LDX] = reinterpret_cast<__bf16(*)[LDX]>(uKQ + SZ_K);
-    __bf16(*sdSt)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uKQ);
-    __bf16(*sPQ)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uPW);
-    __bf16(*sW)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uPW + SZ_PQ);
-    OT(*sOk)[LDO] = reinterpret_cast<OT(*)[LDO]>(uPW);
-    OT(*sOv)[LDO] = reinterpret_cast<OT(*)[LDO]>(uPW + SZ_O);
     float(*sF)[LDF] = reinterpret_cast<float(*)[LDF]>(uF);
     __bf16(*sGAh)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uF);
     __bf16(*sGAl)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uF + SZ_PQ);
-    __shared__ __align__(16) __bf16 sV[C][LDX];
+    __shared__ __align__(16) __bf16 sK[C][LDX];
+    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
     __shared__ __align__(16) __bf16 sGO[C][LDX];
-    __shared__ __align__(16) __bf16 sPK[C][LDS];
-    __shared__ __align__(16) __bf16 sMg[C][LDC];   // Mg as [tau][t]
-    __shared__ __align__(16) __bf16 sMp[C][LDC];   // Mp as [tau][t]
+    __shared__ __align__(16) __bf16 sPK[2][C][LDS];  // by sub-chunk parity
+    __shared__ __align__(16) __bf16 sPQ[C][LDS];
+    __shared__ __align__(16) __bf16 sW[C][LDS];
+    __shared__ __align__(16) __bf16 sdSt[DP][LDS];   // dS^T [d][s]
+    __shared__ __align__(16) __bf16 sMg[C][LDC];     // Mg as [tau][t]
+    __shared__ __align__(16) __bf16 sMp[C][LDC];     // Mp as [tau][t]
     __shared__ __align__(16) __bf16 sStS[CF::NTS == NW ? 1 : ST][LDX];  // St rows when not in registers
     __shared__ __align__(16) __bf16 sGU[C][LDG];
+    __shared__ __align__(16) OT sOk[C][LDO];
+    __shared__ __align__(16) OT sOv[C][LDO];
     __shared__ __align__(16) float sA0[2][ST];
     __shared__ __align__(16) float sGAe[2][ST];
 
@@ -1127,7 +1125,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     fr.load(P, c.l0, c.Lt, lane, wave);
     BackFrags<CF, DP, TPW_O> bk;
     bk.load(P, c.l0, c.Lt, lane, wave, MTC);
-    zero_lds_bf16(&sPK[0][0], C * LDS, tid, NTH);
+    zero_lds_bf16(&sPK[0][0][0], 2 * C * LDS, tid, NTH);
     zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
 
     // St^T at the block start (lane: col s, rows d); suffix dS from the block start
@@ -1163,38 +1161,146 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
 
     const int G = G1 ? 1 : P.G;  // G1: one query head per kv head, the head loop folds away
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
-    int prev_t0 = -1, prev_nv = 0;
     RowPrefetch<CF> pf;
     pf.load(P, c, c.t_begin, c.hk * G, true, tid);
     wait_vmem_all();
     f32x4 accI[TPW_A], accPK[TPW_A], accV[TPW_V], accGA[TPW_A];
     float uk[TPW_P][4];
+#pragma unroll
+    for (int i = 0; i < TPW_A; ++i)
+        accPK[i] = accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < TPW_V; ++i)
+        accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // ---- T5 (sub-chunk buffer pb): gpK^T += dS V^T + gAhat -> sF ; St -> sStS
+    auto tail5 = [&](int pb) {
+#pragma unroll
+        for (int i = 0; i < TPW_A; ++i) {
+            if (a_ok(i)) {
+                const int ts = a_ts(i), tt = a_tt(i);
+                const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+#pragma unroll
+                for (int kd = 0; kd < DP; kd += 32)
+                    EngBF16::mma(accPK[i], ld_tr(&sdSt[0][0], LDS, kd, ts * 16, lane),
+                                 ld_k(&sV[pb][0][0], LDX, tt * 16, kd, lane));
+                f32x4 x;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    x[e] = accPK[i][e] + accGA[i][e];
+                *reinterpret_cast<f32x4 *>(&sF[tok][s]) = x;
+                accPK[i] = accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TPW_S; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTS * CF::NTD) {
+                const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
+                if constexpr (!REG_ST)
+                    st_vec4(&sStS[s][d], accS[i]);
+            }
+        }
+    };
+    // ---- T6 (buffer pb, nv_ valid tokens, k soft bits ukp): gv^T += dS^T pK^T -> sOv ;
+    //      soft-hash backward of k -> sGU
+    auto tail6 = [&](int pb, int nv_, const float (&ukp)[TPW_P][4]) {
+#pragma unroll
+        for (int i = 0; i < TPW_V; ++i) {
+            const int t = wv + i * GVW;
+            if (wv >= 0 && t < CF::NTD * MTC) {
+                const int td = t / MTC, tt = t % MTC;
+                mma_ab<ST, LDS, LDS>(accV[i], &sdSt[0][0], td * 16, &sPK[pb][0][0], tt * 16, lane);
+                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sOv[tok][d]) = accV[i];
+                else
+                    st_vec4(&sOv[tok][d], accV[i]);
+            }
+            accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < TPW_P; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NPT) {
+                const int jt = t / MTC, tt = t % MTC;
+                const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                if (table < CF::LT) {
+                    float gp[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int h = 0; h < R / 4; ++h) {
+                        const f32x4 x = *reinterpret_cast<const f32x4 *>(&sF[tok][table * R + 4 * h]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            gp[4 * h + e] = x[e];
+                    }
+                    float pk[R];
+                    expand_ct<KB>(ukp[i], pk);
+                    const bool ok = tok < nv_ && table < c.Lt;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        pk[r] = ok ? pk[r] : 0.0f;
+                    softhash_bwd_ct<KB>(ukp[i], pk, gp, P.scale, P.inv_scale, gproj);
+                    bf16x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
+                    *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
+                }
+            }
+        }
+    };
+    // ---- T7: dk^T = P gproj^T -> sOk
+    auto tail7 = [&]() {
+#pragma unroll
+        for (int i = 0; i < TPW_O; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTD * MTC) {
+                const int td = t / MTC, tt = t % MTC;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                const __bf16 *pb = &sGU[0][0] + (tt * 16 + (lane & 15)) * LDG + (lane >> 4) * 8;
+#pragma unroll
+                for (int kb = 0; kb < (CF::LKP + 31) / 32; ++kb)
+                    EngBF16::mma(acc, bk.f[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sOk[tok][d]) = acc;
+                else
+                    st_vec4(&sOk[tok][d], acc);
+            }
+        }
+    };
+
+    int prev_t0 = -1, prev_nv = 0;
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
         const int cur = sc & 1, nxt = cur ^ 1;
-#pragma unroll
-        for (int i = 0; i < TPW_A; ++i)
-            accPK[i] = accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < TPW_V; ++i)
-            accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const bool tail = sc > 0;  // the previous sub-chunk's tail runs in H0..H2 (first head)
         for (int g = 0; g < G; ++g) {
-            // ---- P0: rows into LDS (their loads were issued a step ago) ; previous sub-chunk's dk, dv out
+            // ---- H0: rows into LDS (their loads were issued a step ago) | T5 of the previous sub-chunk
             wait_vmem_all();
             if (g == 0) {
                 tile_store_rows<CF>(&sK[0][0], pf.k, nv, tid);
-                tile_store_rows<CF>(&sV[0][0], pf.v, nv, tid);
+                tile_store_rows<CF>(&sV[cur][0][0], pf.v, nv, tid);
             }
             tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
             tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
             pf.advance(P, c, t0, g, tid);
-            if (g == 0 && prev_t0 >= 0) {
-                store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
-                store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
-            }
+            if (g == 0 && tail)
+                tail5(nxt);
             __syncthreads();
-            // ---- P1: soft-hash of k (first head) -> pK ; of q -> pQ   (rows [t][s])
+            // ---- H1: soft-hash of k (first head) -> pK ; of q -> pQ   (rows [t][s])
+            //          | T6 of the previous sub-chunk
+            if (g == 0 && tail) {
+                float ukp[TPW_P][4];
+#pragma unroll
+                for (int i = 0; i < TPW_P; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        ukp[i][e] = uk[i][e];
+                tail6(nxt, prev_nv, ukp);
+            }
 #pragma unroll
             for (int i = 0; i < TPW_P; ++i) {
                 const int t = wave + i * NW;
@@ -1214,7 +1320,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     for (int r = 0; r < R; ++r)
                         p[r] = ok ? p[r] : 0.0f;
                     if (table < CF::LT) {
-                        __bf16 *row = isk ? &sPK[tok][table * R] : &sPQ[tok][table * R];
+                        __bf16 *row = isk ? &sPK[cur][tok][table * R] : &sPQ[tok][table * R];
 #pragma unroll
                         for (int h = 0; h < R / 4; ++h) {
                             bf16x4 w;
@@ -1232,18 +1338,19 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 }
             }
             __syncthreads();
-            // ---- P2: A^T (first head) ; W -> sW ; gW^T = St go^T ; Mg -> sMg
+            // ---- H2: A^T (first head) ; W -> sW ; gW^T = St go^T ; Mg -> sMg | T7 of the previous sub-chunk
+            if (g == 0 && tail)
+                tail7();
             f32x4 accW[TPW_A], accG[TPW_A];
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
-                const int t = wave + i * NW;
                 accW[i] = accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
                 if (a_ok(i)) {
                     const int ts = a_ts(i), tt = a_tt(i);
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
-                        EngBF16::mma(a, ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
+                        EngBF16::mma(a, ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
                         if (tt == MTC - 1 && (lane & 15) == 15)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
@@ -1272,7 +1379,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     // Mg[t][tau] = go_t . v_tau (tau <= t): rows t (tile ta), cols tau (tile tb)
                     const int ta = t / MTC, tb = t % MTC;
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<DP, LDX, LDX>(acc, &sGO[0][0], ta * 16, &sV[0][0], tb * 16, lane);
+                    mma_ab<DP, LDX, LDX>(acc, &sGO[0][0], ta * 16, &sV[cur][0][0], tb * 16, lane);
                     const int r0 = ta * 16 + ((lane >> 4) << 2), c0 = tb * 16 + (lane & 15);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -1282,14 +1389,18 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 }
             }
             __syncthreads();
-            // ---- P3: gW^T += pK^T Mg^T ; gA^T ; gpK^T += W^T Mg ; Mp -> sMp ;
-            //          dS -= W^T go ; St^T += V^T pK (last head) ; gA^T hi/lo -> [tau][s]
+            // ---- H3: gW^T += pK^T Mg^T ; gA^T ; gpK^T += W^T Mg ; Mp -> sMp ;
+            //          dS -= W^T go ; St^T += V^T pK (last head) ; gA^T hi/lo -> [tau][s] ;
+            //          previous sub-chunk's dk, dv out
+            if (g == 0 && tail) {
+                store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
+                store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
+            }
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
-                const int t = wave + i * NW;
                 if (a_ok(i)) {
                     const int ts = a_ts(i), tt = a_tt(i);
-                    EngBF16::mma(accG[i], ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane),
+                    EngBF16::mma(accG[i], ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane),
                                  ld_tr(&sMg[0][0], LDC, 0, tt * 16, lane));
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -1305,7 +1416,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     // Mp[tau][t] = pK_tau . W_t (t >= tau): rows t (tile ta), cols tau (tile tb)
                     const int ta = t / MTC, tb = t % MTC;
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<ST, LDS, LDS>(acc, &sW[0][0], ta * 16, &sPK[0][0], tb * 16, lane);
+                    mma_ab<ST, LDS, LDS>(acc, &sW[0][0], ta * 16, &sPK[cur][0][0], tb * 16, lane);
                     const int r0 = ta * 16 + ((lane >> 4) << 2), c0 = tb * 16 + (lane & 15);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -1324,13 +1435,12 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                                  ld_tr(&sGO[0][0], LDX, 0, td * 16, lane));
                     // St^T[d][s] += sum_t V[t][d] pK[t][s]
                     if (g == G - 1)
-                        EngBF16::mma(accS[i], ld_tr(&sV[0][0], LDX, 0, td * 16, lane),
-                                     ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane));
+                        EngBF16::mma(accS[i], ld_tr(&sV[cur][0][0], LDX, 0, td * 16, lane),
+                                     ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane));
                 }
             }
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
-                const int t = wave + i * NW;
                 if (a_ok(i) && g == G - 1) {
                     // gA^T as a bf16 hi/lo pair, rows [tau][s], for the suffix-scan MFMA
                     const int ts = a_ts(i), tt = a_tt(i);
@@ -1347,7 +1457,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 }
             }
             __syncthreads();
-            // ---- P4: gv^T += go^T Mp^T ; (last head) dS^T -> sdSt, gAhat scan
+            // ---- H4: gv^T += go^T Mp^T ; (last head) dS^T -> sdSt, gAhat scan
 #pragma unroll
             for (int i = 0; i < TPW_V; ++i) {
                 const int t = wv + i * GVW;
@@ -1370,7 +1480,6 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 // term is added back in fp32; the sub-chunk total seeds the next sub-chunk.
 #pragma unroll
                 for (int i = 0; i < TPW_A; ++i) {
-                    const int t = wave + i * NW;
                     if (a_ok(i)) {
                         const int ts = a_ts(i), tt = a_tt(i);
                         const int s = ts * 16 + ((lane >> 4) << 2);
@@ -1390,104 +1499,19 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     }
                 }
             }
-            if (g + 1 < G)
-                __syncthreads();
-        }
-        __syncthreads();
-        // ---- P5: gpK^T += dS V^T + gAhat -> sF ; St -> sStS
-#pragma unroll
-        for (int i = 0; i < TPW_A; ++i) {
-            const int t = wave + i * NW;
-            if (a_ok(i)) {
-                const int ts = a_ts(i), tt = a_tt(i);
-                const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-#pragma unroll
-                for (int kd = 0; kd < DP; kd += 32)
-                    EngBF16::mma(accPK[i], ld_tr(&sdSt[0][0], LDS, kd, ts * 16, lane),
-                                 ld_k(&sV[0][0], LDX, tt * 16, kd, lane));
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    accPK[i][e] += accGA[i][e];
-                *reinterpret_cast<f32x4 *>(&sF[tok][s]) = accPK[i];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < TPW_S; ++i) {
-            const int t = wave + i * NW;
-            if (t < CF::NTS * CF::NTD) {
-                const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
-                if constexpr (!REG_ST)
-                    st_vec4(&sStS[s][d], accS[i]);
-            }
-        }
-        __syncthreads();
-        // ---- P6: soft-hash backward of k -> sGU ; gv^T += dS^T pK^T -> sOv
-#pragma unroll
-        for (int i = 0; i < TPW_V; ++i) {
-            const int t = wv + i * GVW;
-            if (wv >= 0 && t < CF::NTD * MTC) {
-                const int td = t / MTC, tt = t % MTC;
-                mma_ab<ST, LDS, LDS>(accV[i], &sdSt[0][0], td * 16, &sPK[0][0], tt * 16, lane);
-                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                if constexpr (OUT_F32)
-                    *reinterpret_cast<f32x4 *>(&sOv[tok][d]) = accV[i];
-                else
-                    st_vec4(&sOv[tok][d], accV[i]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < TPW_P; ++i) {
-            const int t = wave + i * NW;
-            if (t < CF::NPT) {
-                const int jt = t / MTC, tt = t % MTC;
-                const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
-                if (table < CF::LT) {
-                    float gp[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int h = 0; h < R / 4; ++h) {
-                        const f32x4 x = *reinterpret_cast<const f32x4 *>(&sF[tok][table * R + 4 * h]);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            gp[4 * h + e] = x[e];
-                    }
-                    float pk[R];
-                    expand_ct<KB>(uk[i], pk);
-                    const bool ok = tok < nv && table < c.Lt;
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        pk[r] = ok ? pk[r] : 0.0f;
-                    softhash_bwd_ct<KB>(uk[i], pk, gp, P.scale, P.inv_scale, gproj);
-                    bf16x4 w;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
-                    *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
-                }
-            }
-        }
-        __syncthreads();
-        // ---- P7: dk^T = P gproj^T -> sOk
-#pragma unroll
-        for (int i = 0; i < TPW_O; ++i) {
-            const int t = wave + i * NW;
-            if (t < CF::NTD * MTC) {
-                const int td = t / MTC, tt = t % MTC;
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                const __bf16 *pb = &sGU[0][0] + (tt * 16 + (lane & 15)) * LDG + (lane >> 4) * 8;
-#pragma unroll
-                for (int kb = 0; kb < (CF::LKP + 31) / 32; ++kb)
-                    EngBF16::mma(acc, bk.f[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
-                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                if constexpr (OUT_F32)
-                    *reinterpret_cast<f32x4 *>(&sOk[tok][d]) = acc;
-                else
-                    st_vec4(&sOk[tok][d], acc);
-            }
+            __syncthreads();
         }
         prev_t0 = t0;
         prev_nv = nv;
-        __syncthreads();
     }
+    // tail of the last sub-chunk
+    const int pb = (nsub - 1) & 1;
+    tail5(pb);
+    __syncthreads();
+    tail6(pb, prev_nv, uk);
+    __syncthreads();
+    tail7();
+    __syncthreads();
     store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
     store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
 }
