@@ -26,23 +26,41 @@ RACE_DEV void zero_lds_bf16(__bf16 *p, int n, int tid, int nth)
         p[i] = (__bf16)0.0f;
 }
 
+// Soft-hash of one table from its projections x[0..4) (rows >= KB are unused):
+//   u_k = tanh(x_k) / scale,  a_k = exp(-2 u_k),
+//   p[r] = prod_k sigmoid(2 c_k(r) u_k) = prod_{k: bit k of r clear} a_k / prod_k (1 + a_k),
+// since sigmoid(2u) = 1 / (1 + a) and sigmoid(-2u) = a / (1 + a): one reciprocal per table.
+// Bit k = 0 is the most significant bit of r (corner order of itertools.product([-1, 1])).
+// mask = 0 gives all-zero probabilities (padding tokens and tables).
 template <int KB>
-RACE_DEV void expand_ct(const float *u, float *p)
+RACE_DEV void probs_from_u(const float *u, float mask, float *p)
 {
-    p[0] = 1.0f;
+    float a[KB], den = 1.0f;
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
-        const float e = __expf(-2.0f * u[k]);
-        const float s1 = frcp(1.0f + e);
-        const float s0 = e * s1;
+        a[k] = __expf(-2.0f * u[k]);
+        den *= 1.0f + a[k];
+    }
+    p[0] = frcp(den) * mask;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
         const int n = 1 << k;
 #pragma unroll
         for (int i = n - 1; i >= 0; --i) {
             const float pi = p[i];
-            p[2 * i + 1] = pi * s1;
-            p[2 * i] = pi * s0;
+            p[2 * i + 1] = pi;
+            p[2 * i] = pi * a[k];
         }
     }
+}
+
+template <int KB>
+RACE_DEV void softhash_fwd_ct(const f32x4 &x, float inv_scale, bool ok, float *u, float *p)
+{
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        u[e] = tanh_f(x[e]) * inv_scale;
+    probs_from_u<KB>(u, ok ? 1.0f : 0.0f, p);
 }
 
 template <int ST, int DP, int KB, int NW>
@@ -312,20 +330,17 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
             if (t < CF::NPT) {
                 const int jt = t / CF::MTC, tt = t % CF::MTC;
                 const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, &sK[0][0], tt, lane);
-                float u[4], p[R];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    u[e] = tanh_f(acc[e]) * P.inv_scale;
-                expand_ct<KB>(u, p);
                 const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                 const bool ok = tok < nv && table < c.Lt;
+                float u[4], p[R];
+                softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
                 if (table < CF::LT) {
 #pragma unroll
                     for (int h = 0; h < R / 4; ++h) {
                         bf16x4 w;
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            w[e] = (__bf16)(ok ? p[4 * h + e] : 0.0f);
+                            w[e] = (__bf16)p[4 * h + e];
                         *reinterpret_cast<bf16x4 *>(&sPK[tok][table * R + 4 * h]) = w;
                     }
                 }
@@ -482,18 +497,15 @@ void race_fused_fwd_readout(const ScanParams P)
                     const int tq_ = isk ? t : t - CF::NPT;
                     const int jt = tq_ / MTC, tt = tq_ % MTC;
                     const f32x4 acc = proj_T<CF, DP, TPW_P0>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
-                    float u[4], p[R];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        u[e] = tanh_f(acc[e]) * P.inv_scale;
-                    expand_ct<KB>(u, p);
                     const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                     const bool ok = tok < nv && table < c.Lt;
+                    float u[4], p[R];
+                    softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
                     bf16x8 v8[R / 8 > 0 ? R / 8 : 1];
                     bf16x4 v4;
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        const __bf16 x = (__bf16)(ok ? p[r] : 0.0f);
+                        const __bf16 x = (__bf16)p[r];
                         if (R >= 8)
                             v8[r / 8][r % 8] = x;
                         else
@@ -679,13 +691,22 @@ RACE_DEV void softhash_bwd_ct(const float *u, const float *p, const float *gp, f
 #pragma unroll
     for (int r = 0; r < R; ++r)
         dot += p[r] * gp[r];
+    // gz_r = dL/dz_r (softmax backward); gu_k = sum_r sign_k(r) gz_r, sign +1 where bit k of r
+    // is set: a butterfly over the bits from the least significant one, pair sums feed the
+    // next level and pair differences sum to that bit's gu
+    float z[R];
 #pragma unroll
-    for (int k = 0; k < KB; ++k) {
+    for (int r = 0; r < R; ++r)
+        z[r] = p[r] * (gp[r] - dot);
+#pragma unroll
+    for (int lvl = 0; lvl < KB; ++lvl) {
+        const int k = KB - 1 - lvl;  // bit k of r is the lowest remaining index bit
+        const int n = R >> (lvl + 1);
         float gu = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float gz = p[r] * (gp[r] - dot);
-            gu += ((r >> (KB - 1 - k)) & 1) ? gz : -gz;
+        for (int i = 0; i < n; ++i) {
+            gu += z[2 * i + 1] - z[2 * i];
+            z[i] = z[2 * i] + z[2 * i + 1];
         }
         const float th = u[k] * scale;
         gproj[k] = gu * inv_scale * (1.0f - th * th);
@@ -847,16 +868,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     const int tq_ = isk ? t : t - CF::NPT;
                     const int jt = tq_ / MTC, tt = tq_ % MTC;
                     const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
-                    float u[4], p[R];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        u[e] = tanh_f(acc[e]) * P.inv_scale;
-                    expand_ct<KB>(u, p);
                     const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                     const bool ok = tok < nv && table < c.Lt;
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        p[r] = ok ? p[r] : 0.0f;
+                    float u[4], p[R];
+                    softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
                     if (table < CF::LT) {
                         __bf16 *row = isk ? &sPK[tok][table * R] : &sPQ[tok][table * R];
 #pragma unroll
@@ -1235,11 +1250,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                             gp[4 * h + e] = x[e];
                     }
                     float pk[R];
-                    expand_ct<KB>(ukp[i], pk);
-                    const bool ok = tok < nv_ && table < c.Lt;
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        pk[r] = ok ? pk[r] : 0.0f;
+                    probs_from_u<KB>(ukp[i], tok < nv_ && table < c.Lt ? 1.0f : 0.0f, pk);
                     softhash_bwd_ct<KB>(ukp[i], pk, gp, P.scale, P.inv_scale, gproj);
                     bf16x4 w;
 #pragma unroll
@@ -1309,16 +1320,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     const int tq_ = isk ? t : t - CF::NPT;
                     const int jt = tq_ / MTC, tt = tq_ % MTC;
                     const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
-                    float u[4], p[R];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        u[e] = tanh_f(acc[e]) * P.inv_scale;
-                    expand_ct<KB>(u, p);
                     const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                     const bool ok = tok < nv && table < c.Lt;
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        p[r] = ok ? p[r] : 0.0f;
+                    float u[4], p[R];
+                    softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
                     if (table < CF::LT) {
                         __bf16 *row = isk ? &sPK[cur][tok][table * R] : &sPQ[tok][table * R];
 #pragma unroll
