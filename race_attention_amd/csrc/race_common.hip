@@ -136,7 +136,7 @@ hipError_t launch_reduce_partials(const float *part, int n_st, int64_t tile, con
 // generic over K <= 8 (probabilities written directly, O(R*K) per table).
 RACE_DEV void sigm_pair(float u, float &s0, float &s1)
 {
-    const float e = __expf(-2.0f * u);
+    const float e = __expf(-2.0f * sig_arg(u));
     s1 = frcp(1.0f + e);
     s0 = e * s1;
 }

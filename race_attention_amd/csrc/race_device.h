@@ -140,6 +140,13 @@ RACE_DEV float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
 // tanh(x) = 1 - 2 / (exp(2x) + 1); saturates to +-1 through exp overflow/underflow
 RACE_DEV float tanh_f(float x) { return 1.0f - 2.0f * frcp(__expf(2.0f * x) + 1.0f); }
 
+// Argument of a corner sigmoid, clamped to |u| <= lim: u = tanh(proj) / scale grows without
+// bound as scale -> 0, and exp(-2u) must stay finite so that 1 / (1 + e) and e / (1 + e) never
+// meet inf * 0. With lim = 40 the clamp moves a probability by at most e^-80 (the per-bit
+// sigmoids below); the fused kernels' one-denominator form needs (1 + e^(2 lim))^4 finite and
+// uses lim = 10 (a shift of at most 2e-9, below fp32 resolution next to 1).
+RACE_DEV float sig_arg(float u, float lim = 40.0f) { return __builtin_amdgcn_fmed3f(u, -lim, lim); }
+
 // Probabilities of one hash table from its K soft bits u[0..K):
 // p[r] = prod_k sigmoid(2 c_k(r) u_k), r < 2^K (K <= 4).  Bit k = 0 is the most
 // significant bit of r, matching itertools.product([-1, 1], repeat=K).
@@ -149,7 +156,7 @@ RACE_DEV void expand_probs(const float *u, int K, float p[16])
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         if (k < K) {
-            const float e = __expf(-2.0f * u[k]);
+            const float e = __expf(-2.0f * sig_arg(u[k]));
             const float s1 = frcp(1.0f + e);  // sigmoid(+2u): corner bit set
             const float s0 = e * s1;          // sigmoid(-2u): corner bit clear
             const int n = 1 << k;

@@ -31,14 +31,15 @@ RACE_DEV void zero_lds_bf16(__bf16 *p, int n, int tid, int nth)
 //   p[r] = prod_k sigmoid(2 c_k(r) u_k) = prod_{k: bit k of r clear} a_k / prod_k (1 + a_k),
 // since sigmoid(2u) = 1 / (1 + a) and sigmoid(-2u) = a / (1 + a): one reciprocal per table.
 // Bit k = 0 is the most significant bit of r (corner order of itertools.product([-1, 1])).
-// mask = 0 gives all-zero probabilities (padding tokens and tables).
+// mask = 0 gives all-zero probabilities (padding tokens and tables). With |u| clamped to 10
+// (sig_arg) every factor is finite: den <= (1 + e^20)^4 < 2^117.
 template <int KB>
 RACE_DEV void probs_from_u(const float *u, float mask, float *p)
 {
     float a[KB], den = 1.0f;
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
-        a[k] = __expf(-2.0f * u[k]);
+        a[k] = __expf(-2.0f * sig_arg(u[k], 10.0f));
         den *= 1.0f + a[k];
     }
     p[0] = frcp(den) * mask;

@@ -81,3 +81,40 @@ def test_batched_ace_noncausal_module(dev, share, M):
         r4 = orc.batched_ace_nc_ref(pack(K4), pack(V4), pack(Q4), ace.planes_T.cpu(), ace.protos_T.cpu(), L, K,
                                     share, lt.detach()).mean(0).permute(0, 2, 1, 3)
     check("race_attention", o4, r4, TOL)
+
+
+def test_soft_hash_extreme_temperature(dev):
+    """Temperature at BatchedACE's lower clamp (scale 0.01, scaling/benchmark_time.py:111):
+    u = tanh(proj) / scale reaches +-100, where exp(-2u) overflows fp32 unless the corner
+    sigmoid's argument is bounded. Probabilities, d/dX and d/dscale stay finite and match the
+    fp64 softmax form (scaling/race_common.py:68-72)."""
+    from race_attention_amd import build_planes_protos
+    from race_attention_amd.noncausal import SoftHashTempFn
+    L, Kb, D = 4, 3, 64
+    planes_T, protos_T = build_planes_protos(D, Kb, L, 1, device=dev, seed=3)
+    g = torch.Generator().manual_seed(5)
+    X = torch.randn(1, 2, 300, D, generator=g) * 2
+    gp = torch.randn(2, 300, L << Kb, generator=g)
+    xd = X.to(dev).requires_grad_(True)
+    sd = torch.tensor(0.01, device=dev, requires_grad=True)
+    p = SoftHashTempFn.apply(xd, planes_T, L, Kb, 1, False, sd)
+    p.backward(gp.to(dev))
+    X64 = X.double().requires_grad_(True)
+    s64 = torch.tensor(0.01, dtype=torch.float64, requires_grad=True)
+    ref, _, _, _ = orc.soft_hash_probs(X64.detach(), X64, X64.detach(), planes_T.cpu(), protos_T.cpu(), L, Kb,
+                                       scale=s64)  # first output: probabilities of the K argument
+    ref.backward(gp.double())
+    assert torch.isfinite(p).all() and torch.isfinite(xd.grad).all() and torch.isfinite(sd.grad).all()
+    assert float(ref.detach().abs().max()) > 0.99  # saturated corners: the regime under test
+    # At this temperature the reference formula itself, evaluated in fp32 (torch softmax form,
+    # the reference's arithmetic), is ~1e-4 from fp64 (1 - tanh^2 near saturation, x 1/scale):
+    # the bar is twice that fp32 floor, and never looser than it would be at 1e-4.
+    X32 = X.clone().requires_grad_(True)
+    s32 = torch.tensor(0.01, requires_grad=True)
+    proj32 = (X32.reshape(-1, D) @ planes_T.cpu()).view(2, 300, L, Kb)
+    r32 = torch.softmax((proj32.tanh() / s32) @ protos_T.cpu(), -1).reshape(2, 300, -1)
+    r32.backward(gp)
+    for name, got, g32, g64 in (("probs", p, r32.detach(), ref.detach()), ("dX", xd.grad, X32.grad, X64.grad),
+                                ("dscale", sd.grad.reshape(1), s32.grad.reshape(1), s64.grad.reshape(1))):
+        floor = orc.relerr(g32, g64)
+        check(name, got, g64, max(TOL, 2.0 * floor))
