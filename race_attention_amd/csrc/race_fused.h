@@ -26,20 +26,31 @@ RACE_DEV void zero_lds_bf16(__bf16 *p, int n, int tid, int nth)
         p[i] = (__bf16)0.0f;
 }
 
-// Soft-hash of one table from its projections x[0..4) (rows >= KB are unused):
-//   u_k = tanh(x_k) / scale,  a_k = exp(-2 u_k),
+// Soft-hash of one table from its projections x[0..4) (rows >= KB are unused), in the exp2
+// domain of the hardware exponential:
+//   th_k = tanh(x_k),  u_k = th_k / scale,  a_k = exp(-2 u_k) = 2^(th_k * coef),
+//   coef = -2 log2(e) / scale,
 //   p[r] = prod_k sigmoid(2 c_k(r) u_k) = prod_{k: bit k of r clear} a_k / prod_k (1 + a_k),
 // since sigmoid(2u) = 1 / (1 + a) and sigmoid(-2u) = a / (1 + a): one reciprocal per table.
 // Bit k = 0 is the most significant bit of r (corner order of itertools.product([-1, 1])).
-// mask = 0 gives all-zero probabilities (padding tokens and tables). With |u| clamped to 10
-// (sig_arg) every factor is finite: den <= (1 + e^20)^4 < 2^117.
+// The exponent is clamped to |u| <= 10: sigmoid(20) differs from 1 by 2e-9 (below fp32
+// resolution next to 1) and den <= (1 + e^20)^4 < 2^117 stays finite at any temperature.
+// mask = 0 gives all-zero probabilities (padding tokens and tables).
+constexpr float SH_LOG2E = 1.4426950408889634f;
+constexpr float SH_CLAMP = 20.0f * SH_LOG2E;
+
+RACE_DEV float tanh_exp2(float x)
+{
+    return 1.0f - 2.0f * frcp(__builtin_amdgcn_exp2f(x * (2.0f * SH_LOG2E)) + 1.0f);
+}
+
 template <int KB>
-RACE_DEV void probs_from_u(const float *u, float mask, float *p)
+RACE_DEV void probs_from_th(const float *th, float coef, float mask, float *p)
 {
     float a[KB], den = 1.0f;
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
-        a[k] = __expf(-2.0f * sig_arg(u[k], 10.0f));
+        a[k] = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(th[k] * coef, -SH_CLAMP, SH_CLAMP));
         den *= 1.0f + a[k];
     }
     p[0] = frcp(den) * mask;
@@ -55,13 +66,14 @@ RACE_DEV void probs_from_u(const float *u, float mask, float *p)
     }
 }
 
+// th[0..4) = tanh of the projections (zero beyond KB) and the table's probabilities
 template <int KB>
-RACE_DEV void softhash_fwd_ct(const f32x4 &x, float inv_scale, bool ok, float *u, float *p)
+RACE_DEV void softhash_fwd_ct(const f32x4 &x, float coef, bool ok, float *th, float *p)
 {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        u[e] = tanh_f(x[e]) * inv_scale;
-    probs_from_u<KB>(u, ok ? 1.0f : 0.0f, p);
+        th[e] = e < KB ? tanh_exp2(x[e]) : 0.0f;
+    probs_from_th<KB>(th, coef, ok ? 1.0f : 0.0f, p);
 }
 
 template <int ST, int DP, int KB, int NW>
@@ -289,6 +301,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     __shared__ __align__(16) __bf16 sPK[C][CF::LDS];  // rows [t][s]
 
     const Ctx c = make_ctx(P, ST);
+    const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
     constexpr int TPW_A = (CF::NTS + NW - 1) / NW;
@@ -333,8 +346,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
                 const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, &sK[0][0], tt, lane);
                 const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                 const bool ok = tok < nv && table < c.Lt;
-                float u[4], p[R];
-                softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
+                float th[4], p[R];
+                softhash_fwd_ct<KB>(acc, coef, ok, th, p);
                 if (table < CF::LT) {
 #pragma unroll
                     for (int h = 0; h < R / 4; ++h) {
@@ -412,6 +425,7 @@ void race_fused_fwd_readout(const ScanParams P)
     __shared__ __align__(16) float sA0[2][ST];
 
     const Ctx c = make_ctx(P, ST);
+    const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
     constexpr int TPW_P0 = (2 * CF::NPT + NW - 1) / NW;
     FusedFrags<CF, DP, TPW_P0> fr;
@@ -500,8 +514,8 @@ void race_fused_fwd_readout(const ScanParams P)
                     const f32x4 acc = proj_T<CF, DP, TPW_P0>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
                     const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                     const bool ok = tok < nv && table < c.Lt;
-                    float u[4], p[R];
-                    softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
+                    float th[4], p[R];
+                    softhash_fwd_ct<KB>(acc, coef, ok, th, p);
                     bf16x8 v8[R / 8 > 0 ? R / 8 : 1];
                     bf16x4 v4;
 #pragma unroll
@@ -684,8 +698,7 @@ struct BackFrags {
 // Soft-hash backward of one (token, table): gproj[k] = dL/dproj_k from the table's
 // probabilities p, its soft bits u and dL/dp (softmax + corner + tanh chain).
 template <int KB>
-RACE_DEV void softhash_bwd_ct(const float *u, const float *p, const float *gp, float scale, float inv_scale,
-                              float *gproj)
+RACE_DEV void softhash_bwd_ct(const float *th, const float *p, const float *gp, float inv_scale, float *gproj)
 {
     constexpr int R = 1 << KB;
     float dot = 0.0f;
@@ -709,8 +722,7 @@ RACE_DEV void softhash_bwd_ct(const float *u, const float *p, const float *gp, f
             gu += z[2 * i + 1] - z[2 * i];
             z[i] = z[2 * i] + z[2 * i + 1];
         }
-        const float th = u[k] * scale;
-        gproj[k] = gu * inv_scale * (1.0f - th * th);
+        gproj[k] = gu * inv_scale * (1.0f - th[k] * th[k]);
     }
 }
 
@@ -787,6 +799,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     __shared__ float sGAred[ST];
 
     const Ctx c = make_ctx(P, ST);
+    const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
     constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;   // k then q projection tiles
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
@@ -843,7 +856,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     pf.load(P, c, c.t_begin, c.hk * G, true, tid);
     wait_vmem_all();
     f32x4 accI[TPW_A];  // 1/(A+eps), A^T tiles
-    float uq[TPW_P][4], pq_[TPW_P][R];
+    float thq[TPW_P][4], pq_[TPW_P][R];
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -871,8 +884,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
                     const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                     const bool ok = tok < nv && table < c.Lt;
-                    float u[4], p[R];
-                    softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
+                    float th[4], p[R];
+                    softhash_fwd_ct<KB>(acc, coef, ok, th, p);
                     if (table < CF::LT) {
                         __bf16 *row = isk ? &sPK[tok][table * R] : &sPQ[tok][table * R];
 #pragma unroll
@@ -886,7 +899,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     }
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        uq[i][e] = u[e];
+                        thq[i][e] = th[e];
 #pragma unroll
                     for (int r = 0; r < R; ++r)
                         pq_[i][r] = p[r];
@@ -993,7 +1006,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                             for (int e = 0; e < 4; ++e)
                                 gp[4 * h + e] = x[e];
                         }
-                        softhash_bwd_ct<KB>(uq[i], pq_[i], gp, P.scale, P.inv_scale, gproj);
+                        softhash_bwd_ct<KB>(thq[i], pq_[i], gp, P.inv_scale, gproj);
                         bf16x4 w;
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
@@ -1119,6 +1132,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     __shared__ __align__(16) float sGAe[2][ST];
 
     const Ctx c = make_ctx(P, ST);
+    const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
     constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
@@ -1181,7 +1195,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     pf.load(P, c, c.t_begin, c.hk * G, true, tid);
     wait_vmem_all();
     f32x4 accI[TPW_A], accPK[TPW_A], accV[TPW_V], accGA[TPW_A];
-    float uk[TPW_P][4];
+    float thk[TPW_P][4];
 #pragma unroll
     for (int i = 0; i < TPW_A; ++i)
         accPK[i] = accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1218,9 +1232,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             }
         }
     };
-    // ---- T6 (buffer pb, nv_ valid tokens, k soft bits ukp): gv^T += dS^T pK^T -> sOv ;
+    // ---- T6 (buffer pb, nv_ valid tokens, tanh of the k projections thkp): gv^T += dS^T pK^T -> sOv ;
     //      soft-hash backward of k -> sGU
-    auto tail6 = [&](int pb, int nv_, const float (&ukp)[TPW_P][4]) {
+    auto tail6 = [&](int pb, int nv_, const float (&thkp)[TPW_P][4]) {
 #pragma unroll
         for (int i = 0; i < TPW_V; ++i) {
             const int t = wv + i * GVW;
@@ -1251,8 +1265,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                             gp[4 * h + e] = x[e];
                     }
                     float pk[R];
-                    probs_from_u<KB>(ukp[i], tok < nv_ && table < c.Lt ? 1.0f : 0.0f, pk);
-                    softhash_bwd_ct<KB>(ukp[i], pk, gp, P.scale, P.inv_scale, gproj);
+                    probs_from_th<KB>(thkp[i], coef, tok < nv_ && table < c.Lt ? 1.0f : 0.0f, pk);
+                    softhash_bwd_ct<KB>(thkp[i], pk, gp, P.inv_scale, gproj);
                     bf16x4 w;
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -1305,13 +1319,13 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             // ---- H1: soft-hash of k (first head) -> pK ; of q -> pQ   (rows [t][s])
             //          | T6 of the previous sub-chunk
             if (g == 0 && tail) {
-                float ukp[TPW_P][4];
+                float thkp[TPW_P][4];
 #pragma unroll
                 for (int i = 0; i < TPW_P; ++i)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        ukp[i][e] = uk[i][e];
-                tail6(nxt, prev_nv, ukp);
+                        thkp[i][e] = thk[i][e];
+                tail6(nxt, prev_nv, thkp);
             }
 #pragma unroll
             for (int i = 0; i < TPW_P; ++i) {
@@ -1323,8 +1337,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     const f32x4 acc = proj_T<CF, DP, TPW_P>(fr, i, isk ? &sK[0][0] : &sQ[0][0], tt, lane);
                     const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
                     const bool ok = tok < nv && table < c.Lt;
-                    float u[4], p[R];
-                    softhash_fwd_ct<KB>(acc, P.inv_scale, ok, u, p);
+                    float th[4], p[R];
+                    softhash_fwd_ct<KB>(acc, coef, ok, th, p);
                     if (table < CF::LT) {
                         __bf16 *row = isk ? &sPK[cur][tok][table * R] : &sPQ[tok][table * R];
 #pragma unroll
@@ -1339,7 +1353,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     if (isk) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            uk[i][e] = u[e];
+                            thk[i][e] = th[e];
                     }
                 }
             }
@@ -1514,7 +1528,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     const int pb = (nsub - 1) & 1;
     tail5(pb);
     __syncthreads();
-    tail6(pb, prev_nv, uk);
+    tail6(pb, prev_nv, thk);
     __syncthreads();
     tail7();
     __syncthreads();
