@@ -857,13 +857,79 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     wait_vmem_all();
     f32x4 accI[TPW_A];  // 1/(A+eps), A^T tiles
     float thq[TPW_P][4], pq_[TPW_P][R];
+
+    // Software pipeline over (sub-chunk, head) steps: the tail of a step (T4 soft-hash
+    // backward of q, T5 dq, the dq rows out) runs in the barrier phases P0, P1, P2 of the next
+    // step, so a step costs four barrier phases.
+    // ---- T4: soft-hash backward of q -> gproj -> sGU ; (after the last head) St -> sStS
+    auto tail4 = [&](bool st_rows) {
+#pragma unroll
+        for (int i = 0; i < TPW_P; ++i) {
+            const int t = wave + i * NW;
+            if (t >= CF::NPT && t < 2 * CF::NPT) {
+                const int tq_ = t - CF::NPT;
+                const int jt = tq_ / MTC, tt = tq_ % MTC;
+                const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+                if (table < CF::LT) {
+                    float gp[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int h = 0; h < R / 4; ++h) {
+                        const f32x4 x = *reinterpret_cast<const f32x4 *>(&sGP[tok][table * R + 4 * h]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            gp[4 * h + e] = x[e];
+                    }
+                    softhash_bwd_ct<KB>(thq[i], pq_[i], gp, P.inv_scale, gproj);
+                    bf16x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
+                    *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
+                }
+            }
+        }
+        if (st_rows) {
+#pragma unroll
+            for (int i = 0; i < TPW_S; ++i) {
+                const int t = wave + i * NW;
+                if (t < CF::NTS * CF::NTD) {
+                    const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
+                    if constexpr (!REG_ST)
+                        st_vec4(&sStS[s][d], accS[i]);
+                }
+            }
+        }
+    };
+    // ---- T5: dq^T = P gproj^T -> sO
+    auto tail5 = [&]() {
+#pragma unroll
+        for (int i = 0; i < TPW_O; ++i) {
+            const int t = wave + i * NW;
+            if (t < CF::NTD * MTC) {
+                const int td = t / MTC, tt = t % MTC;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                const __bf16 *pb = &sGU[0][0] + (tt * 16 + (lane & 15)) * LDG + (lane >> 4) * 8;
+#pragma unroll
+                for (int kb = 0; kb < (CF::LKP + 31) / 32; ++kb)
+                    EngBF16::mma(acc, bk.f[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+                const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sO[tok][d]) = acc;
+                else
+                    st_vec4(&sO[tok][d], acc);
+            }
+        }
+    };
+
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
         const int cur = sc & 1, nxt = cur ^ 1;
         for (int g = 0; g < G; ++g) {
             const int hq = c.hk * G + g;
+            const bool tail = prev_t0 >= 0;
             // ---- P0: rows of this (sub-chunk, head) into LDS (their loads were issued a step ago)
+            //          | T4 of the previous step
             wait_vmem_all();
             if (g == 0) {
                 tile_store_rows<CF>(&sK[0][0], pf.k, nv, tid);
@@ -872,8 +938,13 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
             tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
             pf.advance(P, c, t0, g, tid);
+            if (tail)
+                tail4(g == 0);
             __syncthreads();
             // ---- P1: soft-hash of k (first head) -> pK^T ; of q -> pQ (kept in registers)
+            //          | T5 of the previous step
+            if (tail)
+                tail5();
 #pragma unroll
             for (int i = 0; i < TPW_P; ++i) {
                 const int t = wave + i * NW;
@@ -905,10 +976,11 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                         pq_[i][r] = p[r];
                 }
             }
-            if (prev_t0 >= 0)
-                store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
             __syncthreads();
             // ---- P2: A^T scan (first head) -> 1/(A+eps); W -> sW ; Mg -> sMg ; gW^T = St go^T
+            //          | the previous step's dq rows out
+            if (tail)
+                store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
             f32x4 accW[TPW_A], accG[TPW_A];
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
@@ -988,69 +1060,17 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                                      ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane));
                 }
             }
-            __syncthreads();
-            // ---- P4: soft-hash backward of q -> gproj -> sGU ; new St -> sStS (last head)
-#pragma unroll
-            for (int i = 0; i < TPW_P; ++i) {
-                const int t = wave + i * NW;
-                if (t >= CF::NPT && t < 2 * CF::NPT) {
-                    const int tq_ = t - CF::NPT;
-                    const int jt = tq_ / MTC, tt = tq_ % MTC;
-                    const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
-                    if (table < CF::LT) {
-                        float gp[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int h = 0; h < R / 4; ++h) {
-                            const f32x4 x = *reinterpret_cast<const f32x4 *>(&sGP[tok][table * R + 4 * h]);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                gp[4 * h + e] = x[e];
-                        }
-                        softhash_bwd_ct<KB>(thq[i], pq_[i], gp, P.inv_scale, gproj);
-                        bf16x4 w;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
-                        *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
-                    }
-                }
-            }
-            if (g == G - 1) {
-#pragma unroll
-                for (int i = 0; i < TPW_S; ++i) {
-                    const int t = wave + i * NW;
-                    if (t < CF::NTS * CF::NTD) {
-                        const int d = (t / CF::NTS) * 16 + ((lane >> 4) << 2), s = (t % CF::NTS) * 16 + (lane & 15);
-                        if constexpr (!REG_ST)
-                    st_vec4(&sStS[s][d], accS[i]);
-                    }
-                }
-            }
-            __syncthreads();
-            // ---- P5: dq^T = P gproj^T -> sO
-#pragma unroll
-            for (int i = 0; i < TPW_O; ++i) {
-                const int t = wave + i * NW;
-                if (t < CF::NTD * MTC) {
-                    const int td = t / MTC, tt = t % MTC;
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    const __bf16 *pb = &sGU[0][0] + (tt * 16 + (lane & 15)) * LDG + (lane >> 4) * 8;
-#pragma unroll
-                    for (int kb = 0; kb < (CF::LKP + 31) / 32; ++kb)
-                        EngBF16::mma(acc, bk.f[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
-                    const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                    if constexpr (OUT_F32)
-                        *reinterpret_cast<f32x4 *>(&sO[tok][d]) = acc;
-                    else
-                        st_vec4(&sO[tok][d], acc);
-                }
-            }
             prev_t0 = t0;
             prev_nv = nv;
             prev_h = hq;
             __syncthreads();
         }
     }
+    // tail of the last step
+    tail4(false);
+    __syncthreads();
+    tail5();
+    __syncthreads();
     store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
 
     // block totals: dS^T -> ws2B [s][d] ; gA (sum over tokens) -> ws2A
