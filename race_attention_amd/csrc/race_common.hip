@@ -14,21 +14,22 @@ namespace race {
 
 // ============================================================================ block scan
 // One workgroup owns SCAN_COLS consecutive state elements of one stream and walks the
-// blocks in super-chunks of SCAN_SEGS * SCAN_SEG blocks. Each thread loads one segment
-// of SCAN_SEG blocks at once (independent loads, one memory latency per super-chunk),
-// the segment totals are combined through LDS, and each thread writes its segment's
-// running sums from its offset. Sums run in fp64 and are rounded once per output.
+// blocks in super-chunks of SEGS * SEG blocks. Each thread loads one segment of SEG blocks
+// at once (independent loads, one memory latency per super-chunk), the segment totals are
+// combined through LDS, and each thread writes its segment's running sums from its offset.
+// Sums run in fp64 and are rounded once per output. (SEGS, SEG) follow the block count, so a
+// scan over few blocks launches few threads.
 //   rev = 0: slot b <- sum_{b' < b} x_b' (exclusive), slot NB <- total
 //   rev = 1: slot b <- sum_{b' >= b} x_b' (inclusive suffix), slot NB <- 0
-constexpr int SCAN_COLS = 64, SCAN_SEGS = 16, SCAN_SEG = 32;
+constexpr int SCAN_COLS = 64;
 
 // One launch scans two workspaces of the same block count: (wsB, elemsB) with the first
 // ceil(elemsB / SCAN_COLS) workgroups along x, (wsA, elemsA) with the rest.
-template <bool REV>
-__global__ __launch_bounds__(SCAN_COLS *SCAN_SEGS) void race_block_scan(float *wsB, int64_t elemsB, float *wsA,
-                                                                         int64_t elemsA, int NB)
+template <bool REV, int SEGS, int SEG>
+__global__ __launch_bounds__(SCAN_COLS *SEGS) void race_block_scan(float *wsB, int64_t elemsB, float *wsA,
+                                                                  int64_t elemsA, int NB)
 {
-    __shared__ double tot[SCAN_SEGS][SCAN_COLS];
+    __shared__ double tot[SEGS][SCAN_COLS];
     const int col = threadIdx.x % SCAN_COLS, seg = threadIdx.x / SCAN_COLS;
     const int nbB = (int)((elemsB + SCAN_COLS - 1) / SCAN_COLS);
     const bool isB = (int)blockIdx.x < nbB;
@@ -37,39 +38,50 @@ __global__ __launch_bounds__(SCAN_COLS *SCAN_SEGS) void race_block_scan(float *w
     const int64_t e = (int64_t)(isB ? blockIdx.x : blockIdx.x - nbB) * SCAN_COLS + col;
     const bool live = e < elems;
     // loads use a clamped column and block index (always inside this stream's workspace), so
-    // they are unconditional and all SCAN_SEG of them are in flight together
+    // they are unconditional and all SEG of them are in flight together; addresses are formed
+    // per load, so no per-block pointer stays live
     const int64_t ec = live ? e : elems - 1;
     float *base = ws + (int64_t)blockIdx.y * (NB + 1) * elems;
-    constexpr int SUPER = SCAN_SEGS * SCAN_SEG;
+    constexpr int SUPER = SEGS * SEG;
     double carry = 0.0;
     for (int c0 = 0; c0 < NB; c0 += SUPER) {
         // block index of this thread's i-th element (ascending, or descending when REV)
-        const int first = REV ? NB - 1 - c0 - seg * SCAN_SEG : c0 + seg * SCAN_SEG;
-        float x[SCAN_SEG];
+        const int first = REV ? NB - 1 - c0 - seg * SEG : c0 + seg * SEG;
+        float x[SEG];
 #pragma unroll
-        for (int i = 0; i < SCAN_SEG; ++i) {
+        for (int i = 0; i < SEG; ++i) {
             const int b = REV ? first - i : first + i;
-            const bool ok = REV ? b >= 0 : b < NB;
-            const float v = base[(int64_t)(ok ? b : 0) * elems + ec];
-            x[i] = ok ? v : 0.0f;
+            const int bc = REV ? max(b, 0) : min(b, NB - 1);
+            x[i] = base[(int64_t)bc * elems + ec];
+        }
+#pragma unroll
+        for (int i = 0; i < SEG; ++i) {
+            const int b = REV ? first - i : first + i;
+            if (REV ? b < 0 : b >= NB)
+                x[i] = 0.0f;
         }
         double t = 0.0;
 #pragma unroll
-        for (int i = 0; i < SCAN_SEG; ++i)
+        for (int i = 0; i < SEG; ++i)
             t += (double)x[i];
-        tot[seg][col] = t;
-        __syncthreads();
-        double run = carry, all = 0.0;
+        if (SEGS > 1) {
+            tot[seg][col] = t;
+            __syncthreads();
+        }
+        double run = carry, all = t;
+        if (SEGS > 1) {
+            all = 0.0;
 #pragma unroll
-        for (int j = 0; j < SCAN_SEGS; ++j) {
-            const double v = tot[j][col];
-            if (j < seg)
-                run += v;
-            all += v;
+            for (int j = 0; j < SEGS; ++j) {
+                const double v = tot[j][col];
+                if (j < seg)
+                    run += v;
+                all += v;
+            }
         }
         carry += all;
 #pragma unroll
-        for (int i = 0; i < SCAN_SEG; ++i) {
+        for (int i = 0; i < SEG; ++i) {
             const int b = REV ? first - i : first + i;
             const bool ok = live && (REV ? b >= 0 : b < NB);
             if (REV)
@@ -79,10 +91,33 @@ __global__ __launch_bounds__(SCAN_COLS *SCAN_SEGS) void race_block_scan(float *w
             if (!REV)
                 run += (double)x[i];
         }
-        __syncthreads();
+        if (SEGS > 1)
+            __syncthreads();
     }
     if (live && seg == 0)
         base[(int64_t)NB * elems + e] = REV ? 0.0f : (float)carry;
+}
+
+template <bool REV, int SEGS, int SEG>
+static void launch_scan_cfg(dim3 grid, float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB,
+                            hipStream_t s)
+{
+    hipLaunchKernelGGL((race_block_scan<REV, SEGS, SEG>), grid, dim3(SCAN_COLS * SEGS), 0, s, wsB, elemsB, wsA,
+                       elemsA, NB);
+}
+
+template <bool REV>
+static void launch_scan_dir(dim3 grid, float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB,
+                            hipStream_t s)
+{
+    if (NB <= 8)
+        launch_scan_cfg<REV, 1, 8>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+    else if (NB <= 32)
+        launch_scan_cfg<REV, 4, 8>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+    else if (NB <= 128)
+        launch_scan_cfg<REV, 16, 8>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+    else  // super-chunks of 256 blocks (32 loads per thread would not fit the registers)
+        launch_scan_cfg<REV, 16, 16>(grid, wsB, elemsB, wsA, elemsA, NB, s);
 }
 
 hipError_t launch_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB, int Z, int rev,
@@ -91,11 +126,9 @@ hipError_t launch_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t ele
     const dim3 grid((unsigned)((elemsB + SCAN_COLS - 1) / SCAN_COLS + (elemsA + SCAN_COLS - 1) / SCAN_COLS),
                     (unsigned)Z);
     if (rev)
-        hipLaunchKernelGGL(race_block_scan<true>, grid, dim3(SCAN_COLS * SCAN_SEGS), 0, s, wsB, elemsB, wsA, elemsA,
-                           NB);
+        launch_scan_dir<true>(grid, wsB, elemsB, wsA, elemsA, NB, s);
     else
-        hipLaunchKernelGGL(race_block_scan<false>, grid, dim3(SCAN_COLS * SCAN_SEGS), 0, s, wsB, elemsB, wsA, elemsA,
-                           NB);
+        launch_scan_dir<false>(grid, wsB, elemsB, wsA, elemsA, NB, s);
     return hipGetLastError();
 }
 
