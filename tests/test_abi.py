@@ -37,7 +37,12 @@ def test_abi_version_and_sizes():
     assert lib.race_abi_version() == 1
     sh = _lib.QKVShape(1, 4, 4, 1 << 20, 64, 8, 4, 8.0, 1e-6, 0)
     state = lib.race_qkv_state_bytes(sh)
-    assert 40e6 < state < 200e6  # per-block states, not [T,S] probabilities
+    # per-block states (A and St, fp32, one slot per block plus the final state), not [T,S]
+    # probabilities: a whole number of (S, D+1) slots for each of the Z = 4 streams
+    slot = 4 * 128 * (64 + 1) * 4
+    nslots = round(state / slot)
+    assert abs(state - nslots * slot) < 512 and 2 <= nslots <= (1 << 20) // 256 + 1
+    assert state < 0.02 * 2 * 4 * (1 << 20) * 128 * 4
     assert lib.race_qkv_scratch_bytes(sh, 0) == 0  # S = 128 fits one bucket tile
     assert lib.race_qkv_scratch_bytes(sh, 1) >= state
     assert lib.race_op_workspace_bytes(16, 2048, 128, 64, 0, 1) > 0
