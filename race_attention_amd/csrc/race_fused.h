@@ -277,6 +277,17 @@ RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int
     }
 }
 
+// Inclusive prefix sum over the 16 lanes of each DPP row (Hillis-Steele with row_shr and zero
+// fill: four VALU adds, no LDS).
+RACE_DEV float row_scan16(float v)
+{
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xF, 0xF, true));
+    return v;
+}
+
 // s_waitcnt vmcnt(0): every vector-memory operation of the wave has completed. Issued once
 // after a kernel's prologue loads, so that the uses of those registers inside the sub-chunk
 // loop need no wait there (such a wait would also cover the loop's own prefetch loads).
@@ -1479,21 +1490,46 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                                      ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane));
                 }
             }
+            if constexpr (REG_ST) {
+                if (g == G - 1) {
+                    // gAhat_t = gAhat_start - sum_{tau < t} gA_tau. Wave w holds bucket tile w for
+                    // both token tiles, and a token tile's 16 tokens lie along the 16 lanes of a DPP
+                    // row: fp32 row scans, with token tile 0's row total carried into tile 1; the
+                    // sub-chunk total seeds the next sub-chunk.
+                    const int s = wave * 16 + ((lane >> 4) << 2);
+                    const f32x4 g0 = *reinterpret_cast<const f32x4 *>(&sGAe[cur][s]);
+                    f32x4 carry = {0.f, 0.f, 0.f, 0.f}, gend;
 #pragma unroll
-            for (int i = 0; i < TPW_A; ++i) {
-                if (a_ok(i) && g == G - 1) {
-                    // gA^T as a bf16 hi/lo pair, rows [tau][s], for the suffix-scan MFMA
-                    const int ts = a_ts(i), tt = a_tt(i);
-                    const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                    f32x4 lo;
-                    bf16x4 hi;
+                    for (int i = 0; i < TPW_A; ++i) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        hi[e] = (__bf16)accGA[i][e];
-                        lo[e] = accGA[i][e] - (float)hi[e];
+                        for (int e = 0; e < 4; ++e) {
+                            const float inc = row_scan16(accGA[i][e]) + carry[e];
+                            gend[e] = g0[e] - inc;
+                            accGA[i][e] += gend[e];
+                            if (i + 1 < TPW_A)
+                                carry[e] = __shfl(inc, (lane & 48) | 15, 64);
+                        }
                     }
-                    *reinterpret_cast<bf16x4 *>(&sGAh[tok][s]) = hi;
-                    st_vec4(&sGAl[tok][s], lo);
+                    if ((lane & 15) == 15)
+                        *reinterpret_cast<f32x4 *>(&sGAe[nxt][s]) = gend;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < TPW_A; ++i) {
+                    if (a_ok(i) && g == G - 1) {
+                        // gA^T as a bf16 hi/lo pair, rows [tau][s], for the suffix-scan MFMA
+                        const int ts = a_ts(i), tt = a_tt(i);
+                        const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                        f32x4 lo;
+                        bf16x4 hi;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            hi[e] = (__bf16)accGA[i][e];
+                            lo[e] = accGA[i][e] - (float)hi[e];
+                        }
+                        *reinterpret_cast<bf16x4 *>(&sGAh[tok][s]) = hi;
+                        st_vec4(&sGAl[tok][s], lo);
+                    }
                 }
             }
             __syncthreads();
@@ -1515,12 +1551,13 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                         st_vec4(&sdSt[d2][s2], accD[i]);
                     }
                 }
-                // gAhat_t = gAhat_start - sum_{tau < t} gA_tau: the inclusive sum runs on the
-                // MFMA (hi + lo parts, ~16-bit mantissa per term, fp32 accumulation) and the own
-                // term is added back in fp32; the sub-chunk total seeds the next sub-chunk.
+                // (bucket tiles spread over waves) gAhat_t = gAhat_start - sum_{tau < t} gA_tau:
+                // the inclusive sum runs on the MFMA (hi + lo parts, ~16-bit mantissa per term,
+                // fp32 accumulation) and the own term is added back in fp32; the sub-chunk total
+                // seeds the next sub-chunk.
 #pragma unroll
                 for (int i = 0; i < TPW_A; ++i) {
-                    if (a_ok(i)) {
+                    if (!REG_ST && a_ok(i)) {
                         const int ts = a_ts(i), tt = a_tt(i);
                         const int s = ts * 16 + ((lane >> 4) << 2);
                         f32x4 inc = {0.f, 0.f, 0.f, 0.f};
