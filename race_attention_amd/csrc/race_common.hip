@@ -371,14 +371,35 @@ hipError_t softhash_prepare(int D, int LK)
 template <class TX, int D>
 __global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
 {
-    constexpr int VEC = 4, TPR = D / VEC, RIF = 256 / TPR;  // threads per row, rows in flight
-    __shared__ float sIn[DEC_GMAX + 2][D];                  // k, v, q_0..q_{G-1}
-    __shared__ float sU[DEC_GMAX + 1][DEC_LKMAX];           // u for k, q_g
-    __shared__ float sP[DEC_GMAX + 1][DEC_SMAX];            // pK, pQ_g
-    __shared__ float sRed[RIF][DEC_GMAX][D];
-    const int z = blockIdx.x;                                // b * Hkv + hk
-    const int b = z / P.Hkv, hk = z % P.Hkv;
+    // thread layout of the state update: TPR threads per bucket row (VEC floats each), RIF
+    // rows in flight, PFR rows per thread loaded together
+    constexpr int VEC = 4, TPR = D / VEC, RIF = 256 / TPR, PFR = 8;
+    extern __shared__ float sm[];
     const int G = P.G, LK = P.L * P.K, R = 1 << P.K, S = P.L * R;
+    const bool pl_lds = D * LK <= DEC_PL_LDS;  // planes staged in LDS
+    float *sIn = sm;                  // [G + 2][D]: k, v, q_0 .. q_{G-1}
+    float *sU = sIn + (G + 2) * D;    // [G + 1][LK]: u for k, q_g
+    float *sP = sU + (G + 1) * LK;    // [G + 1][S]: pK, pQ_g
+    float *sRed = sP + (G + 1) * S;   // [RIF][G][D]: readout partial sums
+    float *sPl = sRed + RIF * G * D;  // [D][LK] planes (pl_lds)
+    const int z = blockIdx.x;         // b * Hkv + hk
+    const int b = z / P.Hkv, hk = z % P.Hkv;
+    const int rr = threadIdx.x / TPR, dv = (threadIdx.x % TPR) * VEC;
+    float *A = P.A + (int64_t)z * S;
+    float *Bs = P.Bs + (int64_t)z * S * D;
+    f32x4 bpre[PFR];
+    float apre[PFR];
+    // first PFR rows of this thread: loads of clamped rows (always inside the state), all in
+    // flight together. Issued once no later global load has to be waited for before the update
+    // (the memory counter is in order): after the planes are in LDS, or after the projections.
+    auto prefetch_state = [&]() {
+#pragma unroll
+        for (int j = 0; j < PFR; ++j) {
+            const int sr = min(rr + j * RIF, S - 1);
+            bpre[j] = *reinterpret_cast<const f32x4 *>(Bs + (int64_t)sr * D + dv);
+            apre[j] = A[sr];
+        }
+    };
     const TX *q = reinterpret_cast<const TX *>(P.q);
     const TX *k = reinterpret_cast<const TX *>(P.k);
     const TX *v = reinterpret_cast<const TX *>(P.v);
@@ -391,79 +412,118 @@ __global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
             x = (float)v[((int64_t)b * P.Hkv + hk) * D + d];
         else
             x = (float)q[((int64_t)b * P.Hkv * G + hk * G + (row - 2)) * D + d];
-        sIn[row][d] = x;
+        sIn[row * D + d] = x;
+    }
+    if (pl_lds) {
+        for (int i = threadIdx.x; i < D * LK; i += 256) {
+            const float pl = P.planes[i];
+            sPl[i] = P.round_planes ? (float)(__bf16)pl : pl;
+        }
     }
     __syncthreads();
+    if (pl_lds)
+        prefetch_state();
     // projections: row 0 = k, rows 1.. = q_g
     for (int i = threadIdx.x; i < (G + 1) * LK; i += 256) {
         const int row = i / LK, j = i % LK;
-        const float *x = sIn[row == 0 ? 0 : row + 1];
+        const float *x = sIn + (row == 0 ? 0 : row + 1) * D;
         float acc = 0.0f;
-        for (int d = 0; d < D; ++d) {
-            const float pl = P.planes[d * LK + j];
-            acc += x[d] * (P.round_planes ? (float)(__bf16)pl : pl);
+        if (pl_lds) {
+            for (int d = 0; d < D; ++d)
+                acc += x[d] * sPl[d * LK + j];
+        } else {
+#pragma unroll 8
+            for (int d = 0; d < D; ++d) {
+                const float pl = P.planes[d * LK + j];
+                acc += x[d] * (P.round_planes ? (float)(__bf16)pl : pl);
+            }
         }
-        sU[row][j] = tanh_f(acc) * P.inv_scale;
+        sU[row * LK + j] = tanh_f(acc) * P.inv_scale;
     }
+    if (!pl_lds)
+        prefetch_state();
     __syncthreads();
     for (int i = threadIdx.x; i < (G + 1) * P.L; i += 256) {
         const int row = i / P.L, l = i % P.L;
         float u[4], p[16];
         for (int kk = 0; kk < 4; ++kk)
-            u[kk] = (kk < P.K) ? sU[row][l * P.K + kk] : 0.0f;
+            u[kk] = (kk < P.K) ? sU[row * LK + l * P.K + kk] : 0.0f;
         expand_probs(u, P.K, p);
         for (int r = 0; r < 16; ++r)
             if (r < R)
-                sP[row][l * R + r] = p[r];
+                sP[row * S + l * R + r] = p[r];
     }
     __syncthreads();
-    // state update + readout
-    const int rr = threadIdx.x / TPR, dv = (threadIdx.x % TPR) * VEC;
+    // state update + readout, PFR rows per thread at a time
     float acc[DEC_GMAX][VEC];
     for (int g = 0; g < DEC_GMAX; ++g)
         for (int e = 0; e < VEC; ++e)
             acc[g][e] = 0.0f;
-    float *A = P.A + (int64_t)z * S;
-    float *Bs = P.Bs + (int64_t)z * S * D;
     float vv[VEC];
     for (int e = 0; e < VEC; ++e)
-        vv[e] = sIn[1][dv + e];
-    for (int s = rr; s < S; s += RIF) {
-        const float pk = sP[0][s];
-        const float a = A[s] + pk;
-        f32x4 bv = *reinterpret_cast<const f32x4 *>(Bs + (int64_t)s * D + dv);
-        for (int e = 0; e < VEC; ++e)
-            bv[e] += pk * vv[e];
-        *reinterpret_cast<f32x4 *>(Bs + (int64_t)s * D + dv) = bv;
-        if (dv == 0)
-            A[s] = a;
-        const float inv = frcp(a + P.eps);
-        for (int g = 0; g < DEC_GMAX; ++g)
-            if (g < G) {
-                const float w = sP[1 + g][s] * inv;
-                for (int e = 0; e < VEC; ++e)
-                    acc[g][e] += w * bv[e];
+        vv[e] = sIn[D + dv + e];
+    for (int s0 = 0; s0 < S; s0 += PFR * RIF) {
+        if (s0 > 0) {
+#pragma unroll
+            for (int j = 0; j < PFR; ++j) {
+                const int sr = min(s0 + rr + j * RIF, S - 1);
+                bpre[j] = *reinterpret_cast<const f32x4 *>(Bs + (int64_t)sr * D + dv);
+                apre[j] = A[sr];
             }
+        }
+#pragma unroll
+        for (int j = 0; j < PFR; ++j) {
+            const int s = s0 + rr + j * RIF;
+            if (s < S) {
+                const float pk = sP[s];
+                const float a = apre[j] + pk;
+                f32x4 bv = bpre[j];
+                for (int e = 0; e < VEC; ++e)
+                    bv[e] += pk * vv[e];
+                *reinterpret_cast<f32x4 *>(Bs + (int64_t)s * D + dv) = bv;
+                if (dv == 0)
+                    A[s] = a;
+                const float inv = frcp(a + P.eps);
+                for (int g = 0; g < DEC_GMAX; ++g)
+                    if (g < G) {
+                        const float w = sP[(1 + g) * S + s] * inv;
+                        for (int e = 0; e < VEC; ++e)
+                            acc[g][e] += w * bv[e];
+                    }
+            }
+        }
     }
     for (int g = 0; g < DEC_GMAX; ++g)
         if (g < G)
             for (int e = 0; e < VEC; ++e)
-                sRed[rr][g][dv + e] = acc[g][e];
+                sRed[(rr * G + g) * D + dv + e] = acc[g][e];
     __syncthreads();
     TX *out = reinterpret_cast<TX *>(P.out);
     for (int i = threadIdx.x; i < G * D; i += 256) {
         const int g = i / D, d = i % D;
         float sum = 0.0f;
         for (int r = 0; r < RIF; ++r)
-            sum += sRed[r][g][d];
+            sum += sRed[(r * G + g) * D + d];
         out[((int64_t)b * P.Hkv * G + hk * G + g) * D + d] = (TX)sum;
     }
+}
+
+// dynamic LDS of one decode workgroup (floats): inputs, soft bits, probabilities, partial sums
+static size_t decode_smem(const DecodeParams &P)
+{
+    const int LK = P.L * P.K, S = P.L << P.K, RIF = 256 / (P.D / 4);
+    const size_t pl = P.D * LK <= DEC_PL_LDS ? (size_t)P.D * LK : 0;
+    return sizeof(float) * ((size_t)(P.G + 2) * P.D + (size_t)(P.G + 1) * LK + (size_t)(P.G + 1) * S +
+                            (size_t)RIF * P.G * P.D + pl);
 }
 
 hipError_t launch_decode(const DecodeParams &P, int bf16, hipStream_t s)
 {
     const dim3 grid((unsigned)(P.B * P.Hkv));
-#define DEC(TX, DD) hipLaunchKernelGGL((race_decode_step<TX, DD>), grid, dim3(256), 0, s, P)
+    const size_t smem = decode_smem(P);
+    if (smem > 64 * 1024)
+        return hipErrorInvalidValue;
+#define DEC(TX, DD) hipLaunchKernelGGL((race_decode_step<TX, DD>), grid, dim3(256), smem, s, P)
     if (P.D == 64) {
         if (bf16) DEC(__bf16, 64); else DEC(float, 64);
     } else if (P.D == 128) {

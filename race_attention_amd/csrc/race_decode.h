@@ -9,6 +9,7 @@ namespace race {
 constexpr int DEC_GMAX = 8;     // query heads per kv head
 constexpr int DEC_LKMAX = 128;  // L*K
 constexpr int DEC_SMAX = 512;   // L*2^K
+constexpr int DEC_PL_LDS = 4096;  // planes (D * L*K floats) staged in LDS up to this size
 
 struct DecodeParams {
     const void *q;   // [B][Hkv*G][D]
