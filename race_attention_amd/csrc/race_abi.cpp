@@ -150,9 +150,10 @@ int qkv_geometry(const race_qkv_shape *sh, Geo &g)
     g.Z = (int64_t)sh->B * sh->Hkv;
     if (g.Z > 65535)
         return fail(RACE_ERR_UNSUPPORTED, "race_qkv: B*Hkv = %lld exceeds 65535", (long long)g.Z);
-    // the fused backward kernels hold one workgroup per CU: ~1024 workgroups (4 rounds) keep the
-    // block-state traffic and per-block set-up low while filling the chip
-    g.CB = resolve_block(sh->T, g.Z * g.n_st, g.C, sh->block, 1024);
+    // ~768 workgroups per launch: whole rounds on MI355X's 256 CUs both for the backward kernels
+    // (one workgroup per CU: 3 rounds) and for the bf16 readout (three per CU: 1 round), with
+    // few enough blocks to keep the block-state traffic and per-block set-up low
+    g.CB = resolve_block(sh->T, g.Z * g.n_st, g.C, sh->block, 768);
     g.NB = cdiv(sh->T, g.CB);
     fill_ws_sizes(g);
     return RACE_OK;
