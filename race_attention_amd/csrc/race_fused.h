@@ -308,7 +308,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     using CF = FCfg<ST, DP, KB, NW>;
     constexpr int C = CF::C, NTH = CF::NTH, R = CF::R;
     __shared__ __align__(16) __bf16 sK[C][CF::LDX];
-    __shared__ __align__(16) __bf16 sV[C][CF::LDX];
+    __shared__ __align__(16) __bf16 sV[2][C][CF::LDX];  // by sub-chunk parity
     __shared__ __align__(16) __bf16 sPK[C][CF::LDS];  // rows [t][s]
 
     const Ctx c = make_ctx(P, ST);
@@ -336,13 +336,16 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, min(C, c.t_end - c.t_begin), tid);
     tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, min(C, c.t_end - c.t_begin), tid);
     tile_store_rows<CF>(&sK[0][0], pk, min(C, c.t_end - c.t_begin), tid);
-    tile_store_rows<CF>(&sV[0][0], pv, min(C, c.t_end - c.t_begin), tid);
+    tile_store_rows<CF>(&sV[0][0][0], pv, min(C, c.t_end - c.t_begin), tid);
     wait_vmem_all();
     __syncthreads();
 
+    // two barrier phases per sub-chunk: soft-hash of k, then the MFMAs together with the next
+    // sub-chunk's rows into LDS (k rows are free once hashed, v rows double buffered)
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
+        const int cur = sc & 1, nxt = cur ^ 1;
         if (sc + 1 < nsub) {
             const int t1 = t0 + C;
             tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, min(C, c.t_end - t1), tid);
@@ -377,7 +380,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
             const int t = wave + i * NW;
             if (t < CF::NTS * CF::NTD)
                 EngBF16::mma(accS[i], ld_tr(&sPK[0][0], CF::LDS, 0, (t / CF::NTD) * 16, lane),
-                             ld_tr(&sV[0][0], CF::LDX, 0, (t % CF::NTD) * 16, lane));
+                             ld_tr(&sV[cur][0][0], CF::LDX, 0, (t % CF::NTD) * 16, lane));
         }
 #pragma unroll
         for (int i = 0; i < TPW_A; ++i) {
@@ -385,11 +388,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
             if (tn < CF::NTS)
                 EngBF16::mma(accA[i], ones, ld_tr(&sPK[0][0], CF::LDS, 0, tn * 16, lane));
         }
-        __syncthreads();
         wait_vmem_all();
         if (sc + 1 < nsub) {
             tile_store_rows<CF>(&sK[0][0], pk, min(C, c.t_end - t0 - C), tid);
-            tile_store_rows<CF>(&sV[0][0], pv, min(C, c.t_end - t0 - C), tid);
+            tile_store_rows<CF>(&sV[nxt][0][0], pv, min(C, c.t_end - t0 - C), tid);
         }
         __syncthreads();
     }
