@@ -368,20 +368,22 @@ hipError_t softhash_prepare(int D, int LK)
 // updated in place: A += pK, Bs += pK (x) v (inclusive prefix: the new token is
 // part of its own readout), then out_g = sum_s pQ_g[s] Bs[s,:] / (A[s] + eps)
 // for the G query heads of the group.
-template <class TX, int D>
-__global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
+template <class TX, int D, int GM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GM <= 4 ? 8 : 1))) void race_decode_step(DecodeParams P)
 {
     // thread layout of the state update: TPR threads per bucket row (VEC floats each), RIF
-    // rows in flight, PFR rows per thread loaded together
-    constexpr int VEC = 4, TPR = D / VEC, RIF = 256 / TPR, PFR = 8;
+    // rows per pass over the state, PFR rows per thread loaded together; GM >= G query heads.
+    // Registers stay within 64 per lane and LDS within 20 KB, so eight workgroups fit a CU
+    // and a 256-CU device runs the 2048 (sequence, kv head) pairs of a decode batch in one round.
+    constexpr int VEC = 4, TPR = D / VEC, RIF = 256 / TPR, PFR = 4, NWV = 4;
     extern __shared__ float sm[];
     const int G = P.G, LK = P.L * P.K, R = 1 << P.K, S = P.L * R;
     const bool pl_lds = D * LK <= DEC_PL_LDS;  // planes staged in LDS
     float *sIn = sm;                  // [G + 2][D]: k, v, q_0 .. q_{G-1}
     float *sU = sIn + (G + 2) * D;    // [G + 1][LK]: u for k, q_g
     float *sP = sU + (G + 1) * LK;    // [G + 1][S]: pK, pQ_g
-    float *sRed = sP + (G + 1) * S;   // [RIF][G][D]: readout partial sums
-    float *sPl = sRed + RIF * G * D;  // [D][LK] planes (pl_lds)
+    float *sRed = sP + (G + 1) * S;   // [NWV][G][D]: readout partial sums per wave
+    float *sPl = sRed + NWV * G * D;  // [D][LK] planes (pl_lds)
     const int z = blockIdx.x;         // b * Hkv + hk
     const int b = z / P.Hkv, hk = z % P.Hkv;
     const int rr = threadIdx.x / TPR, dv = (threadIdx.x % TPR) * VEC;
@@ -455,8 +457,8 @@ __global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
     }
     __syncthreads();
     // state update + readout, PFR rows per thread at a time
-    float acc[DEC_GMAX][VEC];
-    for (int g = 0; g < DEC_GMAX; ++g)
+    float acc[GM][VEC];
+    for (int g = 0; g < GM; ++g)
         for (int e = 0; e < VEC; ++e)
             acc[g][e] = 0.0f;
     float vv[VEC];
@@ -484,7 +486,7 @@ __global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
                 if (dv == 0)
                     A[s] = a;
                 const float inv = frcp(a + P.eps);
-                for (int g = 0; g < DEC_GMAX; ++g)
+                for (int g = 0; g < GM; ++g)
                     if (g < G) {
                         const float w = sP[(1 + g) * S + s] * inv;
                         for (int e = 0; e < VEC; ++e)
@@ -493,16 +495,25 @@ __global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
             }
         }
     }
-    for (int g = 0; g < DEC_GMAX; ++g)
+    // the rows of one wave share the lanes' head-dim columns: lanes l, l + TPR, ... add up by
+    // shuffles, then one partial sum per wave goes through LDS
+    const int wv = threadIdx.x >> 6;
+    for (int g = 0; g < GM; ++g)
         if (g < G)
-            for (int e = 0; e < VEC; ++e)
-                sRed[(rr * G + g) * D + dv + e] = acc[g][e];
+            for (int e = 0; e < VEC; ++e) {
+                float x = acc[g][e];
+#pragma unroll
+                for (int m = TPR; m < 64; m <<= 1)
+                    x += __shfl_xor(x, m, 64);
+                if ((threadIdx.x & 63) < TPR)
+                    sRed[(wv * G + g) * D + dv + e] = x;
+            }
     __syncthreads();
     TX *out = reinterpret_cast<TX *>(P.out);
     for (int i = threadIdx.x; i < G * D; i += 256) {
         const int g = i / D, d = i % D;
         float sum = 0.0f;
-        for (int r = 0; r < RIF; ++r)
+        for (int r = 0; r < NWV; ++r)
             sum += sRed[(r * G + g) * D + d];
         out[((int64_t)b * P.Hkv * G + hk * G + g) * D + d] = (TX)sum;
     }
@@ -511,10 +522,10 @@ __global__ __launch_bounds__(256) void race_decode_step(DecodeParams P)
 // dynamic LDS of one decode workgroup (floats): inputs, soft bits, probabilities, partial sums
 static size_t decode_smem(const DecodeParams &P)
 {
-    const int LK = P.L * P.K, S = P.L << P.K, RIF = 256 / (P.D / 4);
+    const int LK = P.L * P.K, S = P.L << P.K, NWV = 4;
     const size_t pl = P.D * LK <= DEC_PL_LDS ? (size_t)P.D * LK : 0;
     return sizeof(float) * ((size_t)(P.G + 2) * P.D + (size_t)(P.G + 1) * LK + (size_t)(P.G + 1) * S +
-                            (size_t)RIF * P.G * P.D + pl);
+                            (size_t)NWV * P.G * P.D + pl);
 }
 
 hipError_t launch_decode(const DecodeParams &P, int bf16, hipStream_t s)
@@ -523,14 +534,22 @@ hipError_t launch_decode(const DecodeParams &P, int bf16, hipStream_t s)
     const size_t smem = decode_smem(P);
     if (smem > 64 * 1024)
         return hipErrorInvalidValue;
-#define DEC(TX, DD) hipLaunchKernelGGL((race_decode_step<TX, DD>), grid, dim3(256), smem, s, P)
+    if (P.G < 1 || P.G > DEC_GMAX)
+        return hipErrorInvalidValue;
+#define DEC(TX, DD, GM) hipLaunchKernelGGL((race_decode_step<TX, DD, GM>), grid, dim3(256), smem, s, P)
+#define DEC_G(TX, DD)                 \
+    if (P.G == 1) DEC(TX, DD, 1);     \
+    else if (P.G == 2) DEC(TX, DD, 2); \
+    else if (P.G <= 4) DEC(TX, DD, 4); \
+    else DEC(TX, DD, 8)
     if (P.D == 64) {
-        if (bf16) DEC(__bf16, 64); else DEC(float, 64);
+        if (bf16) { DEC_G(__bf16, 64); } else { DEC_G(float, 64); }
     } else if (P.D == 128) {
-        if (bf16) DEC(__bf16, 128); else DEC(float, 128);
+        if (bf16) { DEC_G(__bf16, 128); } else { DEC_G(float, 128); }
     } else {
         return hipErrorInvalidValue;
     }
+#undef DEC_G
 #undef DEC
     return hipGetLastError();
 }
