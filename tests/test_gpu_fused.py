@@ -169,7 +169,7 @@ def test_batched_ace(dev):
         check(f"BatchedACE unshared m={m}", out2[m], r.transpose(1, 2), 2e-5)
 
 
-@pytest.mark.parametrize("G,D", [(4, 64), (1, 128), (2, 64)])
+@pytest.mark.parametrize("G,D", [(4, 64), (1, 128), (2, 64), (3, 64), (6, 128), (8, 64)])
 def test_decode_matches_forward(dev, G, D):
     """prefill T0 tokens, then decode steps: each step equals the full causal
     forward at that position (the reference's GPT.generate recomputation)."""
