@@ -256,7 +256,9 @@ RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int 
     for (int i = 0; i < CF::PF; ++i) {
         const int idx = tid + i * CF::NTH;
         const int row = min(idx / CH, nv - 1), c = idx % CH;
-        if (idx < CF::CHUNKS)
+        // (no branch when every thread loads whole chunk sets: a fixed number of loads per
+        // thread lets in-order memory-counter waits skip the newest loads)
+        if (CF::CHUNKS % CF::NTH == 0 || idx < CF::CHUNKS)
             r[i] = *reinterpret_cast<const u32x4 *>(base + row * (int)st + c * 8);
     }
 }
@@ -296,6 +298,14 @@ RACE_DEV void wait_vmem_all()
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt 0, expcnt 7 (none), lgkmcnt 15 (none)
 }
 
+// s_waitcnt vmcnt(N): all but the N most recently issued vector-memory operations have completed
+template <int N>
+RACE_DEV void wait_vmem_older()
+{
+    static_assert(N >= 0 && N < 16, "vmcnt immediate (low field)");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
 RACE_DEV const __bf16 *row_ptr(const View &v, int b, int h, int t)
 {
     return reinterpret_cast<const __bf16 *>(v.p) + (b * v.sb + h * v.sh + (int64_t)t * v.st);
@@ -332,25 +342,34 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
         ones[e] = (__bf16)1.0f;
 
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
-    u32x4 pk[CF::PF], pv[CF::PF];
-    tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, min(C, c.t_end - c.t_begin), tid);
-    tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, min(C, c.t_end - c.t_begin), tid);
-    tile_store_rows<CF>(&sK[0][0], pk, min(C, c.t_end - c.t_begin), tid);
-    tile_store_rows<CF>(&sV[0][0][0], pv, min(C, c.t_end - c.t_begin), tid);
+    // rows of sub-chunk sc + 1 are in flight while sub-chunk sc is computed and the loads of
+    // sc + 2 are issued at its start (twice the bytes in flight of a one-step prefetch, which
+    // bounded this kernel by latency): two register sets, the loop unrolled by two so that each
+    // set is named statically. Every thread issues exactly 2 * PF loads per sub-chunk, so
+    // "vmcnt <= 2 * PF" means that all but the newest set have landed.
+    static_assert(CF::CHUNKS % CF::NTH == 0, "every thread loads whole chunk sets");
+    u32x4 pkA[CF::PF], pvA[CF::PF], pkB[CF::PF], pvB[CF::PF];
+    auto load_rows = [&](u32x4 (&rk)[CF::PF], u32x4 (&rv)[CF::PF], int t1) {
+        tile_load<CF>(rk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, min(C, c.t_end - t1), tid);
+        tile_load<CF>(rv, row_ptr(P.v, c.b, c.hk, t1), P.v.st, min(C, c.t_end - t1), tid);
+    };
+    const int t_last = c.t_begin + (nsub - 1) * C;  // start of the last sub-chunk
+    load_rows(pkB, pvB, c.t_begin);
     wait_vmem_all();
+    tile_store_rows<CF>(&sK[0][0], pkB, min(C, c.t_end - c.t_begin), tid);
+    tile_store_rows<CF>(&sV[0][0][0], pvB, min(C, c.t_end - c.t_begin), tid);
+    load_rows(pkA, pvA, min(c.t_begin + C, t_last));
     __syncthreads();
 
     // two barrier phases per sub-chunk: soft-hash of k, then the MFMAs together with the next
     // sub-chunk's rows into LDS (k rows are free once hashed, v rows double buffered)
-    for (int sc = 0; sc < nsub; ++sc) {
+    auto body = [&](int sc, u32x4 (&nk)[CF::PF], u32x4 (&nvr)[CF::PF], u32x4 (&fk)[CF::PF], u32x4 (&fv)[CF::PF]) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
         const int cur = sc & 1, nxt = cur ^ 1;
-        if (sc + 1 < nsub) {
-            const int t1 = t0 + C;
-            tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, min(C, c.t_end - t1), tid);
-            tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, t1), P.v.st, min(C, c.t_end - t1), tid);
-        }
+        // issued unconditionally (a straight-line load stream keeps the compiler's memory-counter
+        // waits exact): past the end it re-reads the last sub-chunk, whose rows are not used
+        load_rows(fk, fv, min(t0 + 2 * C, t_last));
         // soft-hash of k -> pK rows
 #pragma unroll
         for (int i = 0; i < TPW_P; ++i) {
@@ -388,13 +407,20 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
             if (tn < CF::NTS)
                 EngBF16::mma(accA[i], ones, ld_tr(&sPK[0][0], CF::LDS, 0, tn * 16, lane));
         }
-        wait_vmem_all();
-        if (sc + 1 < nsub) {
-            tile_store_rows<CF>(&sK[0][0], pk, min(C, c.t_end - t0 - C), tid);
-            tile_store_rows<CF>(&sV[nxt][0][0], pv, min(C, c.t_end - t0 - C), tid);
-        }
+        // the next rows go to LDS unconditionally (after the last sub-chunk they are zeros that
+        // nothing reads): every prefetch set is consumed on every path, so the compiler's
+        // memory-counter tracking needs no wait before the set is loaded again
+        wait_vmem_older<2 * CF::PF>();
+        tile_store_rows<CF>(&sK[0][0], nk, min(C, c.t_end - t0 - C), tid);
+        tile_store_rows<CF>(&sV[nxt][0][0], nvr, min(C, c.t_end - t0 - C), tid);
         __syncthreads();
+    };
+    for (int sc = 0; sc < nsub; sc += 2) {
+        body(sc, pkA, pvA, pkB, pvB);
+        if (sc + 1 < nsub)
+            body(sc + 1, pkB, pvB, pkA, pvA);
     }
+    wait_vmem_all();
 
     const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
     float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
