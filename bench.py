@@ -52,8 +52,9 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (x3), the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
-    ap.add_argument("--workload", default="cfg3", choices=["cfg3", "cfg5"],
-                    help="cfg5: Llama-3.2-1B-shaped hybrid LM (random init), B=8, T=8192 prefill "
+    ap.add_argument("--workload", default="cfg3", choices=["cfg2", "cfg3", "cfg5"],
+                    help="cfg2: the same layer step at B=4, H=16, T=65536, L=16 (S=256), q/k/v ~ N(0,1); "
+                         "cfg5: Llama-3.2-1B-shaped hybrid LM (random init), B=8, T=8192 prefill "
                          "forward+backward, then 256-token greedy decode through the RACE state cache")
     return ap.parse_args()
 
@@ -121,10 +122,12 @@ def main():
         return
     dev = torch.device("cuda:0")
     B, H, T, D, L, K = args.B, args.H, args.T, 64, args.L, 4
+    std = 1.0 / math.sqrt(D)
+    if args.workload == "cfg2":
+        B, H, T, L, std = 4, 16, 65536, 16, 1.0
     S = L << K
     planes_T, _ = build_planes_protos(D, K, L, 1, device=dev, seed=0)
     g = torch.Generator(device=dev).manual_seed(1)
-    std = 1.0 / math.sqrt(D)
     q = (torch.randn(B, H, T, D, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(True)
     k = (torch.randn(B, H, T, D, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(True)
     v = (torch.randn(B, H, T, D, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(True)
@@ -188,8 +191,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "cfg3: one causal RACE layer fwd+bwd", "B": B, "H": H, "T": T, "D": D, "L": L,
-                   "K": K, "S": S, "inputs": "bf16 q,k,v ~ N(0,1/sqrt(D)), go ~ N(0,1), seed 1; planes seed 0",
+        "config": {"workload": f"{args.workload}: one causal RACE layer fwd+bwd", "B": B, "H": H, "T": T, "D": D,
+                   "L": L, "K": K, "S": S,
+                   "inputs": f"bf16 q,k,v ~ N(0,{'1' if std == 1.0 else '1/sqrt(D)'}), go ~ N(0,1), seed 1; planes seed 0",
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "layer_roofline": layer_roofline,

@@ -133,8 +133,42 @@ hipError_t launch_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t ele
 }
 
 // ============================================================================ partial sums
-__global__ void race_reduce_partials(const float *part, int n_st, int64_t tile, OutView out, int H,
-                                     int T, int D, int64_t total)
+// out[b][h][t][d] = sum over bucket tiles st of part[st * tile + ((b * H + h) * T + t) * D + d].
+// Fast form: grid (chunks of one (b, h) slab, B*H), 32-bit index math, V = 4 consecutive head-dim
+// elements per thread with 16-byte loads and 16-/8-byte stores. The general form (one element per
+// thread, 64-bit index math) serves shapes the fast form does not fit.
+template <int V>
+__global__ __launch_bounds__(256) void race_reduce_partials_vec(const float *part, int n_st, int64_t tile,
+                                                                OutView out, int H, int T, int D)
+{
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int DV = D / V;
+    const int j = blockIdx.x * 256 + threadIdx.x;  // (t, group of V head-dim elements) within the slab
+    if (j >= T * DV)
+        return;
+    const int t = j / DV, d = (j - t * DV) * V;
+    const float *src = part + ((int64_t)bh * T + t) * D + d;
+    f32x4 acc = *reinterpret_cast<const f32x4 *>(src);
+    for (int st = 1; st < n_st; ++st) {
+        const f32x4 x = *reinterpret_cast<const f32x4 *>(src + (int64_t)st * tile);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            acc[e] += x[e];
+    }
+    const int64_t off = b * out.sb + h * out.sh + (int64_t)t * out.st + d;
+    if (out.f32) {
+        *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(out.p) + off) = acc;
+    } else {
+        bf16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = (__bf16)acc[e];
+        *reinterpret_cast<bf16x4 *>(reinterpret_cast<__bf16 *>(out.p) + off) = w;
+    }
+}
+
+__global__ void race_reduce_partials_any(const float *part, int n_st, int64_t tile, OutView out, int H,
+                                         int T, int D, int64_t total)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total)
@@ -159,8 +193,19 @@ hipError_t launch_reduce_partials(const float *part, int n_st, int64_t tile, con
                                   int B, int H, int T, int D, hipStream_t s)
 {
     const int64_t total = (int64_t)B * H * T * D;
-    hipLaunchKernelGGL(race_reduce_partials, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                       part, n_st, tile, out, H, T, D, total);
+    const int esz = out.f32 ? 4 : 2;
+    const bool vec = D % 4 == 0 && out.sb % 4 == 0 && out.sh % 4 == 0 && out.st % 4 == 0 && tile % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(part) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out.p) % (4 * esz) == 0 && (int64_t)T * (D / 4) < (1LL << 31) - 256 &&
+                     (int64_t)B * H <= 65535;
+    if (vec) {
+        const int64_t per_slab = (int64_t)T * (D / 4);
+        hipLaunchKernelGGL(race_reduce_partials_vec<4>, dim3((unsigned)((per_slab + 255) / 256), (unsigned)(B * H)),
+                           dim3(256), 0, s, part, n_st, tile, out, H, T, D);
+    } else {
+        hipLaunchKernelGGL(race_reduce_partials_any, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           part, n_st, tile, out, H, T, D, total);
+    }
     return hipGetLastError();
 }
 
