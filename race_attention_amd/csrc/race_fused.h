@@ -458,9 +458,13 @@ void race_fused_fwd_readout(const ScanParams P)
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // v rows, double buffered
     __shared__ __align__(16) __bf16 sPK[C][LDS];     // rows [t][s]
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
-    __shared__ __align__(16) __bf16 sW[C][LDS];
     __shared__ __align__(16) __bf16 sPm[C][LDC];
-    __shared__ __align__(16) OT sO[C][LDO];
+    // W (written in P2, read in P3) and the output staging (written in P4, read in the next
+    // step's P1) share one buffer: barriers separate every use of one from the other
+    constexpr int SZ_W = C * LDS * 2 > C * LDO * (int)sizeof(OT) ? C * LDS * 2 : C * LDO * (int)sizeof(OT);
+    __shared__ __align__(16) char uW[SZ_W];
+    __bf16(*sW)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uW);
+    OT(*sO)[LDO] = reinterpret_cast<OT(*)[LDO]>(uW);
     __shared__ __align__(16) float sA0[2][ST];
 
     const Ctx c = make_ctx(P, ST);
