@@ -83,3 +83,46 @@ def test_layer_forward_graph_replays_equal_eager(dev):
         ref = race_causal_attention(*x, planes_T, L, Kb)
         torch.cuda.synchronize()
         assert torch.equal(out_s, ref), f"replay {i}: output differs from the eager forward"
+
+
+def test_layer_forward_backward_graph_replays_equal_eager(dev):
+    from race_attention_amd import build_planes_protos, race_causal_attention
+    B, H, T, D, L, Kb = 1, 2, 2500, 64, 8, 4
+    planes_T, _ = build_planes_protos(D, Kb, L, 1, device=dev, seed=7)
+    g = torch.Generator(device=dev).manual_seed(13)
+
+    def draw():
+        return [(torch.randn(B, H, T, D, generator=g, device=dev) * 0.125).bfloat16() for _ in range(4)]
+
+    def step(q, k, v, go):
+        out = race_causal_attention(q, k, v, planes_T, L, Kb)
+        out.backward(go)
+        return out
+
+    leaves = [torch.zeros(B, H, T, D, device=dev, dtype=torch.bfloat16, requires_grad=True) for _ in range(3)]
+    go_s = torch.zeros(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on a side stream, as torch's whole-step capture expects
+        for _ in range(2):
+            step(*leaves, go_s)
+            for t in leaves:
+                t.grad = None
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_s = step(*leaves, go_s)
+    torch.cuda.synchronize()
+
+    for i in range(3):
+        x = draw()
+        with torch.no_grad():
+            for s, t in zip(leaves + [go_s], x):
+                s.copy_(t)
+        graph.replay()
+        ref_leaves = [t.clone().requires_grad_(True) for t in x[:3]]
+        ref = step(*ref_leaves, x[3])
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, ref), f"replay {i}: output differs"
+        for name, a, b in zip("qkv", leaves, ref_leaves):
+            assert torch.equal(a.grad, b.grad), f"replay {i}: d{name} differs"
