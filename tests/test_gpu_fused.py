@@ -66,6 +66,26 @@ def test_fused_block_invariance_and_determinism(dev):
     assert torch.equal(again, outs[0]), "fused forward is not bitwise deterministic"
 
 
+def test_fused_backward_block_invariance_and_determinism(dev):
+    """dq/dk/dv do not depend on the block decomposition (1 .. 16 blocks: the reverse block scan
+    of the suffix states) beyond fp32 rounding, and repeat bitwise."""
+    from race_attention_amd import build_planes_protos, race_causal_attention
+    planes_T, _ = build_planes_protos(64, 4, 8, 1, device=dev, seed=2)
+    q, k, v, go = qkv(1, 2, 2, 2000, 64, seed=6, dev=dev)
+
+    def grads(block):
+        xs = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+        race_causal_attention(*xs, planes_T, 8, 4, block=block, out_dtype=torch.float32).backward(go.float())
+        return [x.grad.float() for x in xs]
+
+    ref = grads(0)
+    for b in (128, 512, 2048):
+        for name, g, r in zip(("dq", "dk", "dv"), grads(b), ref):
+            check(f"{name} block={b}", g, r, 1e-2)
+    for g, r in zip(grads(0), ref):
+        assert torch.equal(g, r), "fused backward is not bitwise deterministic"
+
+
 def test_fused_strided_views(dev):
     """[B,T,H,D] storage viewed as [B,H,T,D] (the nanochat layout) needs no copy."""
     from race_attention_amd import build_planes_protos, race_causal_attention
