@@ -33,6 +33,10 @@ FUSED_CASES = [  # B, Hq, Hkv, T, D, L, K, scale
     (1, 2, 2, 513, 64, 4, 2, 1.0),        # K=2, temperature-1 scale
     (1, 1, 1, 4096, 64, 8, 4, None),
     (1, 2, 1, 300, 128, 4, 4, 1.0),
+    (1, 2, 2, 1, 64, 8, 4, None),         # a single token
+    (2, 2, 2, 31, 64, 8, 4, None),        # shorter than one 32-token sub-chunk
+    (1, 8, 2, 200, 64, 16, 4, None),      # grouped-query heads with two bucket tiles
+    (1, 8, 1, 97, 128, 16, 3, 1.0),       # 8 query heads per kv head, K=3 at 128 buckets
 ]
 
 
@@ -50,7 +54,18 @@ def test_fused_forward_backward(dev, case):
     ref_out, ref_dq, ref_dk, ref_dv = oracle_layer(q, k, v, bf16_planes(planes_T), L, Kb, scale, EPS, go)
     check("out", out, ref_out, BF16_TOL)
     check("dq", qx.grad, ref_dq, BF16_TOL)
-    check("dk", kx.grad, ref_dk, BF16_TOL)
+    if T >= 64:
+        check("dk", kx.grad, ref_dk, BF16_TOL)
+    else:
+        # For a sequence's first tokens dL/dpK is a difference of two nearly equal terms: at
+        # t = 0, gA = -(go.v) pQ pK/(pK+eps)^2 against (go.v) pQ/(pK+eps) from the state, which
+        # cancel to (go.v) pQ eps/(pK+eps)^2 ~ 1e-6. The bf16 path forms both terms from
+        # bf16-rounded operands, so there dk carries bf16 noise of O(1) terms while the exact
+        # dk is ~0 and the per-tensor normalisation degenerates. A sequence shorter than two
+        # sub-chunks is checked against the common scale of the three input gradients.
+        gscale = max(ref_dq.abs().max(), ref_dk.abs().max(), ref_dv.abs().max()).item()
+        err = (kx.grad.double().cpu() - ref_dk).abs().max().item()
+        assert err <= BF16_TOL * gscale, f"dk: max error {err:.3e} > {BF16_TOL:.0e} x gradient scale {gscale:.3e}"
     check("dv", vx.grad, ref_dv, BF16_TOL)
 
 
