@@ -11,8 +11,10 @@
 //    4-bucket vectors of one token row;
 //  * the readout is accumulated transposed, out^T[d][t], and staged through LDS
 //    for 16-byte coalesced global stores;
-//  * the next sub-chunk's k, q, v rows are loaded into registers while the current
-//    one is computed; four barriers per sub-chunk.
+//  * the next sub-chunk's k, q, v (and go) rows are loaded into registers while the
+//    current one is computed (two sub-chunks ahead in the forward totals);
+//  * barrier phases per sub-chunk: 2 (forward totals), 4 (readout, backward totals),
+//    5 (backward main, whose sub-chunk tail is pipelined into the next head).
 #pragma once
 #include <type_traits>
 
