@@ -275,8 +275,8 @@ def bench_hybrid(torch, args, B=8, T=8192, n_new=256):
     RACE L=8 K=4), bf16 random-init weights, uniform synthetic token ids (seed 1).
     prefill: forward + cross-entropy backward over B x T tokens; decode: prefill the
     RACE state cache with the B x T prompt, then n_new greedy tokens, one fused decode
-    kernel per layer per token."""
-    from race_attention_amd.hybrid import HybridConfig, HybridLM
+    kernel per layer per token: eagerly, and replaying one captured HIP graph per token step."""
+    from race_attention_amd.hybrid import GraphedDecoder, HybridConfig, HybridLM
     dev = torch.device("cuda:0")
     cfg = HybridConfig()
     model = HybridLM(cfg).to(dev).init_weights(seed=0)
@@ -311,12 +311,23 @@ def bench_hybrid(torch, args, B=8, T=8192, n_new=256):
             logits = model(nxt, cache)[:, -1]
         torch.cuda.synchronize()
         decode_s = time.perf_counter() - t0
+        del cache, logits
+        dec = GraphedDecoder(model, idx[:, :T])  # prefill and capture, not timed
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n_new):
+            dec.step(keep=False)
+        torch.cuda.synchronize()
+        graph_s = time.perf_counter() - t0
     return {"metric": "cfg5 hybrid LM tokens/sec", "workload": "cfg5", "B": B, "T": T, "params": sum(
                 p.numel() for p in model.parameters()),
             "train_fwd_bwd": {"value": round(B * T / train_s, 1), "unit": "tokens/s", "seconds": round(train_s, 4)},
             "prefill_fwd": {"value": round(B * T / prefill_s, 1), "unit": "tokens/s", "seconds": round(prefill_s, 4)},
             "greedy_decode": {"value": round(B * n_new / decode_s, 1), "unit": "tokens/s", "steps": n_new,
                               "ms_per_token_step": round(decode_s / n_new * 1e3, 3)},
+            "greedy_decode_graphed": {"value": round(B * n_new / graph_s, 1), "unit": "tokens/s", "steps": n_new,
+                                      "ms_per_token_step": round(graph_s / n_new * 1e3, 3),
+                                      "how": "one captured HIP graph per token step (GraphedDecoder)"},
             "dtype": "bf16", "data": "synthetic uniform token ids, random-init weights"}
 
 

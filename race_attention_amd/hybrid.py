@@ -136,10 +136,17 @@ class HybridLM(nn.Module):
         return RaceStateCache(self.cfg.n_layer, batch, a.n_head, a.n_kv_head, a.head_dim, a.L, a.K,
                               [b.attn.planes_T for b in self.blocks], eps=a.eps, device=self.embed.weight.device)
 
-    def forward(self, idx, cache=None, targets=None):
+    def forward(self, idx, cache=None, targets=None, pos=None):
+        """idx [B, T] token ids. With a cache the sequence continues at cache.get_pos(), or at the
+        device tensor `pos` ([1], int64) when given: a captured decode step reads its rotary
+        rows through it, so one HIP graph serves every position."""
         B, T = idx.shape
-        t0 = 0 if cache is None else cache.get_pos()
-        cos_sin = self.cos[:, t0:t0 + T], self.sin[:, t0:t0 + T]
+        if pos is None:
+            t0 = 0 if cache is None else cache.get_pos()
+            cos_sin = self.cos[:, t0:t0 + T], self.sin[:, t0:t0 + T]
+        else:
+            rows = pos + torch.arange(T, device=pos.device)
+            cos_sin = self.cos.index_select(1, rows), self.sin.index_select(1, rows)
         x = self.embed(idx)
         for blk in self.blocks:
             x = blk(x, cos_sin, cache)
@@ -147,6 +154,15 @@ class HybridLM(nn.Module):
         if targets is None:
             return logits
         return F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1))
+
+    @torch.no_grad()
+    def generate_graphed(self, idx, n_new):
+        """Greedy decode as generate(idx, n_new), each token step one replay of a captured HIP
+        graph (GraphedDecoder). Returns the same (tokens, logits) pair."""
+        dec = GraphedDecoder(self, idx)
+        for _ in range(n_new - 1):
+            dec.step()
+        return dec.finish()
 
     @torch.no_grad()
     def generate(self, idx, n_new, use_cache=True):
@@ -171,3 +187,65 @@ class HybridLM(nn.Module):
                 steps.append(logits)
                 seq = torch.cat([seq, nxt], 1)
         return torch.cat(toks, 1), torch.stack(steps)
+
+
+class GraphedDecoder:
+    """Greedy decoding of a HybridLM with one captured HIP graph per token step.
+
+    The constructor prefills a RaceStateCache eagerly from idx [B, T0] and picks the first token;
+    it then captures one step — embedding, the blocks (one fused RACE decode kernel each), the
+    head, the argmax that feeds the next step's token and the position increment, the position
+    living in a device tensor so one graph serves every step. step() replays it: no host work
+    per token beyond the replay. finish() returns (tokens [B, n], logits [n, B, V]) as
+    HybridLM.generate does, and leaves the cache's counters at the decoded length.
+    """
+
+    @torch.no_grad()
+    def __init__(self, model, idx):
+        self.model = model
+        B = idx.shape[0]
+        self.cache = model.make_cache(B)
+        logits = model(idx, self.cache)[:, -1]
+        self.tok = logits.argmax(-1, keepdim=True)
+        self.toks, self.steps = [self.tok.clone()], [logits.clone()]
+        self.pos = torch.tensor([self.cache.get_pos()], dtype=torch.long, device=idx.device)
+        # lazy library state (BLAS handles and workspaces, code objects) is set up by one run on
+        # a throwaway cache, on a side stream, before the capture; the real cache is not touched
+        scratch = model.make_cache(B)
+        tok0, pos0 = self.tok.clone(), self.pos.clone()
+        side = torch.cuda.Stream(device=idx.device)
+        side.wait_stream(torch.cuda.current_stream(idx.device))
+        with torch.cuda.stream(side):
+            self._step(scratch)
+        torch.cuda.current_stream(idx.device).wait_stream(side)
+        self.tok.copy_(tok0)
+        self.pos.copy_(pos0)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = self._step(self.cache)
+        # the capture ran the step's host side once without its kernels: undo its counters
+        self.cache.pos -= 1
+        for st in self.cache.layers:
+            st.tokens -= 1
+        self.n = 0
+
+    def _step(self, cache):
+        out = self.model(self.tok, cache, pos=self.pos)[:, -1]
+        self.tok.copy_(out.argmax(-1, keepdim=True))
+        self.pos.add_(1)
+        return out
+
+    def step(self, keep=True):
+        """One token for every sequence (kept for finish() unless keep=False)."""
+        self.graph.replay()
+        self.n += 1
+        if keep:
+            self.toks.append(self.tok.clone())
+            self.steps.append(self.out.clone())
+
+    def finish(self):
+        self.cache.pos += self.n
+        for st in self.cache.layers:
+            st.tokens += self.n
+        self.n = 0
+        return torch.cat(self.toks, 1), torch.stack(self.steps)
