@@ -120,6 +120,8 @@ int qkv_geometry(const race_qkv_shape *sh, Geo &g)
         return fail(RACE_ERR_INVALID, "race_qkv: null shape");
     if (sh->B <= 0 || sh->Hq <= 0 || sh->Hkv <= 0 || sh->T <= 0 || sh->L <= 0)
         return fail(RACE_ERR_INVALID, "race_qkv: B, Hq, Hkv, T, L must be positive");
+    if (sh->T > (1 << 30))  // token indices and sub-chunk look-ahead stay in 32-bit range
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv: T = %d tokens, at most 2^30 are supported", sh->T);
     if (sh->Hq % sh->Hkv)
         return fail(RACE_ERR_INVALID, "race_qkv: Hq = %d is not a multiple of Hkv = %d", sh->Hq, sh->Hkv);
     if (sh->K < 1 || sh->K > 4)
@@ -278,6 +280,8 @@ static int hash_common(const race_hash_shape *sh, const race_tensor &x, int x_dt
         return fail(RACE_ERR_INVALID, "race_soft_hash: null shape");
     if (sh->B <= 0 || sh->H <= 0 || sh->T <= 0 || sh->D <= 0 || sh->L <= 0 || sh->M <= 0)
         return fail(RACE_ERR_INVALID, "race_soft_hash: B, H, T, D, L, M must be positive");
+    if (sh->T > (1 << 30))  // token indices stay in 32-bit range
+        return fail(RACE_ERR_UNSUPPORTED, "race_soft_hash: T = %d tokens, at most 2^30 are supported", sh->T);
     if (sh->K < 1 || sh->K > 8)
         return fail(RACE_ERR_UNSUPPORTED, "race_soft_hash: K = %d, supported 1..8", sh->K);
     if (x_dtype != RACE_F32 && x_dtype != RACE_BF16)

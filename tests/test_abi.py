@@ -52,6 +52,7 @@ def test_abi_version_and_sizes():
     ((1, 4, 3, 128, 64, 8, 4), "multiple"),      # Hq not a multiple of Hkv
     ((1, 4, 4, 128, 96, 8, 4), "head dim"),      # D not compiled in the fused path
     ((1, 4, 4, 128, 64, 8, 5), "K = 5"),         # K > 4
+    ((1, 4, 4, (1 << 30) + 1, 64, 8, 4), "2^30"),  # token indices beyond 32-bit headroom
 ])
 def test_qkv_validation_errors(shape, msg):
     lib = _lib.load_library()
