@@ -29,6 +29,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK = 8.0e12      # B/s
 BF16_PEAK = 2.5e15     # dense MFMA flop/s
+FP32_PEAK = 157.3e12   # dense fp32 MFMA flop/s
 
 
 def parse():
@@ -52,8 +53,10 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (x3), the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
-    ap.add_argument("--workload", default="cfg3", choices=["cfg2", "cfg3", "cfg5"],
-                    help="cfg2: the same layer step at B=4, H=16, T=65536, L=16 (S=256), q/k/v ~ N(0,1); "
+    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5"],
+                    help="cfg1: the reference's fp32 op path (soft_hash_probs + RaceCausalFn) fwd+bwd at "
+                         "B=2, H=8, T=2048, D=64, L=8, K=4, scale sqrt(D) and 1.0, with the CPU path on the same "
+                         "inputs; cfg2: the same layer step at B=4, H=16, T=65536, L=16 (S=256), q/k/v ~ N(0,1); "
                          "cfg5: Llama-3.2-1B-shaped hybrid LM (random init), B=8, T=8192 prefill "
                          "forward+backward, then 256-token greedy decode through the RACE state cache")
     return ap.parse_args()
@@ -119,6 +122,9 @@ def main():
         return
     if args.workload == "cfg5":
         print(json.dumps(bench_hybrid(torch, args)))
+        return
+    if args.workload == "cfg1":
+        print(json.dumps(bench_cfg1(torch, args)))
         return
     dev = torch.device("cuda:0")
     B, H, T, D, L, K = args.B, args.H, args.T, 64, args.L, 4
@@ -329,6 +335,69 @@ def bench_hybrid(torch, args, B=8, T=8192, n_new=256):
                                       "ms_per_token_step": round(graph_s / n_new * 1e3, 3),
                                       "how": "one captured HIP graph per token step (GraphedDecoder)"},
             "dtype": "bf16", "data": "synthetic uniform token ids, random-init weights"}
+
+
+def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6):
+    """cfg1: fp32 q/k/v/go ~ N(0,1) drawn on the CPU (the same bits on both devices), planes seed 0.
+    GPU: the reference's fp32 op path (soft_hash_probs + RaceCausalFn, forward and backward) at the
+    reference's scale sqrt(D) and at 1.0; CPU: the reference CPU path (the port, whose soft-hash
+    fixes sqrt(D)) on the same inputs, all host cores, median of 3."""
+    from oracle import race_cpu_port
+    from oracle import race_oracle as orc
+    from race_attention_amd.race_causal_cuda import RaceCausalFn
+    from race_attention_amd.race_common import build_planes_protos, soft_hash_probs
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    Q, Kt, V, go = (torch.randn(B, H, T, D, generator=g) for _ in range(4))
+    planes_T, protos_T = build_planes_protos(D, K, L, 1, device=dev, seed=0)
+    q, k, v = (x.to(dev).requires_grad_(True) for x in (Q, Kt, V))
+    gd = go.to(dev)
+    S = L << K
+    f_alg, _ = layer_counts(S, D, L, K, elt=4)
+    n_tok = B * H * T
+    t_bound = max(f_alg * n_tok / FP32_PEAK, 11 * D * 4 * n_tok / HBM_PEAK)
+    gpu = {}
+    for name, scale in (("scale_sqrt_D", math.sqrt(D)), ("scale_1", 1.0)):
+        def step():
+            q.grad = k.grad = v.grad = None
+            pK, pQ, V2, _ = soft_hash_probs(q, k, v, planes_T, protos_T, L, K, 1, True, scale=scale)
+            RaceCausalFn.apply(pK, pQ, V2, eps).view(B, H, T, D).backward(gd)
+
+        for _ in range(max(1, args.warmup)):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        gpu[name] = {"value": round(B * T / (ms / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+                     "layer_roofline": {"bound": "fp32 compute", "t_bound_ms": round(t_bound * 1e3, 4),
+                                        "frac": round(t_bound * 1e3 / ms, 4)}}
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    pl_c, pr_c = orc.build_planes_protos(D, K, L, seed=0)
+    qc, kc, vc = (x.clone().requires_grad_(True) for x in (Q, Kt, V))
+
+    def run_cpu():
+        qc.grad = kc.grad = vc.grad = None
+        race_cpu_port.race_layer_cpu(qc, kc, vc, pl_c, pr_c, L, K).backward(go)
+
+    run_cpu()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run_cpu()
+        ts.append(time.perf_counter() - t0)
+    sec = sorted(ts)[1]
+    return {"metric": "cfg1 fp32 layer fwd+bwd tokens/sec", "workload": "cfg1", "dtype": "f32",
+            "config": {"B": B, "H": H, "T": T, "D": D, "L": L, "K": K, "S": S, "path": "soft_hash_probs + RaceCausalFn"},
+            "gpu": gpu,
+            "cpu_baseline": {"value": round(B * T / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+                             "sample": f"the whole cfg1 layer fwd+bwd (scale sqrt(D)), median of 3",
+                             "seconds_per_step": round(sec, 3)}}
 
 
 def bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, steps):
