@@ -210,8 +210,11 @@ hipError_t launch_reduce_partials(const float *part, int n_st, int64_t tile, con
 }
 
 // ============================================================================ soft-hash
-// Per table: p[r] = prod_k (bit_k(r) ? s1_k : s0_k), s1 = sigmoid(2u), s0 = sigmoid(-2u),
-// generic over K <= 8 (probabilities written directly, O(R*K) per table).
+// Per table: p[r] = prod_k (bit_k(r) ? s1_k : s0_k), s1 = sigmoid(2u), s0 = sigmoid(-2u), with
+// bit k = 0 the most significant bit of r (corner order of itertools.product([-1, 1])). The
+// kernels are compiled per bit count KB = 1..8, so every per-table array stays in registers;
+// for KB <= 4 all 2^KB probabilities are expanded in registers and the backward's corner sums
+// run as a butterfly over the bits.
 RACE_DEV void sigm_pair(float u, float &s0, float &s1)
 {
     const float e = __expf(-2.0f * sig_arg(u));
@@ -219,20 +222,41 @@ RACE_DEV void sigm_pair(float u, float &s0, float &s1)
     s0 = e * s1;
 }
 
-RACE_DEV float corner_prob(const float *s0, const float *s1, int K, int r)
+template <int KB>
+RACE_DEV float corner_prob(const float *s0, const float *s1, int r)
 {
     float p = 1.0f;
-    for (int k = 0; k < K; ++k)
-        p *= ((r >> (K - 1 - k)) & 1) ? s1[k] : s0[k];
+#pragma unroll
+    for (int k = 0; k < KB; ++k)
+        p *= ((r >> (KB - 1 - k)) & 1) ? s1[k] : s0[k];
     return p;
 }
 
-template <class TX>
+// all 2^KB corner probabilities; each factor enters as the lowest index bit and is shifted up
+// by the later ones, so factor 0 ends as the most significant bit
+template <int KB>
+RACE_DEV void corner_probs(const float *s0, const float *s1, float *p)
+{
+    p[0] = 1.0f;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const int n = 1 << k;
+#pragma unroll
+        for (int i = n - 1; i >= 0; --i) {
+            const float pi = p[i];
+            p[2 * i + 1] = pi * s1[k];
+            p[2 * i] = pi * s0[k];
+        }
+    }
+}
+
+template <class TX, int KB>
 __global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
 {
     extern __shared__ float sm[];
-    float *sPl = sm;                     // [D][LK]
-    float *sX = sPl + P.D * P.LK;        // [TT][D]
+    const int PL = P.LK + 1;             // planes pitch: odd, so column reads over d miss no bank
+    float *sPl = sm;                     // [D][PL]
+    float *sX = sPl + P.D * PL;          // [TT][D]
     float *sU = sX + SH_TT * P.D;        // [TT][LK]
     const int bh = blockIdx.y;
     const int m = blockIdx.z;            // ensemble member (unshared planes) or 0
@@ -241,7 +265,7 @@ __global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
     const int b = bh / P.H, h = bh % P.H;
     const float *planes = P.planes + (int64_t)m * P.plane_stride;
     for (int i = threadIdx.x; i < P.D * P.LK; i += blockDim.x)
-        sPl[i] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
+        sPl[i / P.LK * PL + i % P.LK] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
     const TX *x = reinterpret_cast<const TX *>(P.x.p);
     for (int i = threadIdx.x; i < SH_TT * P.D; i += blockDim.x) {
         const int r = i / P.D, d = i % P.D;
@@ -252,30 +276,49 @@ __global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
         const int r = i / P.LK, j = i % P.LK;
         float acc = 0.0f;
         for (int d = 0; d < P.D; ++d)
-            acc += sX[r * P.D + d] * sPl[d * P.LK + j];
+            acc += sX[r * P.D + d] * sPl[d * PL + j];
         sU[i] = tanh_f(acc) * P.inv_scale;
     }
     __syncthreads();
-    const int R = 1 << P.K, S = P.L * R;
+    constexpr int R = 1 << KB;
+    const int S = P.L * R;
     float *out = P.probs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
+    // every token's run of R corners starts 16-byte aligned when the buffer does and R % 4 == 0
+    const bool vec_out = (reinterpret_cast<uintptr_t>(P.probs) & 15) == 0;
     for (int i = threadIdx.x; i < nv * P.L; i += blockDim.x) {
         const int r = i / P.L, l = i % P.L;
-        float s0[8], s1[8];
-        for (int k = 0; k < P.K; ++k)
-            sigm_pair(sU[r * P.LK + l * P.K + k], s0[k], s1[k]);
+        float s0[KB], s1[KB];
+#pragma unroll
+        for (int k = 0; k < KB; ++k)
+            sigm_pair(sU[r * P.LK + l * KB + k], s0[k], s1[k]);
         float *o = out + (int64_t)(t0 + r) * S + l * R;
-        for (int c = 0; c < R; ++c)
-            o[c] = corner_prob(s0, s1, P.K, c);
+        if constexpr (KB <= 4) {
+            float p[R];
+            corner_probs<KB>(s0, s1, p);
+            if (R % 4 == 0 && vec_out) {
+#pragma unroll
+                for (int c = 0; c < R; c += 4)
+                    *reinterpret_cast<f32x4 *>(o + c) = f32x4{p[c], p[c + 1], p[c + 2], p[c + 3]};
+            } else {
+#pragma unroll
+                for (int c = 0; c < R; ++c)
+                    o[c] = p[c];
+            }
+        } else {
+            for (int c = 0; c < R; ++c)
+                o[c] = corner_prob<KB>(s0, s1, c);
+        }
     }
 }
 
 // dx[b,h,t,:] = sum_m sum_j gproj_m[t,j] planes_m[:, j]
-template <class TX>
+template <class TX, int KB>
 __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
 {
     extern __shared__ float sm[];
-    float *sPl = sm;
-    float *sX = sPl + P.D * P.LK;
+    const int PL = P.LK + 1;
+    float *sPl = sm;                     // [D][PL]
+    float *sX = sPl + P.D * PL;
     float *sU = sX + SH_TT * P.D;
     float *sGP = sU + SH_TT * P.LK;  // [TT][LK]
     const int bh = blockIdx.y;
@@ -287,7 +330,9 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
         const int r = i / P.D, d = i % P.D;
         sX[i] = (r < nv) ? (float)x[b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d] : 0.0f;
     }
-    const int R = 1 << P.K, S = P.L * R;
+    constexpr int R = 1 << KB;
+    const int S = P.L * R;
+    const bool vec_in = (reinterpret_cast<uintptr_t>(P.gprobs) & 15) == 0;
     constexpr int MAXO = (SH_TT * 256 + 255) / 256;  // outputs per thread for D <= 256
     float gx[MAXO];
     for (int o = 0; o < MAXO; ++o)
@@ -297,41 +342,85 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
         const float *planes = P.planes + (int64_t)(P.unshared ? m : 0) * P.plane_stride;
         __syncthreads();
         for (int i = threadIdx.x; i < P.D * P.LK; i += blockDim.x)
-            sPl[i] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
+            sPl[i / P.LK * PL + i % P.LK] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
         __syncthreads();
         for (int i = threadIdx.x; i < SH_TT * P.LK; i += blockDim.x) {
             const int r = i / P.LK, j = i % P.LK;
             float acc = 0.0f;
             for (int d = 0; d < P.D; ++d)
-                acc += sX[r * P.D + d] * sPl[d * P.LK + j];
+                acc += sX[r * P.D + d] * sPl[d * PL + j];
             sU[i] = tanh_f(acc) * P.inv_scale;
         }
         __syncthreads();
         const float *gprobs = P.gprobs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
         for (int i = threadIdx.x; i < SH_TT * P.L; i += blockDim.x) {
             const int r = i / P.L, l = i % P.L;
-            float u[8], s0[8], s1[8], gu[8];
-            for (int k = 0; k < P.K; ++k) {
-                u[k] = sU[r * P.LK + l * P.K + k];
+            float u[KB], s0[KB], s1[KB], gu[KB];
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                u[k] = sU[r * P.LK + l * KB + k];
                 sigm_pair(u[k], s0[k], s1[k]);
                 gu[k] = 0.0f;
             }
             if (r < nv) {
                 const float *gp = gprobs + (int64_t)(t0 + r) * S + l * R;
-                float dot = 0.0f;
-                for (int c = 0; c < R; ++c)
-                    dot += corner_prob(s0, s1, P.K, c) * gp[c];
-                for (int c = 0; c < R; ++c) {
-                    const float gz = corner_prob(s0, s1, P.K, c) * (gp[c] - dot);
-                    for (int k = 0; k < P.K; ++k)
-                        gu[k] += ((c >> (P.K - 1 - k)) & 1) ? gz : -gz;
+                if constexpr (KB <= 4) {
+                    // gz_c = p_c (gp_c - sum p gp); gu_k = sum_c sign_k(c) gz_c with sign +1 where
+                    // bit k of c is set: a butterfly from the least significant bit, pair sums
+                    // feed the next level and pair differences sum to that bit's gu
+                    float p[R], z[R], g[R];
+                    if (R % 4 == 0 && vec_in) {
+#pragma unroll
+                        for (int c = 0; c < R; c += 4) {
+                            const f32x4 w = *reinterpret_cast<const f32x4 *>(gp + c);
+                            g[c] = w[0];
+                            g[c + 1] = w[1];
+                            g[c + 2] = w[2];
+                            g[c + 3] = w[3];
+                        }
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < R; ++c)
+                            g[c] = gp[c];
+                    }
+                    corner_probs<KB>(s0, s1, p);
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < R; ++c)
+                        dot += p[c] * g[c];
+#pragma unroll
+                    for (int c = 0; c < R; ++c)
+                        z[c] = p[c] * (g[c] - dot);
+#pragma unroll
+                    for (int lvl = 0; lvl < KB; ++lvl) {
+                        const int n = R >> (lvl + 1);
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < n; ++q) {
+                            acc += z[2 * q + 1] - z[2 * q];
+                            z[q] = z[2 * q] + z[2 * q + 1];
+                        }
+                        gu[KB - 1 - lvl] = acc;
+                    }
+                } else {
+                    float dot = 0.0f;
+                    for (int c = 0; c < R; ++c)
+                        dot += corner_prob<KB>(s0, s1, c) * gp[c];
+                    for (int c = 0; c < R; ++c) {
+                        const float gz = corner_prob<KB>(s0, s1, c) * (gp[c] - dot);
+#pragma unroll
+                        for (int k = 0; k < KB; ++k)
+                            gu[k] += ((c >> (KB - 1 - k)) & 1) ? gz : -gz;
+                    }
                 }
-                for (int k = 0; k < P.K; ++k)
+#pragma unroll
+                for (int k = 0; k < KB; ++k)
                     gsu += gu[k] * u[k];
             }
-            for (int k = 0; k < P.K; ++k) {
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
                 const float th = u[k] * P.scale;
-                sGP[r * P.LK + l * P.K + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+                sGP[r * P.LK + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
             }
         }
         __syncthreads();
@@ -341,7 +430,7 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
                 const int r = i / P.D, d = i % P.D;
                 float acc = 0.0f;
                 for (int j = 0; j < P.LK; ++j)
-                    acc += sGP[r * P.LK + j] * sPl[d * P.LK + j];
+                    acc += sGP[r * P.LK + j] * sPl[d * PL + j];
                 gx[o] += acc;
             }
         }
@@ -368,28 +457,45 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
     }
 }
 
+// kernel of bit count K (1..8) for one direction and dtype
+template <class TX, int KB>
+static const void *softhash_kernel(int bwd)
+{
+    return bwd ? (const void *)race_softhash_bwd<TX, KB> : (const void *)race_softhash_fwd<TX, KB>;
+}
+
+template <class TX>
+static const void *softhash_kernel_k(int K, int bwd)
+{
+    switch (K) {
+    case 1: return softhash_kernel<TX, 1>(bwd);
+    case 2: return softhash_kernel<TX, 2>(bwd);
+    case 3: return softhash_kernel<TX, 3>(bwd);
+    case 4: return softhash_kernel<TX, 4>(bwd);
+    case 5: return softhash_kernel<TX, 5>(bwd);
+    case 6: return softhash_kernel<TX, 6>(bwd);
+    case 7: return softhash_kernel<TX, 7>(bwd);
+    case 8: return softhash_kernel<TX, 8>(bwd);
+    default: return nullptr;
+    }
+}
+
 size_t softhash_smem(int D, int LK, bool bwd)
 {
-    return sizeof(float) * ((size_t)D * LK + (size_t)SH_TT * D + (size_t)SH_TT * LK * (bwd ? 2 : 1));
+    return sizeof(float) * ((size_t)D * (LK + 1) + (size_t)SH_TT * D + (size_t)SH_TT * LK * (bwd ? 2 : 1));
 }
 
 hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s)
 {
+    const void *fn = bf16 ? softhash_kernel_k<__bf16>(P.K, bwd) : softhash_kernel_k<float>(P.K, bwd);
+    if (!fn)
+        return hipErrorInvalidValue;
     const dim3 grid((unsigned)((P.T + SH_TT - 1) / SH_TT), (unsigned)(P.B * P.H),
                     (unsigned)(bwd ? 1 : (P.unshared ? P.M : 1)));
     const size_t smem = softhash_smem(P.D, P.LK, bwd);
-    if (bwd) {
-        if (bf16)
-            hipLaunchKernelGGL(race_softhash_bwd<__bf16>, grid, dim3(256), smem, s, P);
-        else
-            hipLaunchKernelGGL(race_softhash_bwd<float>, grid, dim3(256), smem, s, P);
-    } else {
-        if (bf16)
-            hipLaunchKernelGGL(race_softhash_fwd<__bf16>, grid, dim3(256), smem, s, P);
-        else
-            hipLaunchKernelGGL(race_softhash_fwd<float>, grid, dim3(256), smem, s, P);
-    }
-    return hipGetLastError();
+    SoftHashParams args = P;
+    void *argv[] = {&args};
+    return hipLaunchKernel(fn, grid, dim3(256), argv, smem, s);
 }
 
 hipError_t softhash_prepare(int D, int LK)
@@ -397,13 +503,13 @@ hipError_t softhash_prepare(int D, int LK)
     const int smem = (int)softhash_smem(D, LK, true);
     hipError_t e = hipSuccess;
     if (smem > 64 * 1024) {
-        e = hipFuncSetAttribute((const void *)race_softhash_fwd<float>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)race_softhash_fwd<__bf16>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)race_softhash_bwd<float>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)race_softhash_bwd<__bf16>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+        for (int K = 1; K <= 8 && e == hipSuccess; ++K)
+            for (int bwd = 0; bwd < 2 && e == hipSuccess; ++bwd) {
+                e = hipFuncSetAttribute(softhash_kernel_k<float>(K, bwd), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+                if (e == hipSuccess)
+                    e = hipFuncSetAttribute(softhash_kernel_k<__bf16>(K, bwd),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+            }
     }
     return e;
 }
