@@ -250,35 +250,88 @@ RACE_DEV void corner_probs(const float *s0, const float *s1, float *p)
     }
 }
 
+// LDS of one soft-hash workgroup (floats):
+//   sPl [DX][PL]  planes of one member, zero beyond (D, LK); PL is 4 x odd words, so 16-byte reads by
+//                 16 lanes of consecutive rows d cover the 64 banks once
+//   sX  [TT][DX]  input rows, zero beyond D (DX = D rounded up to 4)
+//   sU  [TT][LK]  tanh(projection) / scale
+//   sGP [TT][PG]  backward only: d loss / d projection, zero beyond LK (PG = LK rounded up to 4)
+__host__ __device__ inline int sh_dx(int D) { return (D + 3) & ~3; }
+__host__ __device__ inline int sh_pg(int LK) { return (LK + 3) & ~3; }
+__host__ __device__ inline int sh_pl(int LK) { return sh_pg(LK) + ((sh_pg(LK) & 4) ? 0 : 4); }
+constexpr int SH_RB = 4;  // rows per thread in the two LDS products
+
+RACE_DEV void sh_load_planes(float *sPl, const float *planes, const SoftHashParams &P)
+{
+    const int DX = sh_dx(P.D), PL = sh_pl(P.LK);
+    for (int i = threadIdx.x; i < DX * PL; i += 256) {
+        const int d = i / PL, j = i - d * PL;
+        float v = 0.0f;
+        if (d < P.D && j < P.LK) {
+            v = planes[d * P.LK + j];
+            if (P.round_planes)
+                v = (float)(__bf16)v;
+        }
+        sPl[i] = v;
+    }
+}
+
+template <class TX>
+RACE_DEV void sh_load_x(float *sX, const SoftHashParams &P, int b, int h, int t0, int nv)
+{
+    const int DX = sh_dx(P.D);
+    const TX *x = reinterpret_cast<const TX *>(P.x.p);
+    for (int i = threadIdx.x; i < SH_TT * DX; i += 256) {
+        const int r = i / DX, d = i - r * DX;
+        sX[i] = (r < nv && d < P.D) ? (float)x[b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d] : 0.0f;
+    }
+}
+
+// sU[r][j] = tanh(sum_d x[r][d] planes[d][j]) / scale. A thread owns SH_RB rows of one column j:
+// x is read as 16-byte runs that all lanes of a row group share, planes as one word per row d
+RACE_DEV void sh_project(const float *sX, const float *sPl, float *sU, const SoftHashParams &P)
+{
+    const int DX = sh_dx(P.D), PL = sh_pl(P.LK), LK = P.LK;
+    for (int i = threadIdx.x; i < (SH_TT / SH_RB) * LK; i += 256) {
+        const int rg = i / LK, j = i - rg * LK;
+        const float *xr = sX + rg * SH_RB * DX;
+        float acc[SH_RB] = {};
+        for (int d = 0; d < DX; d += 4) {
+            float pl[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                pl[e] = sPl[(d + e) * PL + j];
+#pragma unroll
+            for (int q = 0; q < SH_RB; ++q) {
+                const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr + q * DX + d);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[q] += xv[e] * pl[e];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < SH_RB; ++q)
+            sU[(rg * SH_RB + q) * LK + j] = tanh_f(acc[q]) * P.inv_scale;
+    }
+}
+
 template <class TX, int KB>
 __global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
 {
     extern __shared__ float sm[];
-    const int PL = P.LK + 1;             // planes pitch: odd, so column reads over d miss no bank
-    float *sPl = sm;                     // [D][PL]
-    float *sX = sPl + P.D * PL;          // [TT][D]
-    float *sU = sX + SH_TT * P.D;        // [TT][LK]
+    const int DX = sh_dx(P.D);
+    float *sPl = sm;
+    float *sX = sPl + DX * sh_pl(P.LK);
+    float *sU = sX + SH_TT * DX;
     const int bh = blockIdx.y;
     const int m = blockIdx.z;            // ensemble member (unshared planes) or 0
     const int t0 = blockIdx.x * SH_TT;
     const int nv = min(SH_TT, P.T - t0);
     const int b = bh / P.H, h = bh % P.H;
-    const float *planes = P.planes + (int64_t)m * P.plane_stride;
-    for (int i = threadIdx.x; i < P.D * P.LK; i += blockDim.x)
-        sPl[i / P.LK * PL + i % P.LK] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
-    const TX *x = reinterpret_cast<const TX *>(P.x.p);
-    for (int i = threadIdx.x; i < SH_TT * P.D; i += blockDim.x) {
-        const int r = i / P.D, d = i % P.D;
-        sX[i] = (r < nv) ? (float)x[b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d] : 0.0f;
-    }
+    sh_load_planes(sPl, P.planes + (int64_t)m * P.plane_stride, P);
+    sh_load_x<TX>(sX, P, b, h, t0, nv);
     __syncthreads();
-    for (int i = threadIdx.x; i < SH_TT * P.LK; i += blockDim.x) {
-        const int r = i / P.LK, j = i % P.LK;
-        float acc = 0.0f;
-        for (int d = 0; d < P.D; ++d)
-            acc += sX[r * P.D + d] * sPl[d * PL + j];
-        sU[i] = tanh_f(acc) * P.inv_scale;
-    }
+    sh_project(sX, sPl, sU, P);
     __syncthreads();
     constexpr int R = 1 << KB;
     const int S = P.L * R;
@@ -316,41 +369,35 @@ template <class TX, int KB>
 __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
 {
     extern __shared__ float sm[];
-    const int PL = P.LK + 1;
-    float *sPl = sm;                     // [D][PL]
-    float *sX = sPl + P.D * PL;
-    float *sU = sX + SH_TT * P.D;
-    float *sGP = sU + SH_TT * P.LK;  // [TT][LK]
+    const int DX = sh_dx(P.D), PL = sh_pl(P.LK), PG = sh_pg(P.LK);
+    float *sPl = sm;
+    float *sX = sPl + DX * PL;
+    float *sU = sX + SH_TT * DX;
+    float *sGP = sU + SH_TT * P.LK;
     const int bh = blockIdx.y;
     const int t0 = blockIdx.x * SH_TT;
     const int nv = min(SH_TT, P.T - t0);
     const int b = bh / P.H, h = bh % P.H;
-    const TX *x = reinterpret_cast<const TX *>(P.x.p);
-    for (int i = threadIdx.x; i < SH_TT * P.D; i += blockDim.x) {
-        const int r = i / P.D, d = i % P.D;
-        sX[i] = (r < nv) ? (float)x[b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d] : 0.0f;
-    }
+    sh_load_x<TX>(sX, P, b, h, t0, nv);
+    for (int i = threadIdx.x; i < SH_TT * PG; i += 256)  // the padding columns stay zero
+        sGP[i] = 0.0f;
     constexpr int R = 1 << KB;
     const int S = P.L * R;
     const bool vec_in = (reinterpret_cast<uintptr_t>(P.gprobs) & 15) == 0;
-    constexpr int MAXO = (SH_TT * 256 + 255) / 256;  // outputs per thread for D <= 256
-    float gx[MAXO];
-    for (int o = 0; o < MAXO; ++o)
-        gx[o] = 0.0f;
+    // dx items: (row group, d) pairs, SH_RB rows each; at most SH_TT / SH_RB * 256 for D <= 256
+    constexpr int MAXI = SH_TT / SH_RB;
+    float gx[MAXI][SH_RB];
+#pragma unroll
+    for (int o = 0; o < MAXI; ++o)
+#pragma unroll
+        for (int q = 0; q < SH_RB; ++q)
+            gx[o][q] = 0.0f;
     float gsu = 0.0f;  // sum of gu * u over this thread's (token, table) items
     for (int m = 0; m < P.M; ++m) {
-        const float *planes = P.planes + (int64_t)(P.unshared ? m : 0) * P.plane_stride;
         __syncthreads();
-        for (int i = threadIdx.x; i < P.D * P.LK; i += blockDim.x)
-            sPl[i / P.LK * PL + i % P.LK] = P.round_planes ? (float)(__bf16)planes[i] : planes[i];
+        sh_load_planes(sPl, P.planes + (int64_t)(P.unshared ? m : 0) * P.plane_stride, P);
         __syncthreads();
-        for (int i = threadIdx.x; i < SH_TT * P.LK; i += blockDim.x) {
-            const int r = i / P.LK, j = i % P.LK;
-            float acc = 0.0f;
-            for (int d = 0; d < P.D; ++d)
-                acc += sX[r * P.D + d] * sPl[d * PL + j];
-            sU[i] = tanh_f(acc) * P.inv_scale;
-        }
+        sh_project(sX, sPl, sU, P);
         __syncthreads();
         const float *gprobs = P.gprobs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
         for (int i = threadIdx.x; i < SH_TT * P.L; i += blockDim.x) {
@@ -420,28 +467,48 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
 #pragma unroll
             for (int k = 0; k < KB; ++k) {
                 const float th = u[k] * P.scale;
-                sGP[r * P.LK + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+                sGP[r * PG + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
             }
         }
         __syncthreads();
-        for (int o = 0; o < MAXO; ++o) {
+        // gx[r][d] += sum_j gproj[r][j] planes[d][j]: SH_RB rows of one d per item, both operands
+        // read as 16-byte runs over j (gproj shared by the lanes of a row group)
+#pragma unroll
+        for (int o = 0; o < MAXI; ++o) {
             const int i = threadIdx.x + o * 256;
-            if (i < SH_TT * P.D) {
-                const int r = i / P.D, d = i % P.D;
-                float acc = 0.0f;
-                for (int j = 0; j < P.LK; ++j)
-                    acc += sGP[r * P.LK + j] * sPl[d * PL + j];
-                gx[o] += acc;
+            if (i < (SH_TT / SH_RB) * P.D) {
+                const int rg = i / P.D, d = i - rg * P.D;
+                const float *gr = sGP + rg * SH_RB * PG;
+                const float *pr = sPl + d * PL;
+                float acc[SH_RB] = {};
+                for (int j = 0; j < PG; j += 4) {
+                    const f32x4 pv = *reinterpret_cast<const f32x4 *>(pr + j);
+#pragma unroll
+                    for (int q = 0; q < SH_RB; ++q) {
+                        const f32x4 gv = *reinterpret_cast<const f32x4 *>(gr + q * PG + j);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[q] += gv[e] * pv[e];
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < SH_RB; ++q)
+                    gx[o][q] += acc[q];
             }
         }
     }
     TX *dx = reinterpret_cast<TX *>(const_cast<void *>(P.dx.p));
-    for (int o = 0; o < MAXO; ++o) {
+#pragma unroll
+    for (int o = 0; o < MAXI; ++o) {
         const int i = threadIdx.x + o * 256;
-        if (i < SH_TT * P.D) {
-            const int r = i / P.D, d = i % P.D;
-            if (r < nv)
-                dx[b * P.dx.sb + h * P.dx.sh + (int64_t)(t0 + r) * P.dx.st + d] = (TX)gx[o];
+        if (i < (SH_TT / SH_RB) * P.D) {
+            const int rg = i / P.D, d = i - rg * P.D;
+#pragma unroll
+            for (int q = 0; q < SH_RB; ++q) {
+                const int r = rg * SH_RB + q;
+                if (r < nv)
+                    dx[b * P.dx.sb + h * P.dx.sh + (int64_t)(t0 + r) * P.dx.st + d] = (TX)gx[o][q];
+            }
         }
     }
     if (P.gscale) {
@@ -482,7 +549,8 @@ static const void *softhash_kernel_k(int K, int bwd)
 
 size_t softhash_smem(int D, int LK, bool bwd)
 {
-    return sizeof(float) * ((size_t)D * (LK + 1) + (size_t)SH_TT * D + (size_t)SH_TT * LK * (bwd ? 2 : 1));
+    const size_t DX = sh_dx(D);
+    return sizeof(float) * (DX * sh_pl(LK) + SH_TT * DX + (size_t)SH_TT * LK + (bwd ? (size_t)SH_TT * sh_pg(LK) : 0));
 }
 
 hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s)
