@@ -52,8 +52,6 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t rup(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Tokens per workgroup: enough blocks for ~2048 workgroups in total, at least
-// four sub-chunks per block; an explicit request is rounded to the sub-chunk.
 // Tokens per workgroup: `req` rounded to the sub-chunk, or (req = 0) about `target`
 // workgroups per launch with at least 4 sub-chunks each.
 int64_t resolve_block(int64_t T, int64_t streams, int C, int64_t req, int64_t target)
@@ -342,7 +340,7 @@ int race_soft_hash_bwd_partials(const race_hash_shape *sh)
 {
     if (!sh || sh->T <= 0 || sh->B <= 0 || sh->H <= 0)
         return 0;
-    return (int)(cdiv(sh->T, SH_TT) * sh->B * sh->H);
+    return softhash_grid_x(sh->T, sh->B, sh->H) * sh->B * sh->H;
 }
 
 int race_soft_hash_bwd_scale(const race_hash_shape *sh, race_tensor x, int x_dtype, const float *planes_T,

@@ -325,47 +325,54 @@ __global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
     float *sU = sX + SH_TT * DX;
     const int bh = blockIdx.y;
     const int m = blockIdx.z;            // ensemble member (unshared planes) or 0
-    const int t0 = blockIdx.x * SH_TT;
-    const int nv = min(SH_TT, P.T - t0);
     const int b = bh / P.H, h = bh % P.H;
-    sh_load_planes(sPl, P.planes + (int64_t)m * P.plane_stride, P);
-    sh_load_x<TX>(sX, P, b, h, t0, nv);
-    __syncthreads();
-    sh_project(sX, sPl, sU, P);
-    __syncthreads();
+    const int ntt = (P.T + SH_TT - 1) / SH_TT;
+    const int tt1 = min(ntt, ((int)blockIdx.x + 1) * P.tpw);
     constexpr int R = 1 << KB;
     const int S = P.L * R;
     float *out = P.probs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
     // every token's run of R corners starts 16-byte aligned when the buffer does and R % 4 == 0
     const bool vec_out = (reinterpret_cast<uintptr_t>(P.probs) & 15) == 0;
-    for (int i = threadIdx.x; i < nv * P.L; i += blockDim.x) {
-        const int r = i / P.L, l = i % P.L;
-        float s0[KB], s1[KB];
+    sh_load_planes(sPl, P.planes + (int64_t)m * P.plane_stride, P);
+    // tiles of SH_TT tokens; sX is free again once the projection's barrier is passed, and the
+    // barrier after the x load keeps the next projection from overwriting sU under the readers
+    for (int tt = blockIdx.x * P.tpw; tt < tt1; ++tt) {
+        const int t0 = tt * SH_TT;
+        const int nv = min(SH_TT, P.T - t0);
+        sh_load_x<TX>(sX, P, b, h, t0, nv);
+        __syncthreads();
+        sh_project(sX, sPl, sU, P);
+        __syncthreads();
+        for (int i = threadIdx.x; i < nv * P.L; i += blockDim.x) {
+            const int r = i / P.L, l = i % P.L;
+            float s0[KB], s1[KB];
 #pragma unroll
-        for (int k = 0; k < KB; ++k)
-            sigm_pair(sU[r * P.LK + l * KB + k], s0[k], s1[k]);
-        float *o = out + (int64_t)(t0 + r) * S + l * R;
-        if constexpr (KB <= 4) {
-            float p[R];
-            corner_probs<KB>(s0, s1, p);
-            if (R % 4 == 0 && vec_out) {
+            for (int k = 0; k < KB; ++k)
+                sigm_pair(sU[r * P.LK + l * KB + k], s0[k], s1[k]);
+            float *o = out + (int64_t)(t0 + r) * S + l * R;
+            if constexpr (KB <= 4) {
+                float p[R];
+                corner_probs<KB>(s0, s1, p);
+                if (R % 4 == 0 && vec_out) {
 #pragma unroll
-                for (int c = 0; c < R; c += 4)
-                    *reinterpret_cast<f32x4 *>(o + c) = f32x4{p[c], p[c + 1], p[c + 2], p[c + 3]};
+                    for (int c = 0; c < R; c += 4)
+                        *reinterpret_cast<f32x4 *>(o + c) = f32x4{p[c], p[c + 1], p[c + 2], p[c + 3]};
+                } else {
+#pragma unroll
+                    for (int c = 0; c < R; ++c)
+                        o[c] = p[c];
+                }
             } else {
-#pragma unroll
                 for (int c = 0; c < R; ++c)
-                    o[c] = p[c];
+                    o[c] = corner_prob<KB>(s0, s1, c);
             }
-        } else {
-            for (int c = 0; c < R; ++c)
-                o[c] = corner_prob<KB>(s0, s1, c);
         }
     }
 }
 
-// dx[b,h,t,:] = sum_m sum_j gproj_m[t,j] planes_m[:, j]
-template <class TX, int KB>
+// dx[b,h,t,:] = sum_m sum_j gproj_m[t,j] planes_m[:, j]. DI: dx items per thread (D <= 32 * DI),
+// so the accumulators held across a tile take no more registers than the head dim needs
+template <class TX, int KB, int DI>
 __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
 {
     extern __shared__ float sm[];
@@ -375,139 +382,151 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
     float *sU = sX + SH_TT * DX;
     float *sGP = sU + SH_TT * P.LK;
     const int bh = blockIdx.y;
-    const int t0 = blockIdx.x * SH_TT;
-    const int nv = min(SH_TT, P.T - t0);
     const int b = bh / P.H, h = bh % P.H;
-    sh_load_x<TX>(sX, P, b, h, t0, nv);
+    const int ntt = (P.T + SH_TT - 1) / SH_TT;
+    const int tt1 = min(ntt, ((int)blockIdx.x + 1) * P.tpw);
     for (int i = threadIdx.x; i < SH_TT * PG; i += 256)  // the padding columns stay zero
         sGP[i] = 0.0f;
+    if (P.M == 1)  // one set of planes for every tile
+        sh_load_planes(sPl, P.planes, P);
     constexpr int R = 1 << KB;
     const int S = P.L * R;
     const bool vec_in = (reinterpret_cast<uintptr_t>(P.gprobs) & 15) == 0;
-    // dx items: (row group, d) pairs, SH_RB rows each; at most SH_TT / SH_RB * 256 for D <= 256
-    constexpr int MAXI = SH_TT / SH_RB;
-    float gx[MAXI][SH_RB];
-#pragma unroll
-    for (int o = 0; o < MAXI; ++o)
-#pragma unroll
-        for (int q = 0; q < SH_RB; ++q)
-            gx[o][q] = 0.0f;
+    // dx items: (row group, d) pairs, SH_RB rows each: SH_TT / SH_RB * D of them over 256 threads
+    constexpr int MAXI = DI;
+    static_assert(SH_TT / SH_RB * 32 == 256, "D <= 32 * DI gives at most DI items per thread");
     float gsu = 0.0f;  // sum of gu * u over this thread's (token, table) items
-    for (int m = 0; m < P.M; ++m) {
-        __syncthreads();
-        sh_load_planes(sPl, P.planes + (int64_t)(P.unshared ? m : 0) * P.plane_stride, P);
-        __syncthreads();
-        sh_project(sX, sPl, sU, P);
-        __syncthreads();
-        const float *gprobs = P.gprobs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
-        for (int i = threadIdx.x; i < SH_TT * P.L; i += blockDim.x) {
-            const int r = i / P.L, l = i % P.L;
-            float u[KB], s0[KB], s1[KB], gu[KB];
+    // tiles of SH_TT tokens. Per member: barrier, planes (several members only), barrier,
+    // projection, barrier, gproj, barrier, dx products; every LDS buffer is rewritten only after
+    // a barrier that all of its readers have passed
+    for (int tt = blockIdx.x * P.tpw; tt < tt1; ++tt) {
+        const int t0 = tt * SH_TT;
+        const int nv = min(SH_TT, P.T - t0);
+        float gx[MAXI][SH_RB];
 #pragma unroll
-            for (int k = 0; k < KB; ++k) {
-                u[k] = sU[r * P.LK + l * KB + k];
-                sigm_pair(u[k], s0[k], s1[k]);
-                gu[k] = 0.0f;
+        for (int o = 0; o < MAXI; ++o)
+#pragma unroll
+            for (int q = 0; q < SH_RB; ++q)
+                gx[o][q] = 0.0f;
+        sh_load_x<TX>(sX, P, b, h, t0, nv);
+        for (int m = 0; m < P.M; ++m) {
+            __syncthreads();
+            if (P.M > 1) {
+                sh_load_planes(sPl, P.planes + (int64_t)(P.unshared ? m : 0) * P.plane_stride, P);
+                __syncthreads();
             }
-            if (r < nv) {
-                const float *gp = gprobs + (int64_t)(t0 + r) * S + l * R;
-                if constexpr (KB <= 4) {
-                    // gz_c = p_c (gp_c - sum p gp); gu_k = sum_c sign_k(c) gz_c with sign +1 where
-                    // bit k of c is set: a butterfly from the least significant bit, pair sums
-                    // feed the next level and pair differences sum to that bit's gu
-                    float p[R], z[R], g[R];
-                    if (R % 4 == 0 && vec_in) {
+            sh_project(sX, sPl, sU, P);
+            __syncthreads();
+            const float *gprobs = P.gprobs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
+            for (int i = threadIdx.x; i < SH_TT * P.L; i += blockDim.x) {
+                const int r = i / P.L, l = i % P.L;
+                float u[KB], s0[KB], s1[KB], gu[KB];
 #pragma unroll
-                        for (int c = 0; c < R; c += 4) {
-                            const f32x4 w = *reinterpret_cast<const f32x4 *>(gp + c);
-                            g[c] = w[0];
-                            g[c + 1] = w[1];
-                            g[c + 2] = w[2];
-                            g[c + 3] = w[3];
+                for (int k = 0; k < KB; ++k) {
+                    u[k] = sU[r * P.LK + l * KB + k];
+                    sigm_pair(u[k], s0[k], s1[k]);
+                    gu[k] = 0.0f;
+                }
+                if (r < nv) {
+                    const float *gp = gprobs + (int64_t)(t0 + r) * S + l * R;
+                    if constexpr (KB <= 4) {
+                        // gz_c = p_c (gp_c - sum p gp); gu_k = sum_c sign_k(c) gz_c with sign +1 where
+                        // bit k of c is set: a butterfly from the least significant bit, pair sums
+                        // feed the next level and pair differences sum to that bit's gu
+                        float p[R], z[R], g[R];
+                        if (R % 4 == 0 && vec_in) {
+#pragma unroll
+                            for (int c = 0; c < R; c += 4) {
+                                const f32x4 w = *reinterpret_cast<const f32x4 *>(gp + c);
+                                g[c] = w[0];
+                                g[c + 1] = w[1];
+                                g[c + 2] = w[2];
+                                g[c + 3] = w[3];
+                            }
+                        } else {
+#pragma unroll
+                            for (int c = 0; c < R; ++c)
+                                g[c] = gp[c];
                         }
-                    } else {
+                        corner_probs<KB>(s0, s1, p);
+                        float dot = 0.0f;
 #pragma unroll
                         for (int c = 0; c < R; ++c)
-                            g[c] = gp[c];
-                    }
-                    corner_probs<KB>(s0, s1, p);
-                    float dot = 0.0f;
+                            dot += p[c] * g[c];
 #pragma unroll
-                    for (int c = 0; c < R; ++c)
-                        dot += p[c] * g[c];
+                        for (int c = 0; c < R; ++c)
+                            z[c] = p[c] * (g[c] - dot);
 #pragma unroll
-                    for (int c = 0; c < R; ++c)
-                        z[c] = p[c] * (g[c] - dot);
+                        for (int lvl = 0; lvl < KB; ++lvl) {
+                            const int n = R >> (lvl + 1);
+                            float acc = 0.0f;
 #pragma unroll
-                    for (int lvl = 0; lvl < KB; ++lvl) {
-                        const int n = R >> (lvl + 1);
-                        float acc = 0.0f;
-#pragma unroll
-                        for (int q = 0; q < n; ++q) {
-                            acc += z[2 * q + 1] - z[2 * q];
-                            z[q] = z[2 * q] + z[2 * q + 1];
+                            for (int q = 0; q < n; ++q) {
+                                acc += z[2 * q + 1] - z[2 * q];
+                                z[q] = z[2 * q] + z[2 * q + 1];
+                            }
+                            gu[KB - 1 - lvl] = acc;
                         }
-                        gu[KB - 1 - lvl] = acc;
-                    }
-                } else {
-                    float dot = 0.0f;
-                    for (int c = 0; c < R; ++c)
-                        dot += corner_prob<KB>(s0, s1, c) * gp[c];
-                    for (int c = 0; c < R; ++c) {
-                        const float gz = corner_prob<KB>(s0, s1, c) * (gp[c] - dot);
+                    } else {
+                        float dot = 0.0f;
+                        for (int c = 0; c < R; ++c)
+                            dot += corner_prob<KB>(s0, s1, c) * gp[c];
+                        for (int c = 0; c < R; ++c) {
+                            const float gz = corner_prob<KB>(s0, s1, c) * (gp[c] - dot);
 #pragma unroll
-                        for (int k = 0; k < KB; ++k)
-                            gu[k] += ((c >> (KB - 1 - k)) & 1) ? gz : -gz;
+                            for (int k = 0; k < KB; ++k)
+                                gu[k] += ((c >> (KB - 1 - k)) & 1) ? gz : -gz;
+                        }
                     }
+#pragma unroll
+                    for (int k = 0; k < KB; ++k)
+                        gsu += gu[k] * u[k];
                 }
 #pragma unroll
-                for (int k = 0; k < KB; ++k)
-                    gsu += gu[k] * u[k];
+                for (int k = 0; k < KB; ++k) {
+                    const float th = u[k] * P.scale;
+                    sGP[r * PG + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+                }
             }
+            __syncthreads();
+            // gx[r][d] += sum_j gproj[r][j] planes[d][j]: SH_RB rows of one d per item, both operands
+            // read as 16-byte runs over j (gproj shared by the lanes of a row group)
 #pragma unroll
-            for (int k = 0; k < KB; ++k) {
-                const float th = u[k] * P.scale;
-                sGP[r * PG + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+            for (int o = 0; o < MAXI; ++o) {
+                const int i = threadIdx.x + o * 256;
+                if (i < (SH_TT / SH_RB) * P.D) {
+                    const int rg = i / P.D, d = i - rg * P.D;
+                    const float *gr = sGP + rg * SH_RB * PG;
+                    const float *pr = sPl + d * PL;
+                    float acc[SH_RB] = {};
+                    for (int j = 0; j < PG; j += 4) {
+                        const f32x4 pv = *reinterpret_cast<const f32x4 *>(pr + j);
+#pragma unroll
+                        for (int q = 0; q < SH_RB; ++q) {
+                            const f32x4 gv = *reinterpret_cast<const f32x4 *>(gr + q * PG + j);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                acc[q] += gv[e] * pv[e];
+                        }
+                    }
+#pragma unroll
+                    for (int q = 0; q < SH_RB; ++q)
+                        gx[o][q] += acc[q];
+                }
             }
         }
-        __syncthreads();
-        // gx[r][d] += sum_j gproj[r][j] planes[d][j]: SH_RB rows of one d per item, both operands
-        // read as 16-byte runs over j (gproj shared by the lanes of a row group)
+        TX *dx = reinterpret_cast<TX *>(const_cast<void *>(P.dx.p));
 #pragma unroll
         for (int o = 0; o < MAXI; ++o) {
             const int i = threadIdx.x + o * 256;
             if (i < (SH_TT / SH_RB) * P.D) {
                 const int rg = i / P.D, d = i - rg * P.D;
-                const float *gr = sGP + rg * SH_RB * PG;
-                const float *pr = sPl + d * PL;
-                float acc[SH_RB] = {};
-                for (int j = 0; j < PG; j += 4) {
-                    const f32x4 pv = *reinterpret_cast<const f32x4 *>(pr + j);
 #pragma unroll
-                    for (int q = 0; q < SH_RB; ++q) {
-                        const f32x4 gv = *reinterpret_cast<const f32x4 *>(gr + q * PG + j);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[q] += gv[e] * pv[e];
-                    }
+                for (int q = 0; q < SH_RB; ++q) {
+                    const int r = rg * SH_RB + q;
+                    if (r < nv)
+                        dx[b * P.dx.sb + h * P.dx.sh + (int64_t)(t0 + r) * P.dx.st + d] = (TX)gx[o][q];
                 }
-#pragma unroll
-                for (int q = 0; q < SH_RB; ++q)
-                    gx[o][q] += acc[q];
-            }
-        }
-    }
-    TX *dx = reinterpret_cast<TX *>(const_cast<void *>(P.dx.p));
-#pragma unroll
-    for (int o = 0; o < MAXI; ++o) {
-        const int i = threadIdx.x + o * 256;
-        if (i < (SH_TT / SH_RB) * P.D) {
-            const int rg = i / P.D, d = i - rg * P.D;
-#pragma unroll
-            for (int q = 0; q < SH_RB; ++q) {
-                const int r = rg * SH_RB + q;
-                if (r < nv)
-                    dx[b * P.dx.sb + h * P.dx.sh + (int64_t)(t0 + r) * P.dx.st + d] = (TX)gx[o][q];
             }
         }
     }
@@ -524,25 +543,28 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
     }
 }
 
-// kernel of bit count K (1..8) for one direction and dtype
+// kernel of bit count K (1..8) for one direction, dtype and head-dim class (D <= 64, 128, 256)
 template <class TX, int KB>
-static const void *softhash_kernel(int bwd)
+static const void *softhash_kernel(int bwd, int D)
 {
-    return bwd ? (const void *)race_softhash_bwd<TX, KB> : (const void *)race_softhash_fwd<TX, KB>;
+    if (!bwd)
+        return (const void *)race_softhash_fwd<TX, KB>;
+    return D <= 64 ? (const void *)race_softhash_bwd<TX, KB, 2>
+                   : D <= 128 ? (const void *)race_softhash_bwd<TX, KB, 4> : (const void *)race_softhash_bwd<TX, KB, 8>;
 }
 
 template <class TX>
-static const void *softhash_kernel_k(int K, int bwd)
+static const void *softhash_kernel_k(int K, int bwd, int D)
 {
     switch (K) {
-    case 1: return softhash_kernel<TX, 1>(bwd);
-    case 2: return softhash_kernel<TX, 2>(bwd);
-    case 3: return softhash_kernel<TX, 3>(bwd);
-    case 4: return softhash_kernel<TX, 4>(bwd);
-    case 5: return softhash_kernel<TX, 5>(bwd);
-    case 6: return softhash_kernel<TX, 6>(bwd);
-    case 7: return softhash_kernel<TX, 7>(bwd);
-    case 8: return softhash_kernel<TX, 8>(bwd);
+    case 1: return softhash_kernel<TX, 1>(bwd, D);
+    case 2: return softhash_kernel<TX, 2>(bwd, D);
+    case 3: return softhash_kernel<TX, 3>(bwd, D);
+    case 4: return softhash_kernel<TX, 4>(bwd, D);
+    case 5: return softhash_kernel<TX, 5>(bwd, D);
+    case 6: return softhash_kernel<TX, 6>(bwd, D);
+    case 7: return softhash_kernel<TX, 7>(bwd, D);
+    case 8: return softhash_kernel<TX, 8>(bwd, D);
     default: return nullptr;
     }
 }
@@ -553,15 +575,30 @@ size_t softhash_smem(int D, int LK, bool bwd)
     return sizeof(float) * (DX * sh_pl(LK) + SH_TT * DX + (size_t)SH_TT * LK + (bwd ? (size_t)SH_TT * sh_pg(LK) : 0));
 }
 
+int softhash_tiles_per_wg(int T, int B, int H)
+{
+    // a workgroup walks up to 8 consecutive tiles of one (b, h) (planes loaded once), as long as
+    // the grid keeps about 2048 workgroups (8 per CU)
+    const int64_t tiles = (int64_t)((T + SH_TT - 1) / SH_TT) * B * H;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(8, tiles / 2048));
+}
+
+int softhash_grid_x(int T, int B, int H)
+{
+    const int ntt = (T + SH_TT - 1) / SH_TT, tpw = softhash_tiles_per_wg(T, B, H);
+    return (ntt + tpw - 1) / tpw;
+}
+
 hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s)
 {
-    const void *fn = bf16 ? softhash_kernel_k<__bf16>(P.K, bwd) : softhash_kernel_k<float>(P.K, bwd);
+    const void *fn = bf16 ? softhash_kernel_k<__bf16>(P.K, bwd, P.D) : softhash_kernel_k<float>(P.K, bwd, P.D);
     if (!fn)
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((P.T + SH_TT - 1) / SH_TT), (unsigned)(P.B * P.H),
+    const dim3 grid((unsigned)softhash_grid_x(P.T, P.B, P.H), (unsigned)(P.B * P.H),
                     (unsigned)(bwd ? 1 : (P.unshared ? P.M : 1)));
     const size_t smem = softhash_smem(P.D, P.LK, bwd);
     SoftHashParams args = P;
+    args.tpw = softhash_tiles_per_wg(P.T, P.B, P.H);
     void *argv[] = {&args};
     return hipLaunchKernel(fn, grid, dim3(256), argv, smem, s);
 }
@@ -573,9 +610,10 @@ hipError_t softhash_prepare(int D, int LK)
     if (smem > 64 * 1024) {
         for (int K = 1; K <= 8 && e == hipSuccess; ++K)
             for (int bwd = 0; bwd < 2 && e == hipSuccess; ++bwd) {
-                e = hipFuncSetAttribute(softhash_kernel_k<float>(K, bwd), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+                e = hipFuncSetAttribute(softhash_kernel_k<float>(K, bwd, D), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        smem);
                 if (e == hipSuccess)
-                    e = hipFuncSetAttribute(softhash_kernel_k<__bf16>(K, bwd),
+                    e = hipFuncSetAttribute(softhash_kernel_k<__bf16>(K, bwd, D),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, smem);
             }
     }

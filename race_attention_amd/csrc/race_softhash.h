@@ -7,7 +7,7 @@
 
 namespace race {
 
-constexpr int SH_TT = 32;  // tokens per workgroup
+constexpr int SH_TT = 32;  // tokens per tile; a workgroup walks tpw consecutive tiles
 
 struct SoftHashParams {
     View x;               // [B][H][T][D] input (fp32 or bf16)
@@ -21,9 +21,12 @@ struct SoftHashParams {
     int round_planes;     // 1: round planes to bf16 (bf16 inputs, as race_common.py:54)
     float scale, inv_scale;
     float *gscale;        // backward, optional: per-workgroup sums of gu * u (temperature grad)
+    int tpw;              // tiles per workgroup (set by launch_softhash)
 };
 
 size_t softhash_smem(int D, int LK, bool bwd);
+int softhash_tiles_per_wg(int T, int B, int H);
+int softhash_grid_x(int T, int B, int H);  // workgroups along the tiles of one (b, h)
 hipError_t softhash_prepare(int D, int LK);
 hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s);
 

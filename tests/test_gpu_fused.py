@@ -135,6 +135,31 @@ def test_soft_hash_probs_fp32(dev):
         check("dK", Kd.grad, K64.grad, 1e-4)
 
 
+@pytest.mark.parametrize("B,H,T,L,Kb,M,share", [(4, 8, 4141, 4, 3, 2, False), (4, 8, 16389, 2, 2, 1, True)])
+def test_soft_hash_probs_multi_tile(dev, B, H, T, L, Kb, M, share):
+    """Enough 32-token tiles that each soft-hash workgroup walks several of them (2 and 8 per
+    workgroup here), with a ragged last tile and a last workgroup that holds fewer tiles."""
+    from race_attention_amd import build_planes_protos, soft_hash_probs
+    D = 64
+    print(f"case B={B} H={H} T={T} L={L} K={Kb} M={M} share={share}", flush=True)
+    planes_T, protos_T = build_planes_protos(D, Kb, L, M, device=dev, share_planes=share, seed=4)
+    g = torch.Generator().manual_seed(T)
+    Q, K, V = (torch.randn(B, H, T, D, generator=g) for _ in range(3))
+    Qd, Kd, Vd = (x.to(dev).requires_grad_(True) for x in (Q, K, V))
+    pK, pQ, V2, N = soft_hash_probs(Qd, Kd, Vd, planes_T, protos_T, L, Kb, M, share)
+    Q64, K64 = (x.double().requires_grad_(True) for x in (Q, K))
+    rK, rQ, _, rN = orc.soft_hash_probs(Q64, K64, V, planes_T.cpu(), protos_T.cpu(), L, Kb, M, share)
+    assert N == rN and pK.shape == rK.shape
+    check("probsK", pK, rK.detach(), 1e-5)
+    check("probsQ", pQ, rQ.detach(), 1e-5)
+    gk = torch.randn(pK.shape, generator=g)
+    gq = torch.randn(pQ.shape, generator=g)
+    torch.autograd.backward([pK, pQ], [gk.to(dev), gq.to(dev)])
+    torch.autograd.backward([rK, rQ], [gk.double(), gq.double()])
+    check("dQ", Qd.grad, Q64.grad, 1e-4)
+    check("dK", Kd.grad, K64.grad, 1e-4)
+
+
 def test_soft_hash_probs_golden(dev):
     """Against the reference's own outputs (tests/golden, written by scaling/race_common.py)."""
     from race_attention_amd import soft_hash_probs

@@ -83,6 +83,30 @@ def test_batched_ace_noncausal_module(dev, share, M):
     check("race_attention", o4, r4, TOL)
 
 
+def test_soft_hash_temperature_grad_multi_tile(dev):
+    """d loss / d scale summed from the per-workgroup partials when every workgroup walks several
+    32-token tiles (2 per workgroup here, ragged last tile), against the fp64 softmax form."""
+    from race_attention_amd import build_planes_protos
+    from race_attention_amd.noncausal import SoftHashTempFn
+    L, Kb, D, B, H, T = 2, 2, 64, 4, 8, 4141
+    planes_T, protos_T = build_planes_protos(D, Kb, L, 1, device=dev, seed=6)
+    g = torch.Generator().manual_seed(6)
+    X = torch.randn(B, H, T, D, generator=g)
+    gp = torch.randn(B * H, T, L << Kb, generator=g)
+    xd = X.to(dev).requires_grad_(True)
+    sd = torch.tensor(0.7, device=dev, requires_grad=True)
+    p = SoftHashTempFn.apply(xd, planes_T, L, Kb, 1, False, sd)
+    p.backward(gp.to(dev))
+    X64 = X.double().requires_grad_(True)
+    s64 = torch.tensor(0.7, dtype=torch.float64, requires_grad=True)
+    ref, _, _, _ = orc.soft_hash_probs(X64.detach(), X64, X64.detach(), planes_T.cpu(), protos_T.cpu(), L, Kb,
+                                       scale=s64)
+    ref.backward(gp.double())
+    check("probs", p, ref.detach(), 1e-5)
+    check("dX", xd.grad, X64.grad, 1e-4)
+    check("dscale", sd.grad.reshape(1), s64.grad.reshape(1), 1e-4)
+
+
 def test_soft_hash_extreme_temperature(dev):
     """Temperature at BatchedACE's lower clamp (scale 0.01, scaling/benchmark_time.py:111):
     u = tanh(proj) / scale reaches +-100, where exp(-2u) overflows fp32 unless the corner
