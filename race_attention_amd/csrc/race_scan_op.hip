@@ -7,20 +7,19 @@ namespace race {
 template <int ST, int DP>
 static hipError_t launch_v(ScanKernel k, const ScanParams &P, dim3 grid, hipStream_t s)
 {
-    constexpr int C = OP_C, NW = OP_NW;
-    const dim3 block(NW * 64);
+    constexpr int C = OP_C, NWT = OP_NW_TOTALS, NWM = op_nw_main(DP);
     switch (k) {
     case K_FWD_TOTALS:
-        hipLaunchKernelGGL((race_fwd_totals<EngF32, MODE_OP, ST, DP, C, NW>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_fwd_totals<EngF32, MODE_OP, ST, DP, C, NWT>), grid, dim3(NWT * 64), 0, s, P);
         break;
     case K_FWD_READOUT:
-        hipLaunchKernelGGL((race_fwd_readout<EngF32, MODE_OP, ST, DP, C, NW>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_fwd_readout<EngF32, MODE_OP, ST, DP, C, NWM>), grid, dim3(NWM * 64), 0, s, P);
         break;
     case K_BWD_TOTALS:
-        hipLaunchKernelGGL((race_bwd_totals<EngF32, MODE_OP, ST, DP, C, NW>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_bwd_totals<EngF32, MODE_OP, ST, DP, C, NWT>), grid, dim3(NWT * 64), 0, s, P);
         break;
     case K_BWD_MAIN:
-        hipLaunchKernelGGL((race_bwd_main<EngF32, MODE_OP, ST, DP, C, NW>), grid, block, 0, s, P);
+        hipLaunchKernelGGL((race_bwd_main<EngF32, MODE_OP, ST, DP, C, NWM>), grid, dim3(NWM * 64), 0, s, P);
         break;
     }
     return hipGetLastError();
