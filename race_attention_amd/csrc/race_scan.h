@@ -131,36 +131,42 @@ RACE_DEV void load_rows_bf16(__bf16 *dst, __bf16 *dstT, const View &vw, int b, i
     }
 }
 
-// fp32 rows of an [N][T][D] tensor (any D <= DP) into dst [C][LD] / dstT [DP][LDT].
-template <int C, int DP, int NTH, int LD, int LDT, bool ROW, bool TRN>
-RACE_DEV void load_rows_f32(float *dst, float *dstT, const float *src, int D, int t0, int nv,
-                            int tid)
-{
-    for (int i = tid; i < C * DP; i += NTH) {
-        const int r = i / DP, d = i % DP;
-        const float x = (r < nv && d < D) ? src[(int64_t)(t0 + r) * D + d] : 0.0f;
-        if (ROW)
-            dst[r * LD + d] = x;
-        if (TRN)
-            dstT[d * LDT + r] = x;
-    }
-}
+// Register-staged copy of one sub-chunk of an fp32 [N][T][ld] tensor (rows t0 .. t0 + C, columns
+// col0 .. col0 + W): fetch() issues this thread's loads, put() stores them to LDS [C][LD] and / or
+// transposed [W][LDT]. Loads go to clamped rows and columns (always inside the tensor) and are
+// unconditional, so a later wait on the in-order memory counter does not have to drain them early;
+// put() writes zeros for rows >= nv and columns >= ncol. Fetching sub-chunk i + 1 before the
+// MFMA phase of sub-chunk i overlaps its memory latency with that phase.
+template <int C, int W, int NTH>
+struct SubChunkStage {
+    static constexpr int N = (C * W + NTH - 1) / NTH;
+    float x[N];
 
-// fp32 probabilities [N][T][S], bucket columns [s0, s0+ST) of rows t0.., into
-// dst [C][LD] (T) / dstT [ST][LDT] (T); rows >= nv and buckets >= S_here are zero.
-template <class T, int C, int ST, int NTH, int LD, int LDT, bool ROW, bool TRN>
-RACE_DEV void load_probs(T *dst, T *dstT, const float *src, int S, int s0, int S_here, int t0,
-                         int nv, int tid)
-{
-    for (int i = tid; i < C * ST; i += NTH) {
-        const int r = i / ST, s = i % ST;
-        const float x = (r < nv && s < S_here) ? src[(int64_t)(t0 + r) * S + s0 + s] : 0.0f;
-        if (ROW)
-            dst[r * LD + s] = (T)x;
-        if (TRN)
-            dstT[s * LDT + r] = (T)x;
+    RACE_DEV void fetch(const float *src, int ld, int col0, int ncol, int t0, int t_last, int tid)
+    {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = tid + j * NTH, r = i / W, s = i % W;
+            x[j] = src[(int64_t)min(t0 + r, t_last) * ld + col0 + min(s, ncol - 1)];
+        }
     }
-}
+
+    template <class T, int LD, int LDT, bool ROW, bool TRN>
+    RACE_DEV void put(T *dst, T *dstT, int nv, int ncol, int tid) const
+    {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = tid + j * NTH, r = i / W, s = i % W;
+            if (C * W % NTH == 0 || i < C * W) {
+                const float v = (r < nv && s < ncol) ? x[j] : 0.0f;
+                if (ROW)
+                    dst[r * LD + s] = (T)v;
+                if (TRN)
+                    dstT[s * LDT + r] = (T)v;
+            }
+        }
+    }
+};
 
 // ------------------------------------------------------------------ soft-hash pieces
 // Constant planes fragments for this wave (QKV mode only):

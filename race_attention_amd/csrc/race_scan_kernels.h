@@ -90,6 +90,14 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
     __syncthreads();
 
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    // op mode: this sub-chunk's probabilities and values wait in registers, fetched one sub-chunk ahead
+    SubChunkStage<C, ST, NTH> stP;
+    SubChunkStage<C, DP, NTH> stV;
+    const float *srcP = P.pK + (int64_t)c.z * P.T * P.S, *srcV = P.V + (int64_t)c.z * P.T * P.D;
+    if constexpr (!CF::QKV) {
+        stP.fetch(srcP, P.S, c.s0, c.S_here, c.t_begin, P.T - 1, c.tid);
+        stV.fetch(srcV, P.D, 0, P.D, c.t_begin, P.T - 1, c.tid);
+    }
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -108,10 +116,11 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
                         sPKt[lt * R + r][t] = (T)(ok ? pr[r] : 0.0f);
             });
         } else {
-            load_probs<T, C, ST, NTH, LDC, LDC, false, true>(nullptr, &sPKt[0][0], P.pK + (int64_t)c.z * P.T * P.S,
-                                                           P.S, c.s0, c.S_here, t0, nv, c.tid);
-            load_rows_f32<C, DP, NTH, LDC, LDC, false, true>(nullptr, reinterpret_cast<float *>(&sVt[0][0]),
-                                                           P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+            stP.template put<T, LDC, LDC, false, true>(nullptr, &sPKt[0][0], nv, c.S_here, c.tid);
+            stV.template put<T, LDC, LDC, false, true>(nullptr, &sVt[0][0], nv, P.D, c.tid);
+            // next sub-chunk (past the block end: clamped rows, never stored)
+            stP.fetch(srcP, P.S, c.s0, c.S_here, t0 + C, P.T - 1, c.tid);
+            stV.fetch(srcV, P.D, 0, P.D, t0 + C, P.T - 1, c.tid);
         }
         __syncthreads();
 #pragma unroll
@@ -205,6 +214,16 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
 
     f32x4 accA[CF::TPW_CS];
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    // op mode: this sub-chunk's pK, pQ and values wait in registers, fetched one sub-chunk ahead
+    SubChunkStage<C, ST, NTH> stK, stQ;
+    SubChunkStage<C, DP, NTH> stV;
+    const float *srcK = P.pK + (int64_t)c.z * P.T * P.S, *srcQ = P.pQ + (int64_t)c.z * P.T * P.S;
+    const float *srcV = P.V + (int64_t)c.z * P.T * P.D;
+    if constexpr (!CF::QKV) {
+        stK.fetch(srcK, P.S, c.s0, c.S_here, c.t_begin, P.T - 1, c.tid);
+        stQ.fetch(srcQ, P.S, c.s0, c.S_here, c.t_begin, P.T - 1, c.tid);
+        stV.fetch(srcV, P.D, 0, P.D, c.t_begin, P.T - 1, c.tid);
+    }
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -226,12 +245,12 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
                     }
             });
         } else {
-            const float *pk = P.pK + (int64_t)c.z * P.T * P.S;
-            load_probs<T, C, ST, NTH, LDS_, LDC, true, true>(&sPK[0][0], &sPKt[0][0], pk, P.S, c.s0, c.S_here, t0, nv, c.tid);
-            load_probs<float, C, ST, NTH, LDF, LDF, true, false>(&sF[0][0], nullptr, P.pQ + (int64_t)c.z * P.T * P.S,
-                                                               P.S, c.s0, c.S_here, t0, nv, c.tid);
-            load_rows_f32<C, DP, NTH, LDC, LDC, false, true>(nullptr, reinterpret_cast<float *>(&sVt[0][0]),
-                                                           P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+            stK.template put<T, LDS_, LDC, true, true>(&sPK[0][0], &sPKt[0][0], nv, c.S_here, c.tid);
+            stQ.template put<float, LDF, LDF, true, false>(&sF[0][0], nullptr, nv, c.S_here, c.tid);
+            stV.template put<T, LDC, LDC, false, true>(nullptr, &sVt[0][0], nv, P.D, c.tid);
+            stK.fetch(srcK, P.S, c.s0, c.S_here, t0 + C, P.T - 1, c.tid);
+            stQ.fetch(srcQ, P.S, c.s0, c.S_here, t0 + C, P.T - 1, c.tid);
+            stV.fetch(srcV, P.D, 0, P.D, t0 + C, P.T - 1, c.tid);
         }
         __syncthreads();
 
@@ -403,6 +422,20 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
 
     f32x4 accA[CF::TPW_CS], accW[CF::TPW_CS], accG[CF::TPW_CS];
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    // op mode: this sub-chunk's pK, values, pQ and output gradient wait in registers, fetched one
+    // sub-chunk ahead
+    SubChunkStage<C, ST, NTH> stK, stQ;
+    SubChunkStage<C, DP, NTH> stV, stG;
+    const float *srcK = P.pK + (int64_t)c.z * P.T * P.S, *srcQ = P.pQ + (int64_t)c.z * P.T * P.S;
+    const float *srcV = P.V + (int64_t)c.z * P.T * P.D, *srcG = P.gO + (int64_t)c.z * P.T * P.D;
+    auto fetch_op = [&](int t) {
+        stK.fetch(srcK, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
+        stV.fetch(srcV, P.D, 0, P.D, t, P.T - 1, c.tid);
+        stQ.fetch(srcQ, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
+        stG.fetch(srcG, P.D, 0, P.D, t, P.T - 1, c.tid);
+    };
+    if constexpr (!CF::QKV)
+        fetch_op(c.t_begin);
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -421,11 +454,8 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
                         sPKt[lt * R + r][t] = (T)(ok ? pr[r] : 0.0f);
             });
         } else {
-            load_probs<T, C, ST, NTH, LDC, LDC, false, true>(nullptr, &sPKt[0][0], P.pK + (int64_t)c.z * P.T * P.S,
-                                                           P.S, c.s0, c.S_here, t0, nv, c.tid);
-            load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sV[0][0]),
-                                                          reinterpret_cast<float *>(&sVt[0][0]),
-                                                          P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+            stK.template put<T, LDC, LDC, false, true>(nullptr, &sPKt[0][0], nv, c.S_here, c.tid);
+            stV.template put<T, LDX, LDC, true, true>(&sV[0][0], &sVt[0][0], nv, P.D, c.tid);
         }
         __syncthreads();
 
@@ -471,11 +501,9 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
                             sF[t][lt * R + r] = ok ? pr[r] : 0.0f;
                 });
             } else {
-                load_probs<float, C, ST, NTH, LDF, LDF, true, false>(&sF[0][0], nullptr, P.pQ + (int64_t)c.z * P.T * P.S,
-                                                                   P.S, c.s0, c.S_here, t0, nv, c.tid);
-                load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sGO[0][0]),
-                                                              reinterpret_cast<float *>(&sGOt[0][0]),
-                                                              P.gO + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+                stQ.template put<float, LDF, LDF, true, false>(&sF[0][0], nullptr, nv, c.S_here, c.tid);
+                stG.template put<T, LDX, LDC, true, true>(&sGO[0][0], &sGOt[0][0], nv, P.D, c.tid);
+                fetch_op(t0 + C);  // next sub-chunk (op mode has one query head: once per sub-chunk)
             }
             __syncthreads();
             // W = pQ/(A+eps) -> sWt ; gW = go St^T ; Mg = tril(go V^T)
@@ -697,6 +725,20 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
     f32x4 accA[CF::TPW_CS], accW[CF::TPW_CS], accG[CF::TPW_CS], accGA[CF::TPW_CS], accPK[CF::TPW_CS];
     f32x4 accV[CF::TPW_CD];
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    // op mode: this sub-chunk's pK, values, pQ and output gradient wait in registers, fetched one
+    // sub-chunk ahead
+    SubChunkStage<C, ST, NTH> stK, stQ;
+    SubChunkStage<C, DP, NTH> stV, stG;
+    const float *srcK = P.pK + (int64_t)c.z * P.T * P.S, *srcQ = P.pQ + (int64_t)c.z * P.T * P.S;
+    const float *srcV = P.V + (int64_t)c.z * P.T * P.D, *srcG = P.gO + (int64_t)c.z * P.T * P.D;
+    auto fetch_op = [&](int t) {
+        stK.fetch(srcK, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
+        stV.fetch(srcV, P.D, 0, P.D, t, P.T - 1, c.tid);
+        stQ.fetch(srcQ, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
+        stG.fetch(srcG, P.D, 0, P.D, t, P.T - 1, c.tid);
+    };
+    if constexpr (!CF::QKV)
+        fetch_op(c.t_begin);
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -718,11 +760,8 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
                     }
             });
         } else {
-            load_probs<T, C, ST, NTH, LDS_, LDC, true, true>(&sPK[0][0], &sPKt[0][0], P.pK + (int64_t)c.z * P.T * P.S,
-                                                           P.S, c.s0, c.S_here, t0, nv, c.tid);
-            load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sV[0][0]),
-                                                          reinterpret_cast<float *>(&sVt[0][0]),
-                                                          P.V + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+            stK.template put<T, LDS_, LDC, true, true>(&sPK[0][0], &sPKt[0][0], nv, c.S_here, c.tid);
+            stV.template put<T, LDX, LDC, true, true>(&sV[0][0], &sVt[0][0], nv, P.D, c.tid);
         }
         // the state at this sub-chunk's start, for gW = go St^T
 #pragma unroll
@@ -781,11 +820,9 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
                             sF[t][lt * R + r] = ok ? pr[r] : 0.0f;
                 });
             } else {
-                load_probs<float, C, ST, NTH, LDF, LDF, true, false>(&sF[0][0], nullptr, P.pQ + (int64_t)c.z * P.T * P.S,
-                                                                   P.S, c.s0, c.S_here, t0, nv, c.tid);
-                load_rows_f32<C, DP, NTH, LDX, LDC, true, true>(reinterpret_cast<float *>(&sGO[0][0]),
-                                                              reinterpret_cast<float *>(&sGOt[0][0]),
-                                                              P.gO + (int64_t)c.z * P.T * P.D, P.D, t0, nv, c.tid);
+                stQ.template put<float, LDF, LDF, true, false>(&sF[0][0], nullptr, nv, c.S_here, c.tid);
+                stG.template put<T, LDX, LDC, true, true>(&sGO[0][0], &sGOt[0][0], nv, P.D, c.tid);
+                fetch_op(t0 + C);  // next sub-chunk (op mode has one query head: once per sub-chunk)
             }
             __syncthreads();
             // W -> sW, sWt ; gW = go St^T ; Mg = tril(go V^T) -> sMg, sMv
