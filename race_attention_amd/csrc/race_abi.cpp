@@ -93,9 +93,9 @@ int op_geometry(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block, Geo &
     if (D > 256)
         return fail(RACE_ERR_UNSUPPORTED, "race_op: head dim D = %lld > 256 is not compiled", (long long)D);
     g.DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
-    // bucket tiles of at most 32: at 64 x 64 the backward main kernel's LDS allows one workgroup per
-    // CU, and the smaller tile measured faster at every shape tried (2k..256k tokens, S = 64, 128)
-    const int st_max = std::min(32, 4096 / g.DP);
+    // bucket tiles of at most 64 (the largest measured fastest at D = 32 and 64 for S = 64 and 128;
+    // 128-wide tiles at D = 32 are slower)
+    const int st_max = std::min(64, 4096 / g.DP);
     g.ST = st_max;
     for (int st : {16, 32, 64, 128})
         if (st <= st_max && st >= S) {
