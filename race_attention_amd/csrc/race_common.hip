@@ -276,15 +276,38 @@ RACE_DEV void sh_load_planes(float *sPl, const float *planes, const SoftHashPara
     }
 }
 
+// x rows of one tile into sX. vec: D % 4 == 0, and every row starts at a multiple of 4 elements
+// of a buffer aligned to 4 elements, so a row is read as runs of 4 elements (16 or 8 bytes)
 template <class TX>
-RACE_DEV void sh_load_x(float *sX, const SoftHashParams &P, int b, int h, int t0, int nv)
+RACE_DEV void sh_load_x(float *sX, const SoftHashParams &P, int b, int h, int t0, int nv, bool vec)
 {
     const int DX = sh_dx(P.D);
     const TX *x = reinterpret_cast<const TX *>(P.x.p);
+    if (vec) {
+        typedef TX tx4 __attribute__((ext_vector_type(4)));
+        const int D4 = DX / 4;
+        for (int i = threadIdx.x; i < SH_TT * D4; i += 256) {
+            const int r = i / D4, d = (i - r * D4) * 4;
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (r < nv) {
+                const tx4 w = *reinterpret_cast<const tx4 *>(x + b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d);
+                v = f32x4{(float)w[0], (float)w[1], (float)w[2], (float)w[3]};
+            }
+            *reinterpret_cast<f32x4 *>(sX + r * DX + d) = v;
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < SH_TT * DX; i += 256) {
         const int r = i / DX, d = i - r * DX;
         sX[i] = (r < nv && d < P.D) ? (float)x[b * P.x.sb + h * P.x.sh + (int64_t)(t0 + r) * P.x.st + d] : 0.0f;
     }
+}
+
+template <class TX>
+RACE_DEV bool sh_x_vec(const SoftHashParams &P)
+{
+    return (P.D & 3) == 0 && (reinterpret_cast<uintptr_t>(P.x.p) & (4 * sizeof(TX) - 1)) == 0 && (P.x.sb & 3) == 0 &&
+           (P.x.sh & 3) == 0 && (P.x.st & 3) == 0;
 }
 
 // sU[r][j] = tanh(sum_d x[r][d] planes[d][j]) / scale. A thread owns SH_RB rows of one column j:
@@ -333,16 +356,41 @@ __global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
     float *out = P.probs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
     // every token's run of R corners starts 16-byte aligned when the buffer does and R % 4 == 0
     const bool vec_out = (reinterpret_cast<uintptr_t>(P.probs) & 15) == 0;
+    const bool vec_x = sh_x_vec<TX>(P);
     sh_load_planes(sPl, P.planes + (int64_t)m * P.plane_stride, P);
     // tiles of SH_TT tokens; sX is free again once the projection's barrier is passed, and the
     // barrier after the x load keeps the next projection from overwriting sU under the readers
     for (int tt = blockIdx.x * P.tpw; tt < tt1; ++tt) {
         const int t0 = tt * SH_TT;
         const int nv = min(SH_TT, P.T - t0);
-        sh_load_x<TX>(sX, P, b, h, t0, nv);
+        sh_load_x<TX>(sX, P, b, h, t0, nv, vec_x);
         __syncthreads();
         sh_project(sX, sPl, sU, P);
         __syncthreads();
+        if constexpr (KB >= 2 && KB <= 4) {
+            if (vec_out) {
+                // R / 4 threads per (token, table), each storing 4 consecutive corners: consecutive
+                // threads write consecutive 16-byte runs. Corner c = 4q + c2 takes its KB - 2 high
+                // bits from q; products in the same order as corner_probs (bitwise equal).
+                constexpr int Q = R / 4;
+                for (int i = threadIdx.x; i < nv * P.L * Q; i += blockDim.x) {
+                    const int it = i / Q, q = i - it * Q;
+                    const int r = it / P.L, l = it - r * P.L;
+                    float s0[KB], s1[KB];
+#pragma unroll
+                    for (int k = 0; k < KB; ++k)
+                        sigm_pair(sU[r * P.LK + l * KB + k], s0[k], s1[k]);
+                    float pre = 1.0f;
+#pragma unroll
+                    for (int k = 0; k < KB - 2; ++k)
+                        pre *= ((q >> (KB - 3 - k)) & 1) ? s1[k] : s0[k];
+                    const float a0 = pre * s0[KB - 2], a1 = pre * s1[KB - 2];
+                    *reinterpret_cast<f32x4 *>(out + (int64_t)(t0 + r) * S + l * R + 4 * q) =
+                        f32x4{a0 * s0[KB - 1], a0 * s1[KB - 1], a1 * s0[KB - 1], a1 * s1[KB - 1]};
+                }
+                continue;
+            }
+        }
         for (int i = threadIdx.x; i < nv * P.L; i += blockDim.x) {
             const int r = i / P.L, l = i % P.L;
             float s0[KB], s1[KB];
@@ -353,15 +401,9 @@ __global__ __launch_bounds__(256) void race_softhash_fwd(SoftHashParams P)
             if constexpr (KB <= 4) {
                 float p[R];
                 corner_probs<KB>(s0, s1, p);
-                if (R % 4 == 0 && vec_out) {
 #pragma unroll
-                    for (int c = 0; c < R; c += 4)
-                        *reinterpret_cast<f32x4 *>(o + c) = f32x4{p[c], p[c + 1], p[c + 2], p[c + 3]};
-                } else {
-#pragma unroll
-                    for (int c = 0; c < R; ++c)
-                        o[c] = p[c];
-                }
+                for (int c = 0; c < R; ++c)
+                    o[c] = p[c];
             } else {
                 for (int c = 0; c < R; ++c)
                     o[c] = corner_prob<KB>(s0, s1, c);
@@ -392,6 +434,7 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
     constexpr int R = 1 << KB;
     const int S = P.L * R;
     const bool vec_in = (reinterpret_cast<uintptr_t>(P.gprobs) & 15) == 0;
+    const bool vec_x = sh_x_vec<TX>(P);
     // dx items: (row group, d) pairs, SH_RB rows each: SH_TT / SH_RB * D of them over 256 threads
     constexpr int MAXI = DI;
     static_assert(SH_TT / SH_RB * 32 == 256, "D <= 32 * DI gives at most DI items per thread");
@@ -408,7 +451,7 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
 #pragma unroll
             for (int q = 0; q < SH_RB; ++q)
                 gx[o][q] = 0.0f;
-        sh_load_x<TX>(sX, P, b, h, t0, nv);
+        sh_load_x<TX>(sX, P, b, h, t0, nv, vec_x);
         for (int m = 0; m < P.M; ++m) {
             __syncthreads();
             if (P.M > 1) {
