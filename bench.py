@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (x3), the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
-    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5"],
+    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5", "noncausal", "linear"],
                     help="cfg1: the reference's fp32 op path (soft_hash_probs + RaceCausalFn) fwd+bwd at "
                          "B=2, H=8, T=2048, D=64, L=8, K=4, scale sqrt(D) and 1.0, with the CPU path on the same "
                          "inputs; cfg2: the same layer step at B=4, H=16, T=65536, L=16 (S=256), q/k/v ~ N(0,1); "
@@ -125,6 +125,12 @@ def main():
         return
     if args.workload == "cfg1":
         print(json.dumps(bench_cfg1(torch, args)))
+        return
+    if args.workload == "noncausal":
+        print(json.dumps(bench_noncausal(torch, args)))
+        return
+    if args.workload == "linear":
+        print(json.dumps(bench_linear(torch, args)))
         return
     dev = torch.device("cuda:0")
     B, H, T, D, L, K = args.B, args.H, args.T, 64, args.L, 4
@@ -397,6 +403,150 @@ def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6):
             "gpu": gpu,
             "cpu_baseline": {"value": round(B * T / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
                              "sample": f"the whole cfg1 layer fwd+bwd (scale sqrt(D)), median of 3",
+                             "seconds_per_step": round(sec, 3)}}
+
+
+def _time_steps(torch, step, warmup, steps):
+    for _ in range(max(1, warmup)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _kernel_split(torch, _lib, step, steps):
+    """Per-kernel ms per step from the library's HIP events on its launch stream."""
+    _lib.profile(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kern = _lib.profile_read()
+    _lib.profile(False)
+    return {n: round(v[0] / steps, 4) for n, v in kern.items()}
+
+
+def _cpu_median(fn, reps=3):
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def bench_noncausal(torch, args, B=1, H=4, T=1 << 20, D=128, L=3, K=3, M=1, eps=1e-6):
+    """Non-causal BatchedACE (scaling/benchmark_time.py:77-166) at that benchmark's defaults (B=1,
+    H=4, D=128, race_L=3, race_Kbits=3, race_M=1; :357-372) and T = 2^20: fp32 inputs
+    [M,B,T,H,D] ~ N(0,1), one step = forward + backward incl. d loss / d temperature.
+    Per (token, head): 12 S D flops for the state contractions plus the soft-hash term of the layer
+    count; 11 fp32 rows of HBM traffic (q, k, v, out, go, dq, dk, dv with q, k, v read twice).
+    CPU: the fp64 restatement (oracle) fwd+bwd on all host cores on a T = 2^16 sample."""
+    from oracle import race_oracle as orc
+    from race_attention_amd import _lib
+    from race_attention_amd.noncausal import BatchedACE
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    ace = BatchedACE(D, K, L, M, device=dev, share_planes=True)
+    g = torch.Generator(device=dev).manual_seed(1)
+    Kh, Vh, Qh = (torch.randn(M, B, T, H, D, generator=g, device=dev).requires_grad_(True) for _ in range(3))
+    go = torch.randn(M, B, T, H, D, generator=g, device=dev)
+
+    def step():
+        for x in (Kh, Vh, Qh):
+            x.grad = None
+        ace.logit_temp.grad = None
+        ace(Kh, Vh, Qh, eps).backward(go)
+
+    ms = _time_steps(torch, step, args.warmup, args.steps)
+    split = _kernel_split(torch, _lib, step, 3)
+    S = L << K
+    n = M * B * H * T
+    flops = (12 * S * D + 6 * (2 * D * L * K + 2 * L * K * (1 << K) + 4 * S)) * n
+    nbytes = 11 * D * 4 * n
+    t_bound = max(flops / FP32_PEAK, nbytes / HBM_PEAK)
+    Tc = 1 << 16
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gc = torch.Generator().manual_seed(1)
+    Kc, Vc, Qc = (torch.randn(M, B, Tc, H, D, generator=gc, dtype=torch.float64).requires_grad_(True) for _ in range(3))
+    goc = torch.randn(M, B, Tc, H, D, generator=gc, dtype=torch.float64)
+    lt = torch.zeros((), dtype=torch.float64, requires_grad=True)
+    pl, pr = ace.planes_T.cpu(), ace.protos_T.cpu()
+
+    def run_cpu():
+        for x in (Kc, Vc, Qc, lt):
+            x.grad = None
+        orc.batched_ace_nc_ref(Kc, Vc, Qc, pl, pr, L, K, True, lt, eps).backward(goc)
+
+    sec = _cpu_median(run_cpu)
+    return {"metric": "non-causal RACE (BatchedACE) fwd+bwd tokens/sec", "value": round(B * T / (ms / 1e3), 1),
+            "unit": "tokens/s", "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "f32",
+            "data": "synthetic", "vs_baseline": None,
+            "config": {"workload": "noncausal", "B": B, "H": H, "T": T, "D": D, "L": L, "K": K, "M": M, "S": S},
+            "layer_roofline": {"bound": "hbm" if nbytes / HBM_PEAK >= flops / FP32_PEAK else "fp32 compute",
+                               "t_bound_ms": round(t_bound * 1e3, 4), "frac": round(t_bound * 1e3 / ms, 4)},
+            "kernels_ms_per_step": split,
+            "cpu_baseline": {"value": round(B * Tc / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+                             "sample": f"fp64 restatement fwd+bwd at T = 2^16 (same B, H, D, L, K), median of 3",
+                             "seconds_per_step": round(sec, 3)}}
+
+
+def bench_linear(torch, args, B=1, H=4, T=1 << 20, D=64):
+    """Causal linear attention (kernels/cpu/linear_pref.cpp:87-226, the comparison baseline) on the
+    chunked scan kernels: Q, K, V [B,H,T,D] fp32, Q, K ~ U(0,1) (positive features), V ~ N(0,1);
+    one step = forward + backward. Per (token, head): 12 D^2 flops, 11 fp32 rows of HBM traffic.
+    CPU: the fp64 cumulative-sum restatement (oracle) fwd+bwd on a T = 2^12 sample."""
+    from oracle import race_oracle as orc
+    from race_attention_amd import _lib
+    from race_attention_amd.linear_attention import causal_linear_attention
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1)
+    Q = torch.rand(B, H, T, D, generator=g, device=dev).requires_grad_(True)
+    Kk = torch.rand(B, H, T, D, generator=g, device=dev).requires_grad_(True)
+    V = torch.randn(B, H, T, D, generator=g, device=dev).requires_grad_(True)
+    go = torch.randn(B, H, T, D, generator=g, device=dev)
+
+    def step():
+        for x in (Q, Kk, V):
+            x.grad = None
+        causal_linear_attention(Q, Kk, V).backward(go)
+
+    ms = _time_steps(torch, step, args.warmup, args.steps)
+    split = _kernel_split(torch, _lib, step, 3)
+    n = B * H * T
+    flops = 12 * D * D * n
+    nbytes = 11 * D * 4 * n
+    t_bound = max(flops / FP32_PEAK, nbytes / HBM_PEAK)
+    Tc = 1 << 12
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gc = torch.Generator().manual_seed(1)
+    Qc = torch.rand(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
+    Kc = torch.rand(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
+    Vc = torch.randn(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
+    goc = torch.randn(B, H, Tc, D, generator=gc, dtype=torch.float64)
+
+    def run_cpu():
+        for x in (Qc, Kc, Vc):
+            x.grad = None
+        orc.causal_linear_ref(Qc, Kc, Vc).backward(goc)
+
+    sec = _cpu_median(run_cpu)
+    return {"metric": "causal linear attention fwd+bwd tokens/sec", "value": round(B * T / (ms / 1e3), 1),
+            "unit": "tokens/s", "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "f32",
+            "data": "synthetic", "vs_baseline": None,
+            "config": {"workload": "linear", "B": B, "H": H, "T": T, "D": D},
+            "layer_roofline": {"bound": "hbm" if nbytes / HBM_PEAK >= flops / FP32_PEAK else "fp32 compute",
+                               "t_bound_ms": round(t_bound * 1e3, 4), "frac": round(t_bound * 1e3 / ms, 4)},
+            "kernels_ms_per_step": split,
+            "cpu_baseline": {"value": round(B * Tc / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+                             "sample": f"fp64 cumulative-sum restatement fwd+bwd at T = 2^12 (same B, H, D), median of 3",
                              "seconds_per_step": round(sec, 3)}}
 
 

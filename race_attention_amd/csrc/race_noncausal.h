@@ -13,6 +13,7 @@ struct NcParams {
     const float *totB, *totA, *totGE;
     int T, S, D, NB, S_pad, DPw;
     float eps;
+    int tpw;  // token tiles per workgroup (set by launch_noncausal)
 };
 
 // bwd = 0: out ; bwd = 1: gpQ, gpK, gV. DP in {32, 64, 128, 256} (D padded).

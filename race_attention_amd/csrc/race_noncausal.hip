@@ -9,6 +9,9 @@
 // (slot NB of the scanned workspace holds the whole-sequence sum); the kernels here are
 // the per-token readout and backward, fp32 FMA on LDS tiles of NC_TT tokens x NC_SC
 // buckets.
+#include <algorithm>
+
+#include "race_device.h"
 #include "race_launch.h"
 #include "race_noncausal.h"
 
@@ -18,9 +21,9 @@ namespace {
 
 constexpr int NC_TT = 32, NC_SC = 32, NC_NTH = 256;
 
-// E (and optionally gB, gA) rows for buckets s0 .. s0+NC_SC of stream z into LDS
-template <int DP>
-__device__ void load_bucket_rows(const NcParams &P, int z, int s0, float (*sE)[DP], float (*sGB)[DP], float *sGA,
+// E (and optionally gB, gA) rows for buckets s0 .. s0+NC_SC of stream z into LDS rows of LD floats
+template <int DP, int LD>
+__device__ void load_bucket_rows(const NcParams &P, int z, int s0, float (*sE)[LD], float (*sGB)[LD], float *sGA,
                                  int tid)
 {
     const int64_t slot = (int64_t)z * (P.NB + 1) + P.NB;
@@ -59,120 +62,172 @@ __device__ void load_bucket_rows(const NcParams &P, int z, int s0, float (*sE)[D
 template <int DP>
 __global__ __launch_bounds__(NC_NTH) void race_nc_readout(const NcParams P)
 {
-    __shared__ float sE[NC_SC][DP];
+    __shared__ float sE[NC_SC][DP];  // read along d: unpadded rows
     __shared__ float sP[NC_TT][NC_SC + 1];
-    const int tid = threadIdx.x, z = blockIdx.y, t0 = blockIdx.x * NC_TT;
-    const int nv = min(NC_TT, P.T - t0);
-    constexpr int NO = NC_TT * DP / NC_NTH;  // outputs per thread: (t, d) = i / DP, i % DP
-    float acc[NO];
+    const int tid = threadIdx.x, z = blockIdx.y;
+    const int ntt = (P.T + NC_TT - 1) / NC_TT, tt1 = min(ntt, ((int)blockIdx.x + 1) * P.tpw);
+    const bool one_chunk = P.S <= NC_SC;  // E rows stay in LDS for every tile of this workgroup
+    if (one_chunk)
+        load_bucket_rows<DP, DP>(P, z, 0, sE, nullptr, nullptr, tid);
+    for (int tt = blockIdx.x * P.tpw; tt < tt1; ++tt) {
+        const int t0 = tt * NC_TT;
+        const int nv = min(NC_TT, P.T - t0);
+        constexpr int NO = NC_TT * DP / NC_NTH;  // outputs per thread: (t, d) = i / DP, i % DP
+        float acc[NO];
 #pragma unroll
-    for (int o = 0; o < NO; ++o)
-        acc[o] = 0.0f;
-    const float *pQ = P.pQ + ((int64_t)z * P.T + t0) * P.S;
-    for (int s0 = 0; s0 < P.S; s0 += NC_SC) {
-        __syncthreads();
-        load_bucket_rows<DP>(P, z, s0, sE, nullptr, nullptr, tid);
-        for (int i = tid; i < NC_TT * NC_SC; i += NC_NTH) {
-            const int r = i / NC_SC, c = i % NC_SC;
-            sP[r][c] = (r < nv && s0 + c < P.S) ? pQ[(int64_t)r * P.S + s0 + c] : 0.0f;
+        for (int o = 0; o < NO; ++o)
+            acc[o] = 0.0f;
+        const float *pQ = P.pQ + ((int64_t)z * P.T + t0) * P.S;
+        for (int s0 = 0; s0 < P.S; s0 += NC_SC) {
+            __syncthreads();
+            if (!one_chunk)
+                load_bucket_rows<DP, DP>(P, z, s0, sE, nullptr, nullptr, tid);
+            for (int i = tid; i < NC_TT * NC_SC; i += NC_NTH) {
+                const int r = i / NC_SC, c = i % NC_SC;
+                sP[r][c] = (r < nv && s0 + c < P.S) ? pQ[(int64_t)r * P.S + s0 + c] : 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int o = 0; o < NO; ++o) {
+                const int i = tid + o * NC_NTH, r = i / DP, d = i % DP;
+                float a = acc[o];
+#pragma unroll 8
+                for (int c = 0; c < NC_SC; ++c)
+                    a += sP[r][c] * sE[c][d];
+                acc[o] = a;
+            }
         }
-        __syncthreads();
+        float *out = P.out + ((int64_t)z * P.T + t0) * P.D;
 #pragma unroll
         for (int o = 0; o < NO; ++o) {
             const int i = tid + o * NC_NTH, r = i / DP, d = i % DP;
-            float a = acc[o];
-#pragma unroll 8
-            for (int c = 0; c < NC_SC; ++c)
-                a += sP[r][c] * sE[c][d];
-            acc[o] = a;
+            if (r < nv && d < P.D)
+                out[(int64_t)r * P.D + d] = acc[o];
         }
-    }
-    float *out = P.out + ((int64_t)z * P.T + t0) * P.D;
-#pragma unroll
-    for (int o = 0; o < NO; ++o) {
-        const int i = tid + o * NC_NTH, r = i / DP, d = i % DP;
-        if (r < nv && d < P.D)
-            out[(int64_t)r * P.D + d] = acc[o];
     }
 }
 
 template <int DP>
 __global__ __launch_bounds__(NC_NTH) void race_nc_backward(const NcParams P)
 {
-    __shared__ float sE[NC_SC][DP];
-    __shared__ float sGB[NC_SC][DP];
+    // rows at a pitch of 4 x odd words: 16-byte reads with the bucket (E, gB) or token (go, v)
+    // index across 16 lanes cover the 64 banks once
+    constexpr int LDD = DP + 4, LDC = NC_SC + 4;
+    __shared__ __align__(16) float sE[NC_SC][LDD];
+    __shared__ __align__(16) float sGB[NC_SC][LDD];
     __shared__ float sGA[NC_SC];
-    __shared__ float sG[NC_TT][DP + 1];
-    __shared__ float sV[NC_TT][DP + 1];
-    __shared__ float sPK[NC_TT][NC_SC + 1];
-    const int tid = threadIdx.x, z = blockIdx.y, t0 = blockIdx.x * NC_TT;
-    const int nv = min(NC_TT, P.T - t0);
-    const float *go = P.gO + ((int64_t)z * P.T + t0) * P.D;
-    const float *v = P.V + ((int64_t)z * P.T + t0) * P.D;
-    for (int i = tid; i < NC_TT * DP; i += NC_NTH) {
-        const int r = i / DP, d = i % DP;
-        const bool ok = r < nv && d < P.D;
-        sG[r][d] = ok ? go[(int64_t)r * P.D + d] : 0.0f;
-        sV[r][d] = ok ? v[(int64_t)r * P.D + d] : 0.0f;
-    }
-    constexpr int NO = NC_TT * DP / NC_NTH;     // gv outputs per thread
-    constexpr int NS = NC_TT * NC_SC / NC_NTH;  // gpQ / gpK outputs per thread per chunk
-    float gv[NO];
-#pragma unroll
-    for (int o = 0; o < NO; ++o)
-        gv[o] = 0.0f;
-    const float *pK = P.pK + ((int64_t)z * P.T + t0) * P.S;
-    float *gpQ = P.gpQ + ((int64_t)z * P.T + t0) * P.S;
-    float *gpK = P.gpK + ((int64_t)z * P.T + t0) * P.S;
-    for (int s0 = 0; s0 < P.S; s0 += NC_SC) {
-        __syncthreads();
-        for (int i = tid; i < NC_TT * NC_SC; i += NC_NTH) {
-            const int r = i / NC_SC, c = i % NC_SC;
-            sPK[r][c] = (r < nv && s0 + c < P.S) ? pK[(int64_t)r * P.S + s0 + c] : 0.0f;
+    __shared__ __align__(16) float sG[NC_TT][LDD];
+    __shared__ __align__(16) float sV[NC_TT][LDD];
+    __shared__ __align__(16) float sPK[NC_TT][LDC];
+    const int tid = threadIdx.x, z = blockIdx.y;
+    const int ntt = (P.T + NC_TT - 1) / NC_TT, tt1 = min(ntt, ((int)blockIdx.x + 1) * P.tpw);
+    const bool one_chunk = P.S <= NC_SC;  // E, gB, gA rows stay in LDS for every tile
+    if (one_chunk)
+        load_bucket_rows<DP, LDD>(P, z, 0, sE, sGB, sGA, tid);
+    for (int tt = blockIdx.x * P.tpw; tt < tt1; ++tt) {
+        const int t0 = tt * NC_TT;
+        const int nv = min(NC_TT, P.T - t0);
+        const float *go = P.gO + ((int64_t)z * P.T + t0) * P.D;
+        const float *v = P.V + ((int64_t)z * P.T + t0) * P.D;
+        __syncthreads();  // the previous tile's readers of sG, sV and sPK are done
+        for (int i = tid; i < NC_TT * DP; i += NC_NTH) {
+            const int r = i / DP, d = i % DP;
+            const bool ok = r < nv && d < P.D;
+            sG[r][d] = ok ? go[(int64_t)r * P.D + d] : 0.0f;
+            sV[r][d] = ok ? v[(int64_t)r * P.D + d] : 0.0f;
         }
-        load_bucket_rows<DP>(P, z, s0, sE, sGB, sGA, tid);
-        __syncthreads();
+        constexpr int NO = NC_TT * DP / NC_NTH;     // gv outputs per thread
+        constexpr int NS = NC_TT * NC_SC / NC_NTH;  // gpQ / gpK outputs per thread per chunk
+        float gv[NO];
 #pragma unroll
-        for (int o = 0; o < NS; ++o) {
-            const int i = tid + o * NC_NTH, r = i / NC_SC, c = i % NC_SC;
-            float aq = 0.0f, ak = 0.0f;
-#pragma unroll 8
-            for (int d = 0; d < DP; ++d) {
-                aq += sG[r][d] * sE[c][d];
-                ak += sV[r][d] * sGB[c][d];
+        for (int o = 0; o < NO; ++o)
+            gv[o] = 0.0f;
+        const float *pK = P.pK + ((int64_t)z * P.T + t0) * P.S;
+        float *gpQ = P.gpQ + ((int64_t)z * P.T + t0) * P.S;
+        float *gpK = P.gpK + ((int64_t)z * P.T + t0) * P.S;
+        for (int s0 = 0; s0 < P.S; s0 += NC_SC) {
+            __syncthreads();
+            for (int i = tid; i < NC_TT * NC_SC; i += NC_NTH) {
+                const int r = i / NC_SC, c = i % NC_SC;
+                sPK[r][c] = (r < nv && s0 + c < P.S) ? pK[(int64_t)r * P.S + s0 + c] : 0.0f;
             }
-            if (r < nv && s0 + c < P.S) {
-                gpQ[(int64_t)r * P.S + s0 + c] = aq;
-                gpK[(int64_t)r * P.S + s0 + c] = ak + sGA[c];
+            if (!one_chunk)
+                load_bucket_rows<DP, LDD>(P, z, s0, sE, sGB, sGA, tid);
+            __syncthreads();
+            // gpQ[t][s] = go_t . E[s], gpK[t][s] = gA[s] + v_t . gB[s]: a thread owns RB token rows of
+            // one bucket column, all operands read as 16-byte runs along d
+            constexpr int RB = NS;  // rows per thread: NC_TT / RB row groups x NC_SC columns = NC_NTH
+            static_assert(NC_TT / RB * NC_SC == NC_NTH, "one (row group, bucket) item per thread");
+            {
+                const int rg = tid / NC_SC, c = tid % NC_SC;
+                float aq[RB] = {}, ak[RB] = {};
+#pragma unroll 2
+                for (int d = 0; d < DP; d += 4) {
+                    const f32x4 e = *reinterpret_cast<const f32x4 *>(&sE[c][d]);
+                    const f32x4 gb = *reinterpret_cast<const f32x4 *>(&sGB[c][d]);
+#pragma unroll
+                    for (int q = 0; q < RB; ++q) {
+                        const f32x4 g = *reinterpret_cast<const f32x4 *>(&sG[rg * RB + q][d]);
+                        const f32x4 vv = *reinterpret_cast<const f32x4 *>(&sV[rg * RB + q][d]);
+#pragma unroll
+                        for (int e4 = 0; e4 < 4; ++e4) {
+                            aq[q] += g[e4] * e[e4];
+                            ak[q] += vv[e4] * gb[e4];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < RB; ++q) {
+                    const int r = rg * RB + q;
+                    if (r < nv && s0 + c < P.S) {
+                        gpQ[(int64_t)r * P.S + s0 + c] = aq[q];
+                        gpK[(int64_t)r * P.S + s0 + c] = ak[q] + sGA[c];
+                    }
+                }
+            }
+            // gv[t][d] += sum_c pK[t][c] gB[c][d]: this thread's NO outputs share one column d, so each
+            // gB element is read once per bucket and pK as 16-byte runs over 4 buckets
+            {
+                const int d = tid % DP, r0 = tid / DP;
+#pragma unroll 2
+                for (int c = 0; c < NC_SC; c += 4) {
+                    float gb[4];
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4)
+                        gb[e4] = sGB[c + e4][d];
+#pragma unroll
+                    for (int o = 0; o < NO; ++o) {
+                        const f32x4 pk = *reinterpret_cast<const f32x4 *>(&sPK[r0 + o * (NC_NTH / DP)][c]);
+#pragma unroll
+                        for (int e4 = 0; e4 < 4; ++e4)
+                            gv[o] += pk[e4] * gb[e4];
+                    }
+                }
             }
         }
+        float *gV = P.gV + ((int64_t)z * P.T + t0) * P.D;
 #pragma unroll
         for (int o = 0; o < NO; ++o) {
-            const int i = tid + o * NC_NTH, r = i / DP, d = i % DP;
-            float a = gv[o];
-#pragma unroll 8
-            for (int c = 0; c < NC_SC; ++c)
-                a += sPK[r][c] * sGB[c][d];
-            gv[o] = a;
+            const int r = tid / DP + o * (NC_NTH / DP), d = tid % DP;
+            if (r < nv && d < P.D)
+                gV[(int64_t)r * P.D + d] = gv[o];
         }
-    }
-    float *gV = P.gV + ((int64_t)z * P.T + t0) * P.D;
-#pragma unroll
-    for (int o = 0; o < NO; ++o) {
-        const int i = tid + o * NC_NTH, r = i / DP, d = i % DP;
-        if (r < nv && d < P.D)
-            gV[(int64_t)r * P.D + d] = gv[o];
     }
 }
 
 template <int DP>
 hipError_t launch_nc_dp(int bwd, const NcParams &P, int N, hipStream_t s)
 {
-    const dim3 grid((unsigned)((P.T + NC_TT - 1) / NC_TT), (unsigned)N);
+    // a workgroup walks up to 16 consecutive tiles of one stream while the grid keeps about
+    // 2048 workgroups (8 per CU)
+    const int ntt = (P.T + NC_TT - 1) / NC_TT;
+    NcParams Q = P;
+    Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)ntt * N / 2048));
+    const dim3 grid((unsigned)((ntt + Q.tpw - 1) / Q.tpw), (unsigned)N);
     if (bwd)
-        hipLaunchKernelGGL(race_nc_backward<DP>, grid, dim3(NC_NTH), 0, s, P);
+        hipLaunchKernelGGL(race_nc_backward<DP>, grid, dim3(NC_NTH), 0, s, Q);
     else
-        hipLaunchKernelGGL(race_nc_readout<DP>, grid, dim3(NC_NTH), 0, s, P);
+        hipLaunchKernelGGL(race_nc_readout<DP>, grid, dim3(NC_NTH), 0, s, Q);
     return hipGetLastError();
 }
 

@@ -22,8 +22,11 @@ def _probs(N, T, S, D, seed):
     return pk, pq, v, go
 
 
+# the last two: enough 32-token tiles that each workgroup walks several (4 here, ragged last tile),
+# with every bucket in one chunk (S = 24) and over several chunks (S = 64)
 @pytest.mark.parametrize("N,T,S,D", [(1, 1, 8, 16), (2, 7, 24, 64), (3, 300, 128, 64), (1, 4096, 256, 128),
-                                     (2, 1000, 64, 100), (1, 513, 300, 256), (4, 2000, 16, 32)])
+                                     (2, 1000, 64, 100), (1, 513, 300, 256), (4, 2000, 16, 32),
+                                     (4, 70001, 24, 128), (4, 66017, 64, 32)])
 def test_noncausal_op(dev, N, T, S, D):
     from race_attention_amd.noncausal import RaceNonCausalFn
     print(f"nc op N={N} T={T} S={S} D={D}", flush=True)

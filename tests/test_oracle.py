@@ -69,7 +69,7 @@ def test_softhash_softmax_equals_sigmoid_product(L, Kb, scale):
 
 
 def test_softhash_zero_planes_uniform_and_k1():
-    X = torch.randn(1, 1, 5, 8, dtype=F64)
+    X = torch.randn(1, 1, 5, 8, generator=torch.Generator().manual_seed(71), dtype=F64)
     _, protos = orc.build_planes_protos(8, 3, 2)
     p = orc.soft_hash_probs(X, X, X, torch.zeros(8, 6), protos, 2, 3)[0]
     assert torch.all(p == 1.0 / 8)
@@ -77,7 +77,8 @@ def test_softhash_zero_planes_uniform_and_k1():
     planes_T, protos1 = orc.build_planes_protos(8, 1, 1, seed=1)
     p1 = orc.soft_hash_probs(X, X, X, planes_T, protos1, 1, 1)[0]
     u = torch.tanh(X.view(5, 8) @ planes_T.to(F64)) / math.sqrt(8)
-    assert torch.allclose(p1[0, :, 0], torch.sigmoid(-2 * u[:, 0]), atol=1e-15)
+    # the two-way softmax and the sigmoid agree to a few ulp of values <= 1
+    assert torch.allclose(p1[0, :, 0], torch.sigmoid(-2 * u[:, 0]), atol=1e-14)
     assert torch.allclose(p1[0, :, 1], torch.sigmoid(2 * u[:, 0]), atol=1e-15)
 
 
@@ -114,7 +115,7 @@ def test_prefix_ref_zero_planes_known_answer():
     L, Kb, eps = 4, 3, 1e-3
     R = 1 << Kb
     B, H, T, D = 1, 2, 11, 6
-    V = torch.randn(B, H, T, D, dtype=F64)
+    V = torch.randn(B, H, T, D, generator=torch.Generator().manual_seed(72), dtype=F64)
     _, protos = orc.build_planes_protos(D, Kb, L)
     out = orc.race_module_ref(V, V, V, torch.zeros(D, L * Kb), protos, L, Kb, eps=eps)
     t = torch.arange(T, dtype=F64).view(1, 1, T, 1)
