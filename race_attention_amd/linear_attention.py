@@ -19,6 +19,17 @@ def _flat(x):
     return x.detach().float().contiguous().view(N * H, L, F)
 
 
+def _dest(t, inputs):
+    """The [N*H, L, F] fp32 buffer a kernel writes for output `t`: `t` itself when it is contiguous
+    fp32 and shares no storage with an input (the kernels read their inputs in several passes),
+    otherwise a temporary that the caller copies into `t`."""
+    N, H, L, F = t.shape
+    st = t.untyped_storage().data_ptr()
+    if t.dtype == torch.float32 and t.is_contiguous() and all(st != x.untyped_storage().data_ptr() for x in inputs):
+        return t.view(N * H, L, F), False
+    return torch.empty(N * H, L, F, dtype=torch.float32, device=t.device), True
+
+
 def causal_dot_product(queries, keys, values, product):
     """Writes out = causal linear attention into `product` [N,H,L,M] (as the reference)."""
     _lib.require_device(queries, keys, values, product)
@@ -27,12 +38,13 @@ def causal_dot_product(queries, keys, values, product):
     if keys.shape != queries.shape or values.shape[:3] != queries.shape[:3] or product.shape != values.shape:
         raise ValueError("expected Q, K [N,H,L,E], V and product [N,H,L,M]")
     Q, K, V = _flat(queries), _flat(keys), _flat(values)
-    out = torch.empty(N * H, L, M, dtype=torch.float32, device=Q.device)
+    out, copy_out = _dest(product, (queries, keys, values, Q, K, V))
     lib = _lib.lib()
     ws = _lib.workspace(lib.race_op_workspace_bytes(N * H, L, E, M, 0, 0), Q.device)
     _lib.check(lib.race_causal_dot_product(_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(out), N * H, L, E, M, 0,
                                            _lib.ptr(ws), ws.numel(), _lib.stream_of(Q)), "race_causal_dot_product")
-    product.copy_(out.view(N, H, L, M))
+    if copy_out:
+        product.copy_(out.view(N, H, L, M))
     return product
 
 
@@ -42,16 +54,16 @@ def causal_dot_backward(queries, keys, values, grad_out, grad_queries, grad_keys
     N, H, L, E = queries.shape
     M = values.shape[3]
     Q, K, V, G = _flat(queries), _flat(keys), _flat(values), _flat(grad_out)
-    gQ, gK = torch.empty_like(Q), torch.empty_like(K)
-    gV = torch.empty_like(V)
+    ins = (queries, keys, values, grad_out, Q, K, V, G)
+    (gQ, cq), (gK, ck), (gV, cv) = _dest(grad_queries, ins), _dest(grad_keys, ins), _dest(grad_values, ins)
     lib = _lib.lib()
     ws = _lib.workspace(lib.race_op_workspace_bytes(N * H, L, E, M, 0, 1), Q.device)
     _lib.check(lib.race_causal_dot_backward(_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(G), _lib.ptr(gQ),
                                             _lib.ptr(gK), _lib.ptr(gV), N * H, L, E, M, 0, _lib.ptr(ws), ws.numel(),
                                             _lib.stream_of(Q)), "race_causal_dot_backward")
-    grad_queries.copy_(gQ.view(N, H, L, E))
-    grad_keys.copy_(gK.view(N, H, L, E))
-    grad_values.copy_(gV.view(N, H, L, M))
+    for dst, buf, cp in ((grad_queries, gQ, cq), (grad_keys, gK, ck), (grad_values, gV, cv)):
+        if cp:
+            dst.copy_(buf.view(dst.shape))
 
 
 class CausalLinearFn(Function):

@@ -91,7 +91,9 @@ class SoftHashTempFn(Function):
         B, H, T, D = Xc.shape
         Mp = M if unshared else 1
         g = gprobs.float().contiguous().view(Mp, B * H, T, -1)
-        dX = torch.empty(B, H, T, D, dtype=Xc.dtype, device=Xc.device)
+        # in X's own layout (a strided view of the caller's tensor): autograd hands it to the leaf
+        # without a layout copy
+        dX = torch.empty_like(Xc)
         xv, _ = _lib.view4(Xc)
         dv, _ = _lib.view4(dX)
         sh = _hash_shape(Xc, L, Kbits, Mp, unshared, s)

@@ -30,3 +30,29 @@ def test_causal_linear(dev, N, H, L, E, M):
     check("linear gQ", q2.grad, q1.grad, 2e-3)
     check("linear gK", k2.grad, k1.grad, 2e-3)
     check("linear gV", v2.grad, v1.grad, 2e-3)
+
+
+def test_causal_linear_destinations(dev):
+    """Outputs written in place when contiguous fp32, through a temporary otherwise: a strided
+    destination, and a destination that is the value tensor itself (the kernels read their
+    inputs in several passes, so an aliased output must not be written directly)."""
+    from race_attention_amd.linear_attention import causal_dot_backward, causal_dot_product
+    N, H, L, E = 1, 2, 700, 32
+    g = torch.Generator().manual_seed(3)
+    Q, K, V, G = (torch.randn(N, H, L, E, generator=g) for _ in range(4))
+    q1, k1, v1 = (x.double().requires_grad_(True) for x in (Q, K, V))
+    ref = orc.causal_linear_ref(q1, k1, v1)
+    ref.backward(G.double())
+    Qd, Kd, Vd, Gd = (x.to(dev) for x in (Q, K, V, G))
+    strided = torch.zeros(N, L, H, E, device=dev).transpose(1, 2)  # [N,H,L,E] view, not contiguous
+    causal_dot_product(Qd, Kd, Vd, strided)
+    check("strided product", strided, ref, 1e-3)
+    Va = Vd.clone()
+    causal_dot_product(Qd, Kd, Va, Va)  # product aliases the values
+    check("aliased product", Va, ref, 1e-3)
+    gq, gk = torch.empty_like(Qd), torch.zeros(N, L, H, E, device=dev).transpose(1, 2)
+    Ga = Gd.clone()
+    causal_dot_backward(Qd, Kd, Vd, Ga, gq, gk, Ga)  # grad_values aliases grad_out
+    check("gQ", gq, q1.grad, 2e-3)
+    check("gK (strided)", gk, k1.grad, 2e-3)
+    check("gV (aliased)", Ga, v1.grad, 2e-3)
