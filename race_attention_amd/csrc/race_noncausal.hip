@@ -63,7 +63,7 @@ template <int DP>
 __global__ __launch_bounds__(NC_NTH) void race_nc_readout(const NcParams P)
 {
     __shared__ float sE[NC_SC][DP];  // read along d: unpadded rows
-    __shared__ float sP[NC_TT][NC_SC + 1];
+    __shared__ __align__(16) float sP[NC_TT][NC_SC + 4];
     const int tid = threadIdx.x, z = blockIdx.y;
     const int ntt = (P.T + NC_TT - 1) / NC_TT, tt1 = min(ntt, ((int)blockIdx.x + 1) * P.tpw);
     const bool one_chunk = P.S <= NC_SC;  // E rows stay in LDS for every tile of this workgroup
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(NC_NTH) void race_nc_readout(const NcParams P)
     for (int tt = blockIdx.x * P.tpw; tt < tt1; ++tt) {
         const int t0 = tt * NC_TT;
         const int nv = min(NC_TT, P.T - t0);
-        constexpr int NO = NC_TT * DP / NC_NTH;  // outputs per thread: (t, d) = i / DP, i % DP
+        constexpr int NO = NC_TT * DP / NC_NTH;  // outputs per thread: rows tid / DP + o * (NC_NTH / DP), column tid % DP
         float acc[NO];
 #pragma unroll
         for (int o = 0; o < NO; ++o)
@@ -87,20 +87,28 @@ __global__ __launch_bounds__(NC_NTH) void race_nc_readout(const NcParams P)
                 sP[r][c] = (r < nv && s0 + c < P.S) ? pQ[(int64_t)r * P.S + s0 + c] : 0.0f;
             }
             __syncthreads();
+            // this thread's NO outputs share one column d: each E element is read once per bucket,
+            // pQ as 16-byte runs over 4 buckets
+            const int d = tid % DP, r0 = tid / DP;
+#pragma unroll 2
+            for (int c = 0; c < NC_SC; c += 4) {
+                float e[4];
 #pragma unroll
-            for (int o = 0; o < NO; ++o) {
-                const int i = tid + o * NC_NTH, r = i / DP, d = i % DP;
-                float a = acc[o];
-#pragma unroll 8
-                for (int c = 0; c < NC_SC; ++c)
-                    a += sP[r][c] * sE[c][d];
-                acc[o] = a;
+                for (int e4 = 0; e4 < 4; ++e4)
+                    e[e4] = sE[c + e4][d];
+#pragma unroll
+                for (int o = 0; o < NO; ++o) {
+                    const f32x4 pq = *reinterpret_cast<const f32x4 *>(&sP[r0 + o * (NC_NTH / DP)][c]);
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4)
+                        acc[o] += pq[e4] * e[e4];
+                }
             }
         }
         float *out = P.out + ((int64_t)z * P.T + t0) * P.D;
 #pragma unroll
         for (int o = 0; o < NO; ++o) {
-            const int i = tid + o * NC_NTH, r = i / DP, d = i % DP;
+            const int r = tid / DP + o * (NC_NTH / DP), d = tid % DP;
             if (r < nv && d < P.D)
                 out[(int64_t)r * P.D + d] = acc[o];
         }
