@@ -114,8 +114,10 @@ def test_fused_strided_views(dev):
 
 def test_soft_hash_probs_fp32(dev):
     from race_attention_amd import build_planes_protos, soft_hash_probs
+    # D = 130: rows not a multiple of 4 (element-wise x loads, zero-padded LDS rows) and the backward
+    # compiled for D <= 256; D = 256: the largest head dim
     for (L, Kb, D, M, share) in [(2, 2, 16, 1, True), (8, 4, 64, 1, True), (3, 3, 128, 2, True),
-                                 (4, 2, 32, 3, False)]:
+                                 (4, 2, 32, 3, False), (2, 3, 130, 1, True), (4, 4, 256, 2, False)]:
         planes_T, protos_T = build_planes_protos(D, Kb, L, M, device=dev, share_planes=share, seed=2)
         g = torch.Generator().manual_seed(D)
         Q, K, V = (torch.randn(2, 3, 37, D, generator=g) for _ in range(3))
