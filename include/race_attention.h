@@ -93,6 +93,20 @@ int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, in
 int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK,
                 float *gpQ, float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps,
                 int64_t block, void *workspace, size_t workspace_bytes, race_stream stream);
+/* race_op_fwd that also leaves its scanned forward block states in `state`
+ * (race_op_state_bytes bytes, 256-byte aligned), and race_op_bwd that reads them from there
+ * instead of recomputing them (same pK, V, shape and block as the forward; the backward only
+ * reads the state, so it serves any number of backward calls). No counterpart in the reference,
+ * whose backward (kernels/gpu/backward_kernels.cu:174-215) recomputes the forward block states:
+ * for autograd callers that keep the forward's state until the backward. */
+size_t race_op_state_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block);
+int race_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N,
+                     int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
+                     size_t workspace_bytes, float *state, race_stream stream);
+int race_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK,
+                     float *gpQ, float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps,
+                     int64_t block, void *workspace, size_t workspace_bytes, const float *state,
+                     race_stream stream);
 
 /* ---------------------------------------------------------------- causal linear attention */
 /* Katharopoulos causal linear attention, the reference's comparison kernel

@@ -66,6 +66,11 @@ SIGNATURES = {
                                    ctypes.c_size_t, _vp]),
     "race_op_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float,
                                    _i64, _vp, ctypes.c_size_t, _vp]),
+    "race_op_state_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
+    "race_op_fwd_keep": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
+                                        ctypes.c_size_t, _vp, _vp]),
+    "race_op_bwd_kept": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float,
+                                        _i64, _vp, ctypes.c_size_t, _vp, _vp]),
     "race_qkv_state_bytes": (ctypes.c_size_t, [ctypes.POINTER(QKVShape)]),
     "race_qkv_scratch_bytes": (ctypes.c_size_t, [ctypes.POINTER(QKVShape), ctypes.c_int]),
     "race_qkv_fwd": (ctypes.c_int, [ctypes.POINTER(QKVShape), Tensor4, Tensor4, Tensor4, _vp, Tensor4,

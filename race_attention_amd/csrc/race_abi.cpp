@@ -418,9 +418,16 @@ static int op_check(const float *pK, const float *pQ, const float *V, float eps,
     return RACE_OK;
 }
 
+// forward block states [wsB | wsA] inside a caller's state buffer (race_op_state_bytes)
+static void state_views(const Geo &g, const float *state, float *&wsB, float *&wsA)
+{
+    wsB = const_cast<float *>(state);
+    wsA = wsB + align256(g.state_elems_B * 4) / 4;
+}
+
 static int op_fwd_impl(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
                        int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
-                       race_stream stream, int linear, const char *who)
+                       race_stream stream, int linear, const char *who, float *state = nullptr)
 {
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
@@ -435,6 +442,8 @@ static int op_fwd_impl(const float *pK, const float *pQ, const float *V, float *
     P.V = V;
     P.wsB = cv.take(g.state_elems_B);
     P.wsA = cv.take(g.state_elems_A);
+    if (state)
+        state_views(g, state, P.wsB, P.wsA);
     float *part = g.n_st > 1 ? cv.take((size_t)g.n_st * N * T * D) : nullptr;
     P.out = part ? OutView{part, T * D, 0, D, N * T * D, 1} : OutView{out, T * D, 0, D, 0, 1};
     const hipStream_t s = hs(stream);
@@ -457,7 +466,8 @@ int race_op_fwd(const float *pK, const float *pQ, const float *V, float *out, in
 
 static int op_bwd_impl(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
                        float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
-                       void *workspace, size_t workspace_bytes, race_stream stream, int linear, const char *who)
+                       void *workspace, size_t workspace_bytes, race_stream stream, int linear, const char *who,
+                       const float *state = nullptr)
 {
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
@@ -480,9 +490,13 @@ static int op_bwd_impl(const float *pK, const float *pQ, const float *V, const f
     float *part = g.n_st > 1 ? cv.take((size_t)g.n_st * N * T * D) : nullptr;
     P.dv = part ? OutView{part, T * D, 0, D, N * T * D, 1} : OutView{gV, T * D, 0, D, 0, 1};
     const hipStream_t s = hs(stream);
-    // forward block states (the backward recomputes them; nothing is saved between calls)
-    RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    if (state) {  // forward block states kept by race_op_fwd_keep (only read from here on)
+        state_views(g, state, P.wsB, P.wsA);
+    } else {  // recomputed: nothing is saved between calls
+        RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
+        RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s),
+                           "block scan"));
+    }
     RACE_TRY(run_scan_op(K_BWD_TOTALS, g, P, s));
     RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
     RACE_TRY(run_scan_op(K_BWD_MAIN, g, P, s));
@@ -490,6 +504,34 @@ static int op_bwd_impl(const float *pK, const float *pQ, const float *V, const f
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{gV, T * D, 0, D, 0, 1},
                                                   (int)N, 1, (int)T, (int)D, s), "reduce partials"));
     return RACE_OK;
+}
+
+size_t race_op_state_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block)
+{
+    Geo g;
+    if (op_geometry(N, T, S, D, block, g) != RACE_OK)
+        return 0;
+    return align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+}
+
+int race_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
+                     int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
+                     float *state, race_stream stream)
+{
+    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
+        return fail(RACE_ERR_INVALID, "race_op_fwd_keep: state must be a 256-byte aligned buffer");
+    return op_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, 0,
+                       "race_op_fwd_keep", state);
+}
+
+int race_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                     float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                     void *workspace, size_t workspace_bytes, const float *state, race_stream stream)
+{
+    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
+        return fail(RACE_ERR_INVALID, "race_op_bwd_kept: state must be a 256-byte aligned buffer");
+    return op_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream, 0,
+                       "race_op_bwd_kept", state);
 }
 
 int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,

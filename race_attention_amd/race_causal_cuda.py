@@ -46,9 +46,18 @@ def _op_inputs(probsK, probsQ, V2):
     return probsK.contiguous().float(), probsQ.contiguous().float(), V2.contiguous().float()
 
 
-def race_fused_fwd(probsK, probsQ, V2, eps, chunk=0):
+def op_state(probsK, V2, chunk=0):
+    """A buffer for the forward block states that race_fused_fwd(..., state=) keeps for
+    race_backward(..., state=)."""
+    N, T, S = probsK.shape
+    n = _lib.lib().race_op_state_bytes(N, T, S, V2.shape[2], max(int(chunk), 0))
+    return torch.empty((n + 3) // 4, dtype=torch.float32, device=probsK.device)
+
+
+def race_fused_fwd(probsK, probsQ, V2, eps, chunk=0, state=None):
     """out[N,T,D] fp32 = causal RACE(probsK, probsQ, V2) (forward_kernel.cu:110-137).
-    `chunk` is the tokens per workgroup block (<= 0: automatic)."""
+    `chunk` is the tokens per workgroup block (<= 0: automatic). With `state` (op_state), the
+    scanned forward block states are left there for race_backward."""
     pK, pQ, V = _op_inputs(probsK, probsQ, V2)
     N, T, S = pK.shape
     D = V.shape[2]
@@ -56,13 +65,19 @@ def race_fused_fwd(probsK, probsQ, V2, eps, chunk=0):
     L = _lib.lib()
     ws = _lib.workspace(L.race_op_workspace_bytes(N, T, S, D, block, 0), pK.device)
     out = torch.empty(N, T, D, dtype=torch.float32, device=pK.device)
-    _lib.check(L.race_op_fwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(out), N, T, S, D, float(eps),
-                             block, _lib.ptr(ws), ws.numel(), _lib.stream_of(pK)), "race_op_fwd")
+    args = (_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(out), N, T, S, D, float(eps), block, _lib.ptr(ws),
+            ws.numel())
+    if state is None:
+        _lib.check(L.race_op_fwd(*args, _lib.stream_of(pK)), "race_op_fwd")
+    else:
+        _lib.check(L.race_op_fwd_keep(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_op_fwd_keep")
     return out
 
 
-def race_backward(probsK, probsQ, V2, grad_out, eps, chunk=0):
-    """[gradProbsK, gradProbsQ, gradV] (backward_kernels.cu:174-215), exact."""
+def race_backward(probsK, probsQ, V2, grad_out, eps, chunk=0, state=None):
+    """[gradProbsK, gradProbsQ, gradV] (backward_kernels.cu:174-215), exact. With `state` from
+    race_fused_fwd(..., state=) on the same inputs and chunk, the forward block states are read
+    from it instead of recomputed."""
     pK, pQ, V = _op_inputs(probsK, probsQ, V2)
     _lib.require_device(grad_out)
     gO = grad_out.contiguous().float()
@@ -74,9 +89,12 @@ def race_backward(probsK, probsQ, V2, grad_out, eps, chunk=0):
     gpk = torch.empty_like(pK)
     gpq = torch.empty_like(pQ)
     gv = torch.empty_like(V)
-    _lib.check(L.race_op_bwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(gO), _lib.ptr(gpk), _lib.ptr(gpq),
-                             _lib.ptr(gv), N, T, S, D, float(eps), block, _lib.ptr(ws), ws.numel(),
-                             _lib.stream_of(pK)), "race_op_bwd")
+    args = (_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(gO), _lib.ptr(gpk), _lib.ptr(gpq), _lib.ptr(gv), N, T,
+            S, D, float(eps), block, _lib.ptr(ws), ws.numel())
+    if state is None:
+        _lib.check(L.race_op_bwd(*args, _lib.stream_of(pK)), "race_op_bwd")
+    else:
+        _lib.check(L.race_op_bwd_kept(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_op_bwd_kept")
     return [gpk, gpq, gv]
 
 
@@ -86,15 +104,17 @@ class RaceCausalFn(Function):
     @staticmethod
     def forward(ctx, probsK, probsQ, V2, eps):
         pK, pQ, V = _op_inputs(probsK, probsQ, V2)
-        out = race_fused_fwd(pK, pQ, V, eps, 0)
-        ctx.save_for_backward(pK, pQ, V)
+        # the forward block states stay in `state` for the backward (not recomputed there)
+        state = op_state(pK, V)
+        out = race_fused_fwd(pK, pQ, V, eps, 0, state=state)
+        ctx.save_for_backward(pK, pQ, V, state)
         ctx.eps = float(eps)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        pK, pQ, V = ctx.saved_tensors
-        gpk, gpq, gv = race_backward(pK, pQ, V, grad_out, ctx.eps, 0)
+        pK, pQ, V, state = ctx.saved_tensors
+        gpk, gpq, gv = race_backward(pK, pQ, V, grad_out, ctx.eps, 0, state=state)
         return gpk, gpq, gv, None
 
 

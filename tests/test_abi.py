@@ -88,3 +88,15 @@ def test_cpu_tensors_rejected_without_fallback():
     x = torch.rand(1, 8, 4)
     with pytest.raises(RuntimeError, match="GPU"):
         RaceCausalFn.apply(x, x, torch.rand(1, 8, 16), 1e-6)
+
+
+def test_kept_state_must_be_aligned():
+    lib = _lib.load_library()
+    assert lib.race_op_state_bytes(2, 100, 24, 64, 0) > 0
+    assert lib.race_op_state_bytes(0, 100, 24, 64, 0) == 0
+    rc = lib.race_op_fwd_keep(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              2, 100, 24, 64, 1e-6, 0, ctypes.c_void_p(16), 1 << 30, ctypes.c_void_p(256 + 4), None)
+    assert rc == 1 and "256-byte aligned" in lib.race_last_error().decode()
+    rc = lib.race_op_bwd_kept(*(ctypes.c_void_p(16),) * 7, 2, 100, 24, 64, 1e-6, 0, ctypes.c_void_p(16), 1 << 30,
+                              None, None)
+    assert rc == 1 and "256-byte aligned" in lib.race_last_error().decode()

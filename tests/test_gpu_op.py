@@ -71,3 +71,19 @@ def test_s256_tiled(dev):
 def test_many_blocks(dev):
     """More blocks than one pass of the block-state scan covers (625 and 834 blocks, ragged)."""
     run_case(dev, 1, 40000, 4, 4, 64, seed=40000, grad_tol=5e-3, blocks=(0, 48))
+
+
+def test_backward_from_kept_state(dev):
+    """race_backward reading the forward's kept block states (RaceCausalFn's path) is bitwise the
+    one that recomputes them, and the state is only read: a second backward on it is equal."""
+    from race_attention_amd.race_causal_cuda import op_state, race_backward, race_fused_fwd
+    pk, pq, v, go = make_probs(2, 3000, 8, 16, 64, seed=21)  # S = 128: two bucket tiles
+    pkc, pqc, vc, goc = (x.float().to(dev) for x in (pk, pq, v, go))
+    state = op_state(pkc, vc)
+    out_kept = race_fused_fwd(pkc, pqc, vc, EPS, 0, state=state)
+    assert torch.equal(out_kept, race_fused_fwd(pkc, pqc, vc, EPS, 0))
+    ref = race_backward(pkc, pqc, vc, goc, EPS, 0)
+    for rep in range(2):
+        got = race_backward(pkc, pqc, vc, goc, EPS, 0, state=state)
+        for name, a, b in zip(("gpK", "gpQ", "gV"), got, ref):
+            assert torch.equal(a, b), f"call {rep}: {name} from the kept state differs"
