@@ -137,6 +137,18 @@ int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float
                    float *gpK, float *gpQ, float *gV, int64_t N, int64_t T, int64_t S,
                    int64_t D, float eps, int64_t block, void *workspace,
                    size_t workspace_bytes, race_stream stream);
+/* The same pair keeping the forward's whole-sequence totals (sum pK, sum pK v) in `state`
+ * (race_op_state_bytes bytes, 256-byte aligned) for a backward that reads them instead of
+ * recomputing them; bitwise the same results. No counterpart in the reference, whose
+ * BatchedACE backward (torch autograd, scaling/benchmark_time.py:139-160) keeps the totals as
+ * saved tensors: for autograd callers that keep the state until the backward. */
+int race_nc_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N,
+                        int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
+                        size_t workspace_bytes, float *state, race_stream stream);
+int race_nc_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO,
+                        float *gpK, float *gpQ, float *gV, int64_t N, int64_t T, int64_t S,
+                        int64_t D, float eps, int64_t block, void *workspace,
+                        size_t workspace_bytes, const float *state, race_stream stream);
 
 /* ---------------------------------------------------------------- fused layer */
 typedef struct {

@@ -600,8 +600,9 @@ static NcParams nc_params(const Geo &g, int64_t T, int64_t S, int64_t D, float e
     return Q;
 }
 
-int race_nc_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T, int64_t S,
-                   int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes, race_stream stream)
+static int nc_fwd_impl(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
+                       int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
+                       race_stream stream, float *state)
 {
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
@@ -610,6 +611,8 @@ int race_nc_op_fwd(const float *pK, const float *pQ, const float *V, float *out,
         return fail(RACE_ERR_INVALID, "race_nc_op_fwd: null out");
     Carver cv(workspace, workspace_bytes);
     float *wsB = cv.take(g.state_elems_B), *wsA = cv.take(g.state_elems_A);
+    if (state)  // the totals are kept for the backward
+        state_views(g, state, wsB, wsA);
     const hipStream_t s = hs(stream);
     RACE_TRY(nc_totals(g, op_params(g, T, S, D, eps), pK, V, wsB, wsA, s));
     NcParams Q = nc_params(g, T, S, D, eps);
@@ -621,9 +624,9 @@ int race_nc_op_fwd(const float *pK, const float *pQ, const float *V, float *out,
     return hip_check(launch_noncausal(0, g.DP, Q, (int)N, s), "race_nc_op_fwd readout");
 }
 
-int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
-                   float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
-                   void *workspace, size_t workspace_bytes, race_stream stream)
+static int nc_bwd_impl(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                       float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                       void *workspace, size_t workspace_bytes, race_stream stream, const float *state)
 {
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
@@ -635,7 +638,10 @@ int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float
     float *ws2B = cv.take(g.state_elems_B), *ws2A = cv.take(g.state_elems_A);
     const hipStream_t s = hs(stream);
     const ScanParams P = op_params(g, T, S, D, eps);
-    RACE_TRY(nc_totals(g, P, pK, V, wsB, wsA, s));
+    if (state)  // the forward's totals, kept by race_nc_op_fwd_keep
+        state_views(g, state, wsB, wsA);
+    else
+        RACE_TRY(nc_totals(g, P, pK, V, wsB, wsA, s));
     RACE_TRY(nc_totals(g, P, pQ, gO, ws2B, ws2A, s));
     NcParams Q = nc_params(g, T, S, D, eps);
     Q.pK = pK;
@@ -649,6 +655,39 @@ int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float
     Q.totGE = ws2B;
     ProfScope ps(RACE_PROF_NC_BWD, s);
     return hip_check(launch_noncausal(1, g.DP, Q, (int)N, s), "race_nc_op_bwd backward");
+}
+
+int race_nc_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T, int64_t S,
+                   int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes, race_stream stream)
+{
+    return nc_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, nullptr);
+}
+
+int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                   float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                   void *workspace, size_t workspace_bytes, race_stream stream)
+{
+    return nc_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream,
+                       nullptr);
+}
+
+int race_nc_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
+                        int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
+                        float *state, race_stream stream)
+{
+    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
+        return fail(RACE_ERR_INVALID, "race_nc_op_fwd_keep: state must be a 256-byte aligned buffer");
+    return nc_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, state);
+}
+
+int race_nc_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
+                        float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                        void *workspace, size_t workspace_bytes, const float *state, race_stream stream)
+{
+    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
+        return fail(RACE_ERR_INVALID, "race_nc_op_bwd_kept: state must be a 256-byte aligned buffer");
+    return nc_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream,
+                       state);
 }
 
 // ============================================================================ fused layer

@@ -18,23 +18,29 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import _lib
-from .race_causal_cuda import _op_inputs
+from .race_causal_cuda import _op_inputs, op_state
 from .race_common import _hash_shape
 
 
-def race_nc_fwd(probsK, probsQ, V2, eps, block=0):
+def race_nc_fwd(probsK, probsQ, V2, eps, block=0, state=None):
+    """With `state` (race_causal_cuda.op_state), the whole-sequence totals are left there for
+    race_nc_bwd."""
     pK, pQ, V = _op_inputs(probsK, probsQ, V2)
     N, T, S = pK.shape
     D = V.shape[2]
     lib = _lib.lib()
     ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, block, 0), pK.device)
     out = torch.empty(N, T, D, dtype=torch.float32, device=pK.device)
-    _lib.check(lib.race_nc_op_fwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(out), N, T, S, D, float(eps),
-                                  block, _lib.ptr(ws), ws.numel(), _lib.stream_of(pK)), "race_nc_op_fwd")
+    args = (_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(out), N, T, S, D, float(eps), block, _lib.ptr(ws),
+            ws.numel())
+    if state is None:
+        _lib.check(lib.race_nc_op_fwd(*args, _lib.stream_of(pK)), "race_nc_op_fwd")
+    else:
+        _lib.check(lib.race_nc_op_fwd_keep(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_nc_op_fwd_keep")
     return out
 
 
-def race_nc_bwd(probsK, probsQ, V2, grad_out, eps, block=0):
+def race_nc_bwd(probsK, probsQ, V2, grad_out, eps, block=0, state=None):
     pK, pQ, V = _op_inputs(probsK, probsQ, V2)
     N, T, S = pK.shape
     D = V.shape[2]
@@ -42,9 +48,12 @@ def race_nc_bwd(probsK, probsQ, V2, grad_out, eps, block=0):
     lib = _lib.lib()
     ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, block, 1), pK.device)
     gpK, gpQ, gV = torch.empty_like(pK), torch.empty_like(pQ), torch.empty_like(V)
-    _lib.check(lib.race_nc_op_bwd(_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(gO), _lib.ptr(gpK),
-                                  _lib.ptr(gpQ), _lib.ptr(gV), N, T, S, D, float(eps), block, _lib.ptr(ws),
-                                  ws.numel(), _lib.stream_of(pK)), "race_nc_op_bwd")
+    args = (_lib.ptr(pK), _lib.ptr(pQ), _lib.ptr(V), _lib.ptr(gO), _lib.ptr(gpK), _lib.ptr(gpQ), _lib.ptr(gV), N, T,
+            S, D, float(eps), block, _lib.ptr(ws), ws.numel())
+    if state is None:
+        _lib.check(lib.race_nc_op_bwd(*args, _lib.stream_of(pK)), "race_nc_op_bwd")
+    else:
+        _lib.check(lib.race_nc_op_bwd_kept(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_nc_op_bwd_kept")
     return gpK, gpQ, gV
 
 
@@ -53,14 +62,16 @@ class RaceNonCausalFn(Function):
 
     @staticmethod
     def forward(ctx, probsK, probsQ, V2, eps):
-        ctx.save_for_backward(probsK, probsQ, V2)
+        state = op_state(probsK, V2)  # the totals stay there for the backward
+        out = race_nc_fwd(probsK, probsQ, V2, eps, state=state)
+        ctx.save_for_backward(probsK, probsQ, V2, state)
         ctx.eps = float(eps)
-        return race_nc_fwd(probsK, probsQ, V2, eps)
+        return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        pK, pQ, V2 = ctx.saved_tensors
-        gpK, gpQ, gV = race_nc_bwd(pK, pQ, V2, grad_out, ctx.eps)
+        pK, pQ, V2, state = ctx.saved_tensors
+        gpK, gpQ, gV = race_nc_bwd(pK, pQ, V2, grad_out, ctx.eps, state=state)
         return gpK, gpQ, gV.to(V2.dtype), None
 
 

@@ -145,3 +145,18 @@ def test_soft_hash_extreme_temperature(dev):
                                 ("dscale", sd.grad.reshape(1), s32.grad.reshape(1), s64.grad.reshape(1))):
         floor = orc.relerr(g32, g64)
         check(name, got, g64, max(TOL, 2.0 * floor))
+
+
+def test_noncausal_backward_from_kept_totals(dev):
+    """race_nc_bwd reading the forward's kept totals (RaceNonCausalFn's path) is bitwise the one
+    that recomputes them; the state is only read, so a second backward on it is equal."""
+    from race_attention_amd.noncausal import race_nc_bwd, race_nc_fwd
+    from race_attention_amd.race_causal_cuda import op_state
+    pk, pq, v, go = (x.to(dev) for x in _probs(2, 5000, 24, 64, seed=31))
+    state = op_state(pk, v)
+    assert torch.equal(race_nc_fwd(pk, pq, v, 1e-6, state=state), race_nc_fwd(pk, pq, v, 1e-6))
+    ref = race_nc_bwd(pk, pq, v, go, 1e-6)
+    for rep in range(2):
+        got = race_nc_bwd(pk, pq, v, go, 1e-6, state=state)
+        for name, a, b in zip(("gpK", "gpQ", "gV"), got, ref):
+            assert torch.equal(a, b), f"call {rep}: {name} from the kept totals differs"
