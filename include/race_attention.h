@@ -122,6 +122,18 @@ int race_causal_dot_backward(const float *Q, const float *K, const float *V, con
                              float *gQ, float *gK, float *gV, int64_t N, int64_t L, int64_t E,
                              int64_t M, int64_t block, void *workspace, size_t workspace_bytes,
                              race_stream stream);
+/* The same pair keeping the forward's block states in `state` (race_op_state_bytes(N, L, E, M,
+ * block) bytes, 256-byte aligned) for a backward that reads them instead of recomputing them;
+ * bitwise the same results. No counterpart in the reference (linear_pref.cpp:138-213 recomputes
+ * the running sums in its backward): for autograd callers that keep the state. */
+int race_causal_dot_product_keep(const float *Q, const float *K, const float *V, float *out,
+                                 int64_t N, int64_t L, int64_t E, int64_t M, int64_t block,
+                                 void *workspace, size_t workspace_bytes, float *state,
+                                 race_stream stream);
+int race_causal_dot_backward_kept(const float *Q, const float *K, const float *V, const float *gO,
+                                  float *gQ, float *gK, float *gV, int64_t N, int64_t L, int64_t E,
+                                  int64_t M, int64_t block, void *workspace,
+                                  size_t workspace_bytes, const float *state, race_stream stream);
 
 /* ---------------------------------------------------------------- non-causal op */
 /* Non-causal RACE of BatchedACE (scaling/benchmark_time.py:139-160), replacing its

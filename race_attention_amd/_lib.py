@@ -65,6 +65,10 @@ SIGNATURES = {
                                                ctypes.c_size_t, _vp]),
     "race_causal_dot_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                                 _vp, ctypes.c_size_t, _vp]),
+    "race_causal_dot_product_keep": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp,
+                                                    ctypes.c_size_t, _vp, _vp]),
+    "race_causal_dot_backward_kept": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                                     _i64, _vp, ctypes.c_size_t, _vp, _vp]),
     "race_op_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, ctypes.c_int]),
     "race_op_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
                                    ctypes.c_size_t, _vp]),

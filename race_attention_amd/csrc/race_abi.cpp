@@ -560,6 +560,26 @@ int race_causal_dot_backward(const float *Q, const float *K, const float *V, con
                        "race_causal_dot_backward");
 }
 
+int race_causal_dot_product_keep(const float *Q, const float *K, const float *V, float *out, int64_t N, int64_t L,
+                                 int64_t E, int64_t M, int64_t block, void *workspace, size_t workspace_bytes,
+                                 float *state, race_stream stream)
+{
+    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
+        return fail(RACE_ERR_INVALID, "race_causal_dot_product_keep: state must be a 256-byte aligned buffer");
+    return op_fwd_impl(K, Q, V, out, N, L, E, M, 0.0f, block, workspace, workspace_bytes, stream, 1,
+                       "race_causal_dot_product_keep", state);
+}
+
+int race_causal_dot_backward_kept(const float *Q, const float *K, const float *V, const float *gO, float *gQ,
+                                  float *gK, float *gV, int64_t N, int64_t L, int64_t E, int64_t M, int64_t block,
+                                  void *workspace, size_t workspace_bytes, const float *state, race_stream stream)
+{
+    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
+        return fail(RACE_ERR_INVALID, "race_causal_dot_backward_kept: state must be a 256-byte aligned buffer");
+    return op_bwd_impl(K, Q, V, gO, gK, gQ, gV, N, L, E, M, 0.0f, block, workspace, workspace_bytes, stream, 1,
+                       "race_causal_dot_backward_kept", state);
+}
+
 // ============================================================================ non-causal op
 static size_t nc_bytes(const Geo &g, int backward)
 {

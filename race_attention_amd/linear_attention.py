@@ -30,8 +30,17 @@ def _dest(t, inputs):
     return torch.empty(N * H, L, F, dtype=torch.float32, device=t.device), True
 
 
-def causal_dot_product(queries, keys, values, product):
-    """Writes out = causal linear attention into `product` [N,H,L,M] (as the reference)."""
+def linear_state(queries, values):
+    """A buffer for the block states that causal_dot_product(..., state=) keeps for
+    causal_dot_backward(..., state=)."""
+    N, H, L, E = queries.shape
+    n = _lib.lib().race_op_state_bytes(N * H, L, E, values.shape[3], 0)
+    return torch.empty((n + 3) // 4, dtype=torch.float32, device=queries.device)
+
+
+def causal_dot_product(queries, keys, values, product, state=None):
+    """Writes out = causal linear attention into `product` [N,H,L,M] (as the reference). With
+    `state` (linear_state), the block states are left there for causal_dot_backward."""
     _lib.require_device(queries, keys, values, product)
     N, H, L, E = queries.shape
     M = values.shape[3]
@@ -41,15 +50,21 @@ def causal_dot_product(queries, keys, values, product):
     out, copy_out = _dest(product, (queries, keys, values, Q, K, V))
     lib = _lib.lib()
     ws = _lib.workspace(lib.race_op_workspace_bytes(N * H, L, E, M, 0, 0), Q.device)
-    _lib.check(lib.race_causal_dot_product(_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(out), N * H, L, E, M, 0,
-                                           _lib.ptr(ws), ws.numel(), _lib.stream_of(Q)), "race_causal_dot_product")
+    args = (_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(out), N * H, L, E, M, 0, _lib.ptr(ws), ws.numel())
+    if state is None:
+        _lib.check(lib.race_causal_dot_product(*args, _lib.stream_of(Q)), "race_causal_dot_product")
+    else:
+        _lib.check(lib.race_causal_dot_product_keep(*args, _lib.ptr(state), _lib.stream_of(Q)),
+                   "race_causal_dot_product_keep")
     if copy_out:
         product.copy_(out.view(N, H, L, M))
     return product
 
 
-def causal_dot_backward(queries, keys, values, grad_out, grad_queries, grad_keys, grad_values):
-    """Writes the gradients of causal_dot_product into grad_queries / grad_keys / grad_values."""
+def causal_dot_backward(queries, keys, values, grad_out, grad_queries, grad_keys, grad_values, state=None):
+    """Writes the gradients of causal_dot_product into grad_queries / grad_keys / grad_values;
+    with `state` from causal_dot_product(..., state=) on the same inputs, the forward block
+    states are read from it instead of recomputed."""
     _lib.require_device(queries, keys, values, grad_out)
     N, H, L, E = queries.shape
     M = values.shape[3]
@@ -58,9 +73,13 @@ def causal_dot_backward(queries, keys, values, grad_out, grad_queries, grad_keys
     (gQ, cq), (gK, ck), (gV, cv) = _dest(grad_queries, ins), _dest(grad_keys, ins), _dest(grad_values, ins)
     lib = _lib.lib()
     ws = _lib.workspace(lib.race_op_workspace_bytes(N * H, L, E, M, 0, 1), Q.device)
-    _lib.check(lib.race_causal_dot_backward(_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(G), _lib.ptr(gQ),
-                                            _lib.ptr(gK), _lib.ptr(gV), N * H, L, E, M, 0, _lib.ptr(ws), ws.numel(),
-                                            _lib.stream_of(Q)), "race_causal_dot_backward")
+    args = (_lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), _lib.ptr(G), _lib.ptr(gQ), _lib.ptr(gK), _lib.ptr(gV), N * H, L, E,
+            M, 0, _lib.ptr(ws), ws.numel())
+    if state is None:
+        _lib.check(lib.race_causal_dot_backward(*args, _lib.stream_of(Q)), "race_causal_dot_backward")
+    else:
+        _lib.check(lib.race_causal_dot_backward_kept(*args, _lib.ptr(state), _lib.stream_of(Q)),
+                   "race_causal_dot_backward_kept")
     for dst, buf, cp in ((grad_queries, gQ, cq), (grad_keys, gK, ck), (grad_values, gV, cv)):
         if cp:
             dst.copy_(buf.view(dst.shape))
@@ -72,17 +91,18 @@ class CausalLinearFn(Function):
     @staticmethod
     def forward(ctx, Q, K, V):
         out = torch.empty(Q.shape[0], Q.shape[1], Q.shape[2], V.shape[3], dtype=torch.float32, device=Q.device)
-        causal_dot_product(Q, K, V, out)
-        ctx.save_for_backward(Q, K, V)
+        state = linear_state(Q, V)  # the block states stay there for the backward
+        causal_dot_product(Q, K, V, out, state=state)
+        ctx.save_for_backward(Q, K, V, state)
         return out
 
     @staticmethod
     def backward(ctx, g):
-        Q, K, V = ctx.saved_tensors
+        Q, K, V, state = ctx.saved_tensors
         gQ = torch.empty(Q.shape, dtype=torch.float32, device=Q.device)
         gK = torch.empty(K.shape, dtype=torch.float32, device=K.device)
         gV = torch.empty(V.shape, dtype=torch.float32, device=V.device)
-        causal_dot_backward(Q, K, V, g, gQ, gK, gV)
+        causal_dot_backward(Q, K, V, g, gQ, gK, gV, state=state)
         return gQ.to(Q.dtype), gK.to(K.dtype), gV.to(V.dtype)
 
 

@@ -56,3 +56,23 @@ def test_causal_linear_destinations(dev):
     check("gQ", gq, q1.grad, 2e-3)
     check("gK (strided)", gk, k1.grad, 2e-3)
     check("gV (aliased)", Ga, v1.grad, 2e-3)
+
+
+def test_causal_linear_backward_from_kept_state(dev):
+    """causal_dot_backward reading the forward's kept block states (CausalLinearFn's path) is
+    bitwise the one that recomputes them, also when called twice on the same state."""
+    from race_attention_amd.linear_attention import causal_dot_backward, causal_dot_product, linear_state
+    g = torch.Generator(device=dev).manual_seed(4)
+    Q, K, V, G = (torch.randn(2, 2, 3000, 32, generator=g, device=dev) for _ in range(4))
+    st = linear_state(Q, V)
+    a, b = torch.empty_like(V), torch.empty_like(V)
+    causal_dot_product(Q, K, V, a, state=st)
+    causal_dot_product(Q, K, V, b)
+    assert torch.equal(a, b)
+    ref = [torch.empty_like(x) for x in (Q, K, V)]
+    causal_dot_backward(Q, K, V, G, *ref)
+    for rep in range(2):
+        got = [torch.empty_like(x) for x in (Q, K, V)]
+        causal_dot_backward(Q, K, V, G, *got, state=st)
+        for name, x, y in zip(("gQ", "gK", "gV"), got, ref):
+            assert torch.equal(x, y), f"call {rep}: {name} from the kept state differs"
