@@ -32,8 +32,8 @@ bool op_variant_exists(int ST, int DP);
 constexpr int QKV_C = 32, QKV_NW = 4;
 // fp32 op path: waves per workgroup. 4 for the totals kernels; for the readout and backward main
 // kernels 8 at head-dim tiles of 64 and more, whose long sub-chunk phases hide more latency with
-// them (at 2^20 tokens and D = 64: 1.57 -> 1.05 and 4.81 -> 3.50 ms; D = 128 and 256 alike),
-// and 4 at 32, where 8 measured slower
+// them (at 2^20 (token, head) pairs and D = 64: 1.57 -> 1.05 and 4.81 -> 3.50 ms; D = 128 and
+// 256 alike), and 4 at 32, where 8 measured slower
 constexpr int OP_C = 16, OP_NW_TOTALS = 4;
 constexpr int op_nw_main(int DP) { return DP >= 64 ? 8 : 4; }
 
