@@ -62,17 +62,20 @@ class RaceNonCausalFn(Function):
 
     @staticmethod
     def forward(ctx, probsK, probsQ, V2, eps):
-        state = op_state(probsK, V2)  # the totals stay there for the backward
-        out = race_nc_fwd(probsK, probsQ, V2, eps, state=state)
-        ctx.save_for_backward(probsK, probsQ, V2, state)
+        # contiguous fp32 once, saved as such (a strided V2 view is not copied again in the backward)
+        pK, pQ, V = _op_inputs(probsK, probsQ, V2)
+        state = op_state(pK, V)  # the totals stay there for the backward
+        out = race_nc_fwd(pK, pQ, V, eps, state=state)
+        ctx.save_for_backward(pK, pQ, V, state)
+        ctx.v_dtype = V2.dtype
         ctx.eps = float(eps)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        pK, pQ, V2, state = ctx.saved_tensors
-        gpK, gpQ, gV = race_nc_bwd(pK, pQ, V2, grad_out, ctx.eps, state=state)
-        return gpK, gpQ, gV.to(V2.dtype), None
+        pK, pQ, V, state = ctx.saved_tensors
+        gpK, gpQ, gV = race_nc_bwd(pK, pQ, V, grad_out, ctx.eps, state=state)
+        return gpK, gpQ, gV.to(ctx.v_dtype), None
 
 
 class SoftHashTempFn(Function):
