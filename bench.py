@@ -101,7 +101,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
-              "(the hot path shards over heads/sequence with one exchange; see DESIGN.md)", file=sys.stderr)
+              "(the hot path would shard over kv heads and sequence blocks, with one exchange of block states)", file=sys.stderr)
         sys.exit(2)
 
     import torch
