@@ -53,7 +53,8 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (x3), the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
-    ap.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5", "noncausal", "linear"],
+    ap.add_argument("--workload", default="cfg3",
+                    choices=["cfg1", "cfg2", "cfg3", "cfg5", "op", "noncausal", "linear"],
                     help="cfg1: the reference's fp32 op path (soft_hash_probs + RaceCausalFn) fwd+bwd at "
                          "B=2, H=8, T=2048, D=64, L=8, K=4, scale sqrt(D) and 1.0, with the CPU path on the same "
                          "inputs; cfg2: the same layer step at B=4, H=16, T=65536, L=16 (S=256), q/k/v ~ N(0,1); "
@@ -125,6 +126,9 @@ def main():
         return
     if args.workload == "cfg1":
         print(json.dumps(bench_cfg1(torch, args)))
+        return
+    if args.workload == "op":  # the fp32 op path at 2^20 (token, head) pairs
+        print(json.dumps(bench_cfg1(torch, args, B=1, H=4, T=1 << 18, name="op", cpu_T=1 << 13)))
         return
     if args.workload == "noncausal":
         print(json.dumps(bench_noncausal(torch, args)))
@@ -343,11 +347,13 @@ def bench_hybrid(torch, args, B=8, T=8192, n_new=256):
             "dtype": "bf16", "data": "synthetic uniform token ids, random-init weights"}
 
 
-def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6):
+def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6, name="cfg1", cpu_T=None):
     """cfg1: fp32 q/k/v/go ~ N(0,1) drawn on the CPU (the same bits on both devices), planes seed 0.
     GPU: the reference's fp32 op path (soft_hash_probs + RaceCausalFn, forward and backward) at the
     reference's scale sqrt(D) and at 1.0; CPU: the reference CPU path (the port, whose soft-hash
-    fixes sqrt(D)) on the same inputs, all host cores, median of 3."""
+    fixes sqrt(D)) on the same inputs (their first cpu_T tokens when given), all host cores,
+    median of 3. The same function serves the `op` workload (the op path at 2^20 (token, head)
+    pairs) with per-kernel times from the library's HIP events."""
     from oracle import race_cpu_port
     from oracle import race_oracle as orc
     from race_attention_amd.race_causal_cuda import RaceCausalFn
@@ -363,7 +369,7 @@ def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6):
     n_tok = B * H * T
     t_bound = max(f_alg * n_tok / FP32_PEAK, 11 * D * 4 * n_tok / HBM_PEAK)
     gpu = {}
-    for name, scale in (("scale_sqrt_D", math.sqrt(D)), ("scale_1", 1.0)):
+    for sname, scale in (("scale_sqrt_D", math.sqrt(D)), ("scale_1", 1.0)):
         def step():
             q.grad = k.grad = v.grad = None
             pK, pQ, V2, _ = soft_hash_probs(q, k, v, planes_T, protos_T, L, K, 1, True, scale=scale)
@@ -379,17 +385,23 @@ def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6):
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / args.steps
-        gpu[name] = {"value": round(B * T / (ms / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+        gpu[sname] = {"value": round(B * T / (ms / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
                      "layer_roofline": {"bound": "fp32 compute", "t_bound_ms": round(t_bound * 1e3, 4),
                                         "frac": round(t_bound * 1e3 / ms, 4)}}
+    split = None
+    if cpu_T is not None:  # per-kernel times at scale 1.0 (the last configuration timed)
+        from race_attention_amd import _lib
+        split = _kernel_split(torch, _lib, step, 3)
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     pl_c, pr_c = orc.build_planes_protos(D, K, L, seed=0)
-    qc, kc, vc = (x.clone().requires_grad_(True) for x in (Q, Kt, V))
+    Tc = T if cpu_T is None else min(T, cpu_T)
+    qc, kc, vc = (x[:, :, :Tc].clone().requires_grad_(True) for x in (Q, Kt, V))
+    goc = go[:, :, :Tc].contiguous()
 
     def run_cpu():
         qc.grad = kc.grad = vc.grad = None
-        race_cpu_port.race_layer_cpu(qc, kc, vc, pl_c, pr_c, L, K).backward(go)
+        race_cpu_port.race_layer_cpu(qc, kc, vc, pl_c, pr_c, L, K).backward(goc)
 
     run_cpu()
     ts = []
@@ -398,12 +410,16 @@ def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6):
         run_cpu()
         ts.append(time.perf_counter() - t0)
     sec = sorted(ts)[1]
-    return {"metric": "cfg1 fp32 layer fwd+bwd tokens/sec", "workload": "cfg1", "dtype": "f32",
-            "config": {"B": B, "H": H, "T": T, "D": D, "L": L, "K": K, "S": S, "path": "soft_hash_probs + RaceCausalFn"},
-            "gpu": gpu,
-            "cpu_baseline": {"value": round(B * T / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
-                             "sample": f"the whole cfg1 layer fwd+bwd (scale sqrt(D)), median of 3",
-                             "seconds_per_step": round(sec, 3)}}
+    sample = (f"the whole {name} layer fwd+bwd (scale sqrt(D)), median of 3" if Tc == T else
+              f"the {name} layer fwd+bwd on its first {Tc} tokens (scale sqrt(D)), median of 3")
+    r = {"metric": f"{name} fp32 layer fwd+bwd tokens/sec", "workload": name, "dtype": "f32",
+         "config": {"B": B, "H": H, "T": T, "D": D, "L": L, "K": K, "S": S, "path": "soft_hash_probs + RaceCausalFn"},
+         "gpu": gpu,
+         "cpu_baseline": {"value": round(B * Tc / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+                          "sample": sample, "seconds_per_step": round(sec, 3)}}
+    if split is not None:
+        r["kernels_ms_per_step"] = split
+    return r
 
 
 def _time_steps(torch, step, warmup, steps):
