@@ -25,7 +25,10 @@ def lib():
         L.orc_prefix_mean_flat_bw.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, dbl]
         L.orc_race_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, dbl]
         L.orc_race_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, dbl]
-        for f in (L.orc_prefix_mean_flat, L.orc_prefix_mean_flat_bw, L.orc_race_fwd, L.orc_race_bwd):
+        L.orc_race_windows.argtypes = [vp, vp, vp, vp, i64, i64, i64, dbl, vp, vp, vp, i64, i64,
+                                       vp, vp, vp, vp]
+        for f in (L.orc_prefix_mean_flat, L.orc_prefix_mean_flat_bw, L.orc_race_fwd, L.orc_race_bwd,
+                  L.orc_race_windows):
             f.restype = None
         _LIB = L
     return _LIB
@@ -88,6 +91,42 @@ def race_bwd(pK, pQ, V, gO, eps):
     lib().orc_race_bwd(a, b, c, d, ctypes.c_void_p(gpK.data_ptr()), ctypes.c_void_p(gpQ.data_ptr()),
                        ctypes.c_void_p(gV.data_ptr()), N, T, S, D, float(eps))
     return gpK, gpQ, gV
+
+
+def race_windows(pK, pQ, V, gO, eps, wins, wlen, A0=None, B0=None):
+    """One stream (pK, pQ [T,S], V [T,D], gO [T,D] or None) of the streaming fp64 forward
+    and backward, kept on the token windows [w, w + wlen) for w in `wins` (sorted, disjoint),
+    starting from the carried-in bucket state (A0 [S], B0 [S,D]) when given.
+    Returns out [nwin,wlen,D] and, with gO, (gpK, gpQ [nwin,wlen,S], gV [nwin,wlen,D])."""
+    pK, a = _c(pK, torch.float64)
+    pQ, b = _c(pQ, torch.float64)
+    V, c = _c(V, torch.float64)
+    T, S = pK.shape
+    D = V.shape[1]
+    wins = sorted(int(w) for w in wins)
+    for i, w in enumerate(wins):
+        if w < 0 or w + wlen > T or (i and wins[i - 1] + wlen > w):
+            raise ValueError(f"window starts {wins} (length {wlen}) must be disjoint and inside [0, {T})")
+    wt = torch.tensor(wins, dtype=torch.int64)
+    nw = len(wins)
+    out = torch.empty(nw, wlen, D, dtype=torch.float64)
+    keep = [pK, pQ, V, wt]
+    gp = ctypes.c_void_p(0)
+    res = [out]
+    if gO is not None:
+        gO, gp = _c(gO, torch.float64)
+        keep.append(gO)
+        res += [torch.empty(nw, wlen, S, dtype=torch.float64), torch.empty(nw, wlen, S, dtype=torch.float64),
+                torch.empty(nw, wlen, D, dtype=torch.float64)]
+    pa = pb = ctypes.c_void_p(0)
+    if A0 is not None:
+        A0, pa = _c(A0, torch.float64)
+        B0, pb = _c(B0, torch.float64)
+        keep += [A0, B0]
+    ptrs = [ctypes.c_void_p(r.data_ptr()) for r in res] + [ctypes.c_void_p(0)] * (4 - len(res))
+    lib().orc_race_windows(a, b, c, gp, T, S, D, float(eps), pa, pb, ctypes.c_void_p(wt.data_ptr()), nw,
+                           int(wlen), *ptrs)
+    return res[0] if gO is None else tuple(res)
 
 
 def _load_ref(name):

@@ -20,6 +20,9 @@
  *                             gA = -pQ*gW/(A+eps)^2; gB = pQ*go/(A+eps);
  *                             suffix sums gAn, gBn; gpK = gAn + <gBn, v>;
  *                             gv = sum_s pK * gBn.
+ *  orc_race_windows         the same forward/backward for one long stream with
+ *                           the buckets split over threads, an optional carried-in
+ *                           prefix state, and outputs kept only on token windows.
  * Pinned in tests/test_oracle.py against torch fp64 autograd, gradcheck and the
  * compiled reference kernel (oracle/_ref) when that is built.
  */
@@ -193,4 +196,133 @@ void orc_race_bwd(const double *pK, const double *pQ, const double *V, const dou
         free(gA);
         free(W);
     }
+}
+
+/*
+ * orc_race_windows: one stream of the same streaming fp64 forward/backward as
+ * orc_race_fwd / orc_race_bwd (race_common.py:76-90; backward_kernels.cu:10-17),
+ * for long sequences where only some token windows are compared. The buckets are
+ * split over the OpenMP threads (every bucket's scan is independent; the outputs
+ * that sum over buckets are reduced at the end), so one stream of 2^20 tokens at
+ * S = 128 runs in seconds.
+ *   pK, pQ [T][S], V [T][D], gO [T][D] or NULL (forward only);
+ *   A0 [S], B0 [S][D] or NULL: bucket state carried in before token 0 (the
+ *     sequence's earlier tokens), so a late window of a long sequence is checked
+ *     from its exact prefix state;
+ *   wins [nwin] sorted, non-overlapping window starts, each [w, w + wlen) in [0, T);
+ *   out_w [nwin][wlen][D]; with gO also gpK_w, gpQ_w [nwin][wlen][S], gV_w [nwin][wlen][D]
+ *   (the suffix sums of the backward run over [0, T)).
+ */
+#include <omp.h>
+
+void orc_race_windows(const double *pK, const double *pQ, const double *V, const double *gO,
+                      int64_t T, int64_t S, int64_t D, double eps, const double *A0,
+                      const double *B0, const int64_t *wins, int64_t nwin, int64_t wlen,
+                      double *out_w, double *gpK_w, double *gpQ_w, double *gV_w)
+{
+    int32_t *widx = (int32_t *)malloc((size_t)T * sizeof(int32_t));
+    for (int64_t t = 0; t < T; ++t)
+        widx[t] = -1;
+    for (int64_t w = 0; w < nwin; ++w)
+        for (int64_t i = 0; i < wlen; ++i)
+            widx[wins[w] + i] = (int32_t)(w * wlen + i);
+    const int64_t nrow = nwin * wlen;
+    int nth = omp_get_max_threads();
+    if (nth > S)
+        nth = (int)S;
+    double *part_out = (double *)calloc((size_t)(nth * nrow * D), sizeof(double));
+    double *part_gv = gO ? (double *)calloc((size_t)(nth * nrow * D), sizeof(double)) : NULL;
+#pragma omp parallel num_threads(nth)
+    {
+        const int id = omp_get_thread_num();
+        const int64_t s0 = S * id / nth, s1 = S * (id + 1) / nth, ns = s1 - s0;
+        double *A = (double *)calloc((size_t)ns, sizeof(double));
+        double *B = (double *)calloc((size_t)(ns * D), sizeof(double));
+        double *W = gO ? (double *)malloc((size_t)(T * ns) * sizeof(double)) : NULL;
+        double *gA = gO ? (double *)malloc((size_t)(T * ns) * sizeof(double)) : NULL;
+        double *po = part_out + id * nrow * D;
+        if (A0)
+            for (int64_t j = 0; j < ns; ++j)
+                A[j] = A0[s0 + j];
+        if (B0)
+            memcpy(B, B0 + s0 * D, (size_t)(ns * D) * sizeof(double));
+        for (int64_t t = 0; t < T; ++t) {
+            const int32_t wi = widx[t];
+            const double *v = V + t * D;
+            const double *go = gO ? gO + t * D : NULL;
+            for (int64_t j = 0; j < ns; ++j) {
+                const int64_t s = s0 + j;
+                const double pk = pK[t * S + s];
+                A[j] += pk;
+                double *b = B + j * D;
+                double gw = 0.0;
+                if (go) {
+                    for (int64_t d = 0; d < D; ++d) {
+                        b[d] += pk * v[d];
+                        gw += go[d] * b[d];
+                    }
+                } else {
+                    for (int64_t d = 0; d < D; ++d)
+                        b[d] += pk * v[d];
+                }
+                const double inv = 1.0 / (A[j] + eps);
+                const double w = pQ[t * S + s] * inv;
+                if (go) {
+                    W[t * ns + j] = w;
+                    gA[t * ns + j] = -w * gw * inv;
+                }
+                if (wi >= 0) {
+                    double *o = po + (int64_t)wi * D;
+                    for (int64_t d = 0; d < D; ++d)
+                        o[d] += w * b[d];
+                    if (go)
+                        gpQ_w[(int64_t)wi * S + s] = gw * inv;
+                }
+            }
+        }
+        if (gO) {
+            double *pg = part_gv + id * nrow * D;
+            memset(A, 0, (size_t)ns * sizeof(double));
+            memset(B, 0, (size_t)(ns * D) * sizeof(double));
+            for (int64_t t = T - 1; t >= 0; --t) {
+                const int32_t wi = widx[t];
+                const double *v = V + t * D;
+                const double *go = gO + t * D;
+                for (int64_t j = 0; j < ns; ++j) {
+                    A[j] += gA[t * ns + j];
+                    double *gb = B + j * D;
+                    const double w = W[t * ns + j];
+                    for (int64_t d = 0; d < D; ++d)
+                        gb[d] += w * go[d];
+                    if (wi >= 0) {
+                        const double pk = pK[t * S + s0 + j];
+                        double dot = 0.0, *g = pg + (int64_t)wi * D;
+                        for (int64_t d = 0; d < D; ++d) {
+                            dot += gb[d] * v[d];
+                            g[d] += pk * gb[d];
+                        }
+                        gpK_w[(int64_t)wi * S + s0 + j] = A[j] + dot;
+                    }
+                }
+            }
+        }
+        free(A);
+        free(B);
+        free(W);
+        free(gA);
+    }
+    for (int64_t i = 0; i < nrow * D; ++i) {
+        double so = 0.0, sg = 0.0;
+        for (int k = 0; k < nth; ++k) {
+            so += part_out[k * nrow * D + i];
+            if (gO)
+                sg += part_gv[k * nrow * D + i];
+        }
+        out_w[i] = so;
+        if (gO)
+            gV_w[i] = sg;
+    }
+    free(part_out);
+    free(part_gv);
+    free(widx);
 }

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_sizes():
     lib = _lib.load_library()
-    assert lib.race_abi_version() == 1
+    assert lib.race_abi_version() == 2
     sh = _lib.QKVShape(1, 4, 4, 1 << 20, 64, 8, 4, 8.0, 1e-6, 0)
     state = lib.race_qkv_state_bytes(sh)
     # per-block states (A and St, fp32, one slot per block plus the final state), not [T,S]
@@ -95,8 +95,64 @@ def test_kept_state_must_be_aligned():
     assert lib.race_op_state_bytes(2, 100, 24, 64, 0) > 0
     assert lib.race_op_state_bytes(0, 100, 24, 64, 0) == 0
     rc = lib.race_op_fwd_keep(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
-                              2, 100, 24, 64, 1e-6, 0, ctypes.c_void_p(16), 1 << 30, ctypes.c_void_p(256 + 4), None)
+                              2, 100, 24, 64, 1e-6, 0, ctypes.c_void_p(16), 1 << 30, ctypes.c_void_p(256 + 4), 1 << 30,
+                              None)
     assert rc == 1 and "256-byte aligned" in lib.race_last_error().decode()
     rc = lib.race_op_bwd_kept(*(ctypes.c_void_p(16),) * 7, 2, 100, 24, 64, 1e-6, 0, ctypes.c_void_p(16), 1 << 30,
-                              None, None)
+                              None, 1 << 30, None)
     assert rc == 1 and "256-byte aligned" in lib.race_last_error().decode()
+
+
+KEPT = [("race_op_fwd_keep", 4), ("race_op_bwd_kept", 7), ("race_nc_op_fwd_keep", 4), ("race_nc_op_bwd_kept", 7),
+        ("race_causal_dot_product_keep", 4), ("race_causal_dot_backward_kept", 7)]
+
+
+@pytest.mark.parametrize("name,nptr", KEPT)
+def test_kept_state_size_is_checked(name, nptr):
+    """Every kept-state entry point rejects, on the host, a state buffer smaller than its own
+    geometry needs (one sized for a shorter sequence or another block), before any launch."""
+    lib = _lib.load_library()
+    fn = getattr(lib, name)
+    linear = "dot" in name
+    need = lib.race_op_state_bytes(2, 4096, 24, 64, 0)
+    small = lib.race_op_state_bytes(2, 1024, 24, 64, 0)
+    assert 0 < small < need
+    ptrs = (ctypes.c_void_p(256),) * nptr
+    head = (2, 4096, 24, 64) + (() if linear else (1e-6,)) + (0, ctypes.c_void_p(256), 1 << 30)
+    for bytes_, ok in ((small, False), (need - 1, False)):
+        rc = fn(*ptrs, *head, ctypes.c_void_p(512), bytes_, None)
+        assert rc == 3 and "state of" in lib.race_last_error().decode(), (name, bytes_)
+    # a buffer sized for another block (128 tokens: fewer block slots than the automatic 64)
+    other = lib.race_op_state_bytes(2, 4096, 24, 64, 128)
+    assert 0 < other < need
+    assert fn(*ptrs, *head, ctypes.c_void_p(512), other, None) == 3
+
+
+def test_op_state_raises_the_geometry_error():
+    """op_state / linear_state raise the library's reason when the geometry is rejected (here a
+    head dim beyond the compiled 256) instead of handing on an empty buffer."""
+    import torch
+    from race_attention_amd.race_causal_cuda import op_state
+    with pytest.raises(_lib.RaceError, match="head dim"):
+        op_state(torch.empty(1, 8, 24), torch.empty(1, 8, 300))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,D,L,Kb", [(1, 4, 4, 1 << 20, 64, 8, 4), (4, 16, 16, 65536, 64, 16, 4),
+                                               (1, 8, 2, 1 << 18, 64, 8, 4), (1, 4, 4, 1 << 24, 64, 8, 4),
+                                               (2, 4, 1, 333, 128, 3, 3), (1, 2, 2, 65536, 64, 8, 4)])
+def test_full_size_tests_know_the_block_geometry(B, Hq, Hkv, T, D, L, Kb):
+    """tests/race_ref.qkv_blocks (where the full-size GPU tests put their block-boundary windows)
+    agrees with the library: the state it sizes holds exactly NB + 1 slots per stream and tile."""
+    import sys
+    sys.path.insert(0, os.path.dirname(__file__))
+    from race_ref import qkv_blocks
+    lib = _lib.load_library()
+    sh = _lib.QKVShape(B, Hq, Hkv, T, D, L, Kb, 8.0, 1e-6, 0)
+    CB, NB = qkv_blocks(T, B * Hkv, L, Kb, D)
+    S = L << Kb
+    st = next((x for x in (32, 64, 128) if (128 if D == 64 else 64) >= x >= S), 128 if D == 64 else 64)
+    S_pad = -(-S // st) * st
+    slots = B * Hkv * (NB + 1) * S_pad
+    a256 = lambda n: (n + 255) // 256 * 256
+    assert lib.race_qkv_state_bytes(sh) == a256(slots * D * 4) + a256(slots * 4)
+    assert (NB - 1) * CB < T <= NB * CB and CB % 32 == 0

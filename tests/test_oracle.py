@@ -162,6 +162,71 @@ def test_c_streaming_fwd_bwd_equal_autograd():
     assert orc.relerr(gv, c.grad) < 1e-12
 
 
+def test_c_windows_equal_streaming_fwd_bwd():
+    """orc_race_windows (buckets split over threads, outputs on windows) equals the full
+    streaming C forward/backward on every window, including the first and last token."""
+    g = torch.Generator().manual_seed(5)
+    T, L, R, D, eps = 700, 3, 8, 9, 1e-6
+    pk, pq = softmax_probs(1, T, L, R, g)[0], torch.rand(T, L * R, generator=g, dtype=F64)
+    v = torch.randn(T, D, generator=g, dtype=F64)
+    go = torch.randn(T, D, generator=g, dtype=F64)
+    out, _, _ = oracle_c.race_fwd(pk[None], pq[None], v[None], eps)
+    gpk, gpq, gv = oracle_c.race_bwd(pk[None], pq[None], v[None], go[None], eps)
+    wins, wl = [0, 301, T - 33], 33
+    o, a, b, c = oracle_c.race_windows(pk, pq, v, go, eps, wins, wl)
+    of = oracle_c.race_windows(pk, pq, v, None, eps, wins, wl)
+    for i, w in enumerate(wins):
+        assert orc.relerr(o[i], out[0, w:w + wl]) < 1e-13 and torch.equal(of[i], o[i])
+        assert orc.relerr(a[i], gpk[0, w:w + wl]) < 1e-12
+        assert orc.relerr(b[i], gpq[0, w:w + wl]) < 1e-12
+        assert orc.relerr(c[i], gv[0, w:w + wl]) < 1e-12
+    with pytest.raises(ValueError):
+        oracle_c.race_windows(pk, pq, v, None, eps, [0, 20], 33)  # overlapping windows
+
+
+def test_c_windows_carried_state_is_the_prefix():
+    """A window of [t0, T) scanned from the prefix state (A, B) of [0, t0) equals the same
+    window of the whole sequence (the late-window check of the long-context sweep)."""
+    g = torch.Generator().manual_seed(6)
+    T, t0, S, D, eps = 900, 611, 16, 5, 1e-6
+    pk, pq = softmax_probs(1, T, 2, 8, g)[0], softmax_probs(1, T, 2, 8, g)[0]
+    v = torch.randn(T, D, generator=g, dtype=F64)
+    out, _, _ = oracle_c.race_fwd(pk[None], pq[None], v[None], eps)
+    A0 = pk[:t0].sum(0)
+    B0 = pk[:t0].T @ v[:t0]
+    o = oracle_c.race_windows(pk[t0:], pq[t0:], v[t0:], None, eps, [0, 100, T - t0 - 20], 20, A0, B0)
+    for i, w in enumerate([0, 100, T - t0 - 20]):
+        assert orc.relerr(o[i], out[0, t0 + w:t0 + w + 20]) < 1e-13
+
+
+def test_group_windows_and_prefix_state_equal_layer_oracle():
+    """tests/race_ref.oracle_group_windows (the full-size GPU tests' reference) equals the whole-
+    sequence layer oracle on its windows, grouped-query heads included, and oracle_prefix_state
+    equals race_prefix_ref's final state."""
+    import sys
+    sys.path.insert(0, os.path.dirname(__file__))
+    from race_ref import oracle_group_windows, oracle_layer, oracle_prefix_state
+    g = torch.Generator().manual_seed(8)
+    B, Hq, Hkv, T, D, L, Kb, scale, eps = 2, 4, 2, 300, 16, 2, 3, 2.5, 1e-6
+    q, k, v, go = (torch.randn(B, h, T, D, generator=g) for h in (Hq, Hkv, Hkv, Hq))
+    planes_T, protos = orc.build_planes_protos(D, Kb, L, seed=3)
+    ref = oracle_layer(q, k, v, planes_T, L, Kb, scale, eps, go)
+    wins, wl = [0, 150, T - 20], 20
+    for b, hk in ((0, 0), (1, 1)):
+        out, dq, dk, dv = oracle_group_windows(q, k, v, go, planes_T, L, Kb, scale, eps, b, hk, wins, wl)
+        for i, w in enumerate(wins):
+            for gi in range(Hq // Hkv):
+                h = hk * (Hq // Hkv) + gi
+                assert orc.relerr(out[gi, i], ref[0][b, h, w:w + wl]) < 1e-12
+                assert orc.relerr(dq[gi, i], ref[1][b, h, w:w + wl]) < 1e-10
+            assert orc.relerr(dk[i], ref[2][b, hk, w:w + wl]) < 1e-10
+            assert orc.relerr(dv[i], ref[3][b, hk, w:w + wl]) < 1e-10
+    A, Bst = oracle_prefix_state(k[1, 0], v[1, 0], planes_T, L, Kb, scale, chunk=128)
+    pK, _, V2, _ = orc.soft_hash_probs(k[1:, :1], k[1:, :1], v[1:, :1], planes_T, protos, L, Kb, scale=scale)
+    _, A_ref, B_ref = orc.race_prefix_ref(pK, pK, V2)
+    assert orc.relerr(A, A_ref[0]) < 1e-12 and orc.relerr(Bst, B_ref[0]) < 1e-12
+
+
 @pytest.mark.parametrize("NS,T,D", [(1, 1, 1), (4, 1, 8), (8, 16, 32), (16, 512, 64)])
 def test_c_prefix_mean_flat(NS, T, D):
     """kernels/cpu/test_cpu_kernels.py:49-53 sweep: C restatement vs fp64 cumsum."""
