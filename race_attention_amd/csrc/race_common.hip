@@ -21,19 +21,23 @@ namespace race {
 // scan over few blocks launches few threads.
 //   rev = 0: slot b <- sum_{b' < b} x_b' (exclusive), slot NB <- total
 //   rev = 1: slot b <- sum_{b' >= b} x_b' (inclusive suffix), slot NB <- 0
+// With LO, every value is the pair (hi, lo) of a double-float (hi in ws, lo at the same offset in
+// the lo array): the inputs are read as hi + lo and the sums are written back as such pairs, so a
+// block total carried in fp64 by its producer reaches the consumer with ~48 mantissa bits.
 constexpr int SCAN_COLS = 64;
 
 // One launch scans two workspaces of the same block count: (wsB, elemsB) with the first
 // ceil(elemsB / SCAN_COLS) workgroups along x, (wsA, elemsA) with the rest.
-template <bool REV, int SEGS, int SEG>
+template <bool REV, bool LO, int SEGS, int SEG>
 __global__ __launch_bounds__(SCAN_COLS *SEGS) void race_block_scan(float *wsB, int64_t elemsB, float *wsA,
-                                                                  int64_t elemsA, int NB)
+                                                                  int64_t elemsA, float *loB, float *loA, int NB)
 {
     __shared__ double tot[SEGS][SCAN_COLS];
     const int col = threadIdx.x % SCAN_COLS, seg = threadIdx.x / SCAN_COLS;
     const int nbB = (int)((elemsB + SCAN_COLS - 1) / SCAN_COLS);
     const bool isB = (int)blockIdx.x < nbB;
     float *ws = isB ? wsB : wsA;
+    float *lo = isB ? loB : loA;
     const int64_t elems = isB ? elemsB : elemsA;
     const int64_t e = (int64_t)(isB ? blockIdx.x : blockIdx.x - nbB) * SCAN_COLS + col;
     const bool live = e < elems;
@@ -42,28 +46,31 @@ __global__ __launch_bounds__(SCAN_COLS *SEGS) void race_block_scan(float *wsB, i
     // per load, so no per-block pointer stays live
     const int64_t ec = live ? e : elems - 1;
     float *base = ws + (int64_t)blockIdx.y * (NB + 1) * elems;
+    float *lbase = LO ? lo + (int64_t)blockIdx.y * (NB + 1) * elems : nullptr;
     constexpr int SUPER = SEGS * SEG;
     double carry = 0.0;
     for (int c0 = 0; c0 < NB; c0 += SUPER) {
         // block index of this thread's i-th element (ascending, or descending when REV)
         const int first = REV ? NB - 1 - c0 - seg * SEG : c0 + seg * SEG;
-        float x[SEG];
+        double x[SEG];
 #pragma unroll
         for (int i = 0; i < SEG; ++i) {
             const int b = REV ? first - i : first + i;
             const int bc = REV ? max(b, 0) : min(b, NB - 1);
-            x[i] = base[(int64_t)bc * elems + ec];
+            x[i] = (double)base[(int64_t)bc * elems + ec];
+            if (LO)
+                x[i] += (double)lbase[(int64_t)bc * elems + ec];
         }
 #pragma unroll
         for (int i = 0; i < SEG; ++i) {
             const int b = REV ? first - i : first + i;
             if (REV ? b < 0 : b >= NB)
-                x[i] = 0.0f;
+                x[i] = 0.0;
         }
         double t = 0.0;
 #pragma unroll
         for (int i = 0; i < SEG; ++i)
-            t += (double)x[i];
+            t += x[i];
         if (SEGS > 1) {
             tot[seg][col] = t;
             __syncthreads();
@@ -85,50 +92,66 @@ __global__ __launch_bounds__(SCAN_COLS *SEGS) void race_block_scan(float *wsB, i
             const int b = REV ? first - i : first + i;
             const bool ok = live && (REV ? b >= 0 : b < NB);
             if (REV)
-                run += (double)x[i];
-            if (ok)
-                base[(int64_t)b * elems + e] = (float)run;
+                run += x[i];
+            if (ok) {
+                const float hi = (float)run;
+                base[(int64_t)b * elems + e] = hi;
+                if (LO)
+                    lbase[(int64_t)b * elems + e] = (float)(run - (double)hi);
+            }
             if (!REV)
-                run += (double)x[i];
+                run += x[i];
         }
         if (SEGS > 1)
             __syncthreads();
     }
-    if (live && seg == 0)
-        base[(int64_t)NB * elems + e] = REV ? 0.0f : (float)carry;
+    if (live && seg == 0) {
+        const float hi = REV ? 0.0f : (float)carry;
+        base[(int64_t)NB * elems + e] = hi;
+        if (LO)
+            lbase[(int64_t)NB * elems + e] = REV ? 0.0f : (float)(carry - (double)hi);
+    }
 }
 
-template <bool REV, int SEGS, int SEG>
-static void launch_scan_cfg(dim3 grid, float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB,
-                            hipStream_t s)
+template <bool REV, bool LO, int SEGS, int SEG>
+static void launch_scan_cfg(dim3 grid, float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, float *loB,
+                            float *loA, int NB, hipStream_t s)
 {
-    hipLaunchKernelGGL((race_block_scan<REV, SEGS, SEG>), grid, dim3(SCAN_COLS * SEGS), 0, s, wsB, elemsB, wsA,
-                       elemsA, NB);
+    hipLaunchKernelGGL((race_block_scan<REV, LO, SEGS, SEG>), grid, dim3(SCAN_COLS * SEGS), 0, s, wsB, elemsB, wsA,
+                       elemsA, loB, loA, NB);
 }
 
-template <bool REV>
-static void launch_scan_dir(dim3 grid, float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB,
-                            hipStream_t s)
+template <bool REV, bool LO>
+static void launch_scan_dir(dim3 grid, float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, float *loB,
+                            float *loA, int NB, hipStream_t s)
 {
     if (NB <= 8)
-        launch_scan_cfg<REV, 1, 8>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+        launch_scan_cfg<REV, LO, 1, 8>(grid, wsB, elemsB, wsA, elemsA, loB, loA, NB, s);
     else if (NB <= 32)
-        launch_scan_cfg<REV, 4, 8>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+        launch_scan_cfg<REV, LO, 4, 8>(grid, wsB, elemsB, wsA, elemsA, loB, loA, NB, s);
     else if (NB <= 128)
-        launch_scan_cfg<REV, 16, 8>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+        launch_scan_cfg<REV, LO, 16, 8>(grid, wsB, elemsB, wsA, elemsA, loB, loA, NB, s);
     else  // super-chunks of 256 blocks (32 loads per thread would not fit the registers)
-        launch_scan_cfg<REV, 16, 16>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+        launch_scan_cfg<REV, LO, 16, 16>(grid, wsB, elemsB, wsA, elemsA, loB, loA, NB, s);
 }
 
 hipError_t launch_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB, int Z, int rev,
-                             hipStream_t s)
+                             hipStream_t s, float *loB, float *loA)
 {
     const dim3 grid((unsigned)((elemsB + SCAN_COLS - 1) / SCAN_COLS + (elemsA + SCAN_COLS - 1) / SCAN_COLS),
                     (unsigned)Z);
-    if (rev)
-        launch_scan_dir<true>(grid, wsB, elemsB, wsA, elemsA, NB, s);
-    else
-        launch_scan_dir<false>(grid, wsB, elemsB, wsA, elemsA, NB, s);
+    if ((loB == nullptr) != (loA == nullptr))
+        return hipErrorInvalidValue;
+    if (loB) {
+        if (rev)
+            launch_scan_dir<true, true>(grid, wsB, elemsB, wsA, elemsA, loB, loA, NB, s);
+        else
+            launch_scan_dir<false, true>(grid, wsB, elemsB, wsA, elemsA, loB, loA, NB, s);
+    } else if (rev) {
+        launch_scan_dir<true, false>(grid, wsB, elemsB, wsA, elemsA, nullptr, nullptr, NB, s);
+    } else {
+        launch_scan_dir<false, false>(grid, wsB, elemsB, wsA, elemsA, nullptr, nullptr, NB, s);
+    }
     return hipGetLastError();
 }
 

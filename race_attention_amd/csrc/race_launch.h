@@ -38,9 +38,10 @@ constexpr int OP_C = 16, OP_NW_TOTALS = 4;
 constexpr int op_nw_main(int DP) { return DP >= 64 ? 8 : 4; }
 
 // race_common.hip
-// scans wsB [Z][NB+1][elemsB] and wsA [Z][NB+1][elemsA] over the block axis in one launch
+// scans wsB [Z][NB+1][elemsB] and wsA [Z][NB+1][elemsA] over the block axis in one launch; with
+// loB / loA (both or neither) every value is the double-float hi (ws) + lo (lo array, same layout)
 hipError_t launch_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB, int Z, int rev,
-                             hipStream_t s);
+                             hipStream_t s, float *loB = nullptr, float *loA = nullptr);
 // out[i] (view, f32 or bf16) = sum_{st < n_st} part[st * tile + i] over a [B][H][T][D] box
 hipError_t launch_reduce_partials(const float *part, int n_st, int64_t tile, const OutView &out,
                                   int B, int H, int T, int D, hipStream_t s);

@@ -40,6 +40,8 @@ struct ScanParams {
     // workspaces: block states [Z][NB+1][S_pad][DPw] and [Z][NB+1][S_pad]
     float *wsB, *wsA;    // forward: prefix (A, B) at each block start; slot NB = final
     float *ws2B, *ws2A;  // backward: suffix sums (of W^T go, gA) from each block's start
+    // generic backward kernels: low parts of the same suffix sums (ws2 + ws3 = a double-float)
+    float *ws3B, *ws3A;
     // op mode only: 1 = unnormalised causal linear attention, W = pQ (no 1/(A+eps), gA = 0)
     int linear;
 };

@@ -59,6 +59,51 @@ RACE_DEV void zero_lds(T *p, int n, int tid, int nth)
         p[i] = (T)0.0f;
 }
 
+// The backward carries its suffix states (sum of W^T go, sum of gA) across a block as
+// double-floats: the backward totals kernel adds each sub-chunk's contribution to an fp64 block
+// total, and the main kernel walks the block forward from the inclusive block suffix and takes
+// away bitwise the same sub-chunk contributions in fp64. Those cancel exactly, so the suffix after
+// a sub-chunk keeps the accuracy of its own terms even when the block's first tokens (tiny A at a
+// sequence start, W = pQ/(A+eps) up to ~1e4 with sharp probabilities) dominate the block total.
+// Both kernels form each contribution with the helpers below, which keep every product rounded on
+// its own (no contraction into a fused multiply-add that the other kernel might not form).
+//
+// acc += gA = -(gW / (A + eps)) W, term by term
+RACE_DEV void ga_accum(f32x4 &acc, const f32x4 &gw, const f32x4 &inva, const f32x4 &w)
+{
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float gpq = gw[e] * inva[e];
+        acc[e] = acc[e] - gpq * w[e];
+    }
+}
+
+// Sum over a sub-chunk's token rows of one 16-column group (accumulator tiles j*MTC .. +MTC-1):
+// per lane over its rows, then across the four lane groups; every lane of a column gets the same
+// value.
+template <int MTC>
+RACE_DEV float col_total(const f32x4 *acc, int j)
+{
+    float v = 0.0f;
+#pragma unroll
+    for (int tm = 0; tm < MTC; ++tm)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v += acc[j * MTC + tm][e];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Split an fp64 value into the (hi, lo) fp32 pair of the backward workspaces.
+RACE_DEV void put_hilo(float *hi, float *lo, double x)
+{
+    const float h = (float)x;
+    *hi = h;
+    *lo = (float)(x - (double)h);
+}
+
 // ============================================================================ forward totals
 template <class E, int MODE, int ST, int DP, int C, int NW>
 __global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
@@ -393,14 +438,17 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
     zero_lds(&sF[0][0], C * LDF, c.tid, NTH);
 
     const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
-    f32x4 accS[CF::TPW_SD], accDS[CF::TPW_SD];
+    f32x4 accS[CF::TPW_SD];
+    double dS64[CF::TPW_SD][4];  // block total of W^T go (fp64 sum of the sub-chunk totals)
     {
         const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
 #pragma unroll
         for (int i = 0; i < CF::TPW_SD; ++i) {
             const int t = c.wave + i * NW;
             accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            accDS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                dS64[i][e] = 0.0;
             if (t < CF::NTS * CF::NTD) {
                 const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
                 const int r = acc_row(m0, c.lane), col = acc_col(n0, c.lane);
@@ -414,13 +462,14 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
         for (int s = c.tid; s < ST; s += NTH)
             sA0[s] = wA[s];
     }
-    float dGA[NCG > 0 ? NCG : 1];
+    double dGA[NCG > 0 ? NCG : 1];  // block column totals of gA (fp64 sum of sub-chunk totals)
 #pragma unroll
     for (int j = 0; j < NCG; ++j)
-        dGA[j] = 0.0f;
+        dGA[j] = 0.0;
     __syncthreads();
 
-    f32x4 accA[CF::TPW_CS], accW[CF::TPW_CS], accG[CF::TPW_CS];
+    f32x4 accA[CF::TPW_CS], accW[CF::TPW_CS], accG[CF::TPW_CS], accGA[CF::TPW_CS];
+    f32x4 accT[CF::TPW_SD];
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     // op mode: this sub-chunk's pK, values, pQ and output gradient wait in registers, fetched one
     // sub-chunk ahead
@@ -483,6 +532,12 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
                 sA0[tn * 16 + (c.lane & 15)] = carry[i];
         }
 
+#pragma unroll
+        for (int i = 0; i < CF::TPW_CS; ++i)
+            accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i)
+            accT[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         const int G = CF::QKV ? P.G : 1;
         for (int g = 0; g < G; ++g) {
             const int hq = c.hk * P.G + g;
@@ -537,23 +592,19 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
                 }
             }
             __syncthreads();
-            // gW += Mg pK ; gpQ = gW/(A+eps) ; gA = -gpQ W ; dS += W^T go
+            // gW += Mg pK ; gpQ = gW/(A+eps) ; gA = -gpQ W ; this sub-chunk's W^T go
 #pragma unroll
             for (int i = 0; i < CF::TPW_CS; ++i) {
                 const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
                 if (tn < CF::NTS) {
                     mma_tile<E, C>(accG[i], &sMg[0][0], LDC, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
+                    if (!P.linear)
+                        ga_accum(accGA[i], accG[i], accA[i], accW[i]);
                     f32x4 gpq;
-                    float colsum = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
+                    for (int e = 0; e < 4; ++e)
                         gpq[e] = accG[i][e] * accA[i][e];
-                        colsum -= gpq[e] * accW[i][e];
-                    }
-                    if (P.linear)
-                        colsum = 0.0f;
                     accG[i] = gpq;
-                    dGA[i / MTC] += colsum;  // reduced across lanes at the end
                     if constexpr (!CF::QKV)
                         store_probs_tile(P.gpQ + (int64_t)c.z * P.T * P.S, P.S, c.s0, c.S_here, t0, nv,
                                          tm * 16, tn * 16, c.lane, gpq);
@@ -563,7 +614,7 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
             for (int i = 0; i < CF::TPW_SD; ++i) {
                 const int t = c.wave + i * NW;
                 if (t < CF::NTS * CF::NTD)
-                    mma_tile<E, C>(accDS[i], &sWt[0][0], LDC, &sGOt[0][0], LDC, (t / CF::NTD) * 16,
+                    mma_tile<E, C>(accT[i], &sWt[0][0], LDC, &sGOt[0][0], LDC, (t / CF::NTD) * 16,
                                    (t % CF::NTD) * 16, c.lane);
             }
             if constexpr (CF::QKV) {
@@ -606,6 +657,15 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
             }
             __syncthreads();
         }
+        // this sub-chunk's totals into the fp64 block totals
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                dS64[i][e] += (double)accT[i][e];
+#pragma unroll
+        for (int j = 0; j < NCG; ++j)
+            dGA[j] += (double)col_total<MTC>(accGA, j);
         // St += pK^T V
 #pragma unroll
         for (int i = 0; i < CF::TPW_SD; ++i) {
@@ -619,27 +679,26 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
         __syncthreads();
     }
 
-    // block totals of W^T go and gA
-    float *wB = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+    // block totals of W^T go and gA as double-floats (ws2 = hi, ws3 = lo)
+    const int64_t offB = (slot * P.S_pad + c.s0) * P.DPw;
 #pragma unroll
     for (int i = 0; i < CF::TPW_SD; ++i) {
         const int t = c.wave + i * NW;
         if (t < CF::NTS * CF::NTD) {
             const int r = acc_row((t / CF::NTD) * 16, c.lane), col = acc_col((t % CF::NTD) * 16, c.lane);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                wB[(int64_t)(r + e) * P.DPw + col] = accDS[i][e];
+            for (int e = 0; e < 4; ++e) {
+                const int64_t o = offB + (int64_t)(r + e) * P.DPw + col;
+                put_hilo(P.ws2B + o, P.ws3B + o, dS64[i][e]);
+            }
         }
     }
-    float *wA = P.ws2A + slot * P.S_pad + c.s0;
+    const int64_t offA = slot * P.S_pad + c.s0;
 #pragma unroll
     for (int j = 0; j < NCG; ++j) {
-        float v = dGA[j];
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
         const int tn = c.wave + j * NW;
         if (tn < CF::NTS && c.lane < 16)
-            wA[tn * 16 + c.lane] = v;
+            put_hilo(P.ws2A + offA + tn * 16 + c.lane, P.ws3A + offA + tn * 16 + c.lane, dGA[j]);
     }
 }
 
@@ -648,10 +707,10 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
 // exactly as in the forward pass (small early A values are never rebuilt by
 // subtraction, where 1/A^2 in gA would amplify the rounding). The reverse states
 // come from the inclusive block suffixes of the backward workspace and shrink by
-// each sub-chunk's own contribution:
+// each sub-chunk's own contribution, in fp64 and bitwise the contributions the
+// backward totals kernel added (see ga_accum), so the subtraction cancels exactly:
 //   dS_end(c)   = dS_start(c) - W_c^T go_c
 //   gAhat_end(c)= gAhat_start(c) - colsum(gA_c)
-// whose rounding is absolute and is not divided by A.
 template <class E, int MODE, int ST, int DP, int C, int NW>
 __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
 {
@@ -680,7 +739,7 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
     __shared__ __align__(16) T sMv[C][LDC];
     __shared__ __align__(16) T sMp[C][LDC];
     __shared__ float sA0[ST];
-    __shared__ float sGAe[ST];
+    __shared__ double sGAe[ST];  // suffix of gA after the current sub-chunk (fp64)
     static_assert(!CF::QKV || sizeof(T) * XR * LDG <= sizeof(float) * XR * LDU, "sGU alias");
     T *sGU = reinterpret_cast<T *>(&sUq[0][0]);
 
@@ -692,38 +751,43 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
     zero_lds(&sPKt[0][0], ST * LDC, c.tid, NTH);
     zero_lds(&sF[0][0], C * LDF, c.tid, NTH);
 
-    // forward state at the block start; reverse suffix from the block start (inclusive)
+    // forward state at the block start; reverse suffix from the block start (inclusive), as the
+    // double-float the backward totals kernel and the block scan carried
     const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
     f32x4 accS[CF::TPW_SD], accDS[CF::TPW_SD];
+    double dS64[CF::TPW_SD][4];
     {
-        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
-        const float *wB2 = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+        const int64_t offB = (slot * P.S_pad + c.s0) * P.DPw;
+        const float *wB = P.wsB + offB;
 #pragma unroll
         for (int i = 0; i < CF::TPW_SD; ++i) {
             const int t = c.wave + i * NW;
             accS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
             accDS[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                dS64[i][e] = 0.0;
             if (t < CF::NTS * CF::NTD) {
                 const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
                 const int r = acc_row(m0, c.lane), col = acc_col(n0, c.lane);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    accS[i][e] = wB[(int64_t)(r + e) * P.DPw + col];
-                    accDS[i][e] = wB2[(int64_t)(r + e) * P.DPw + col];
+                    const int64_t o = (int64_t)(r + e) * P.DPw + col;
+                    accS[i][e] = wB[o];
+                    dS64[i][e] = (double)P.ws2B[offB + o] + (double)P.ws3B[offB + o];
                 }
             }
         }
-        const float *wA = P.wsA + slot * P.S_pad + c.s0;
-        const float *wA2 = P.ws2A + slot * P.S_pad + c.s0;
+        const int64_t offA = slot * P.S_pad + c.s0;
         for (int s = c.tid; s < ST; s += NTH) {
-            sA0[s] = wA[s];
-            sGAe[s] = wA2[s];
+            sA0[s] = P.wsA[offA + s];
+            sGAe[s] = (double)P.ws2A[offA + s] + (double)P.ws3A[offA + s];
         }
     }
     __syncthreads();
 
     f32x4 accA[CF::TPW_CS], accW[CF::TPW_CS], accG[CF::TPW_CS], accGA[CF::TPW_CS], accPK[CF::TPW_CS];
-    f32x4 accV[CF::TPW_CD];
+    f32x4 accV[CF::TPW_CD], accT[CF::TPW_SD];
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     // op mode: this sub-chunk's pK, values, pQ and output gradient wait in registers, fetched one
     // sub-chunk ahead
@@ -794,6 +858,9 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
 #pragma unroll
         for (int i = 0; i < CF::TPW_CD; ++i)
             accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < CF::TPW_SD; ++i)
+            accT[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < CF::TPW_CS; ++i) {
@@ -874,15 +941,14 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
                     st_rm(&sMp[0][0], LDC, tm * 16, tn * 16, c.lane, acc);
                 }
             }
-            // gW += Mg pK ; gA += -gW W/(A+eps) ; gpK += triu(V go^T) W ; dS -= W^T go
+            // gW += Mg pK ; gA += -gW W/(A+eps) ; gpK += triu(V go^T) W ; this sub-chunk's W^T go
 #pragma unroll
             for (int i = 0; i < CF::TPW_CS; ++i) {
                 const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
                 if (tn < CF::NTS) {
                     mma_tile<E, C>(accG[i], &sMg[0][0], LDC, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        accGA[i][e] -= P.linear ? 0.0f : accG[i][e] * accA[i][e] * accW[i][e];
+                    if (!P.linear)
+                        ga_accum(accGA[i], accG[i], accA[i], accW[i]);
                     mma_tile<E, C>(accPK[i], &sMv[0][0], LDC, &sWt[0][0], LDC, tm * 16, tn * 16, c.lane);
                 }
             }
@@ -890,8 +956,8 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
             for (int i = 0; i < CF::TPW_SD; ++i) {
                 const int t = c.wave + i * NW;
                 if (t < CF::NTS * CF::NTD)
-                    mma_tile<E, C, true>(accDS[i], &sWt[0][0], LDC, &sGOt[0][0], LDC, (t / CF::NTD) * 16,
-                                         (t % CF::NTD) * 16, c.lane);
+                    mma_tile<E, C>(accT[i], &sWt[0][0], LDC, &sGOt[0][0], LDC, (t / CF::NTD) * 16,
+                                   (t % CF::NTD) * 16, c.lane);
             }
             __syncthreads();
             // gv += Mp go
@@ -906,16 +972,29 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
                 __syncthreads();
         }
 
-        // dS now holds the suffix after this sub-chunk: copies for V dS^T and pK dS;
-        // gA of this sub-chunk to sF for its suffix sums
+        // the suffixes after this sub-chunk: dS (fp64, less this sub-chunk's W^T go), copies for
+        // V dS^T and pK dS; gAhat_end (fp64, less this sub-chunk's column totals of gA); gA of this
+        // sub-chunk to sF for its within-sub-chunk suffix sums
 #pragma unroll
         for (int i = 0; i < CF::TPW_SD; ++i) {
             const int t = c.wave + i * NW;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dS64[i][e] -= (double)accT[i][e];
+                accDS[i][e] = (float)dS64[i][e];
+            }
             if (t < CF::NTS * CF::NTD) {
                 const int m0 = (t / CF::NTD) * 16, n0 = (t % CF::NTD) * 16;
                 st_rm(&sdS[0][0], LDX, m0, n0, c.lane, accDS[i]);
                 st_cm(&sdSt[0][0], LDS_, m0, n0, c.lane, accDS[i]);
             }
+        }
+#pragma unroll
+        for (int j = 0; j < CF::TPW_CS / MTC; ++j) {
+            const float tot = col_total<MTC>(accGA, j);
+            const int tn = c.wave + j * NW;
+            if (tn < CF::NTS && c.lane < 16)
+                sGAe[tn * 16 + c.lane] -= (double)tot;
         }
 #pragma unroll
         for (int i = 0; i < CF::TPW_CS; ++i) {
@@ -924,18 +1003,13 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
                 st_rm(&sF[0][0], LDF, tm * 16, tn * 16, c.lane, accGA[i]);
         }
         __syncthreads();
-        // gAhat_t = gAhat_end + sum_{tau>=t} gA_tau with gAhat_end = gAhat_start - sum_c gA
+        // gAhat_t = gAhat_end + sum_{tau>=t, tau in this sub-chunk} gA_tau
         for (int s = c.tid; s < ST; s += NTH) {
-            float tot = 0.0f;
-            for (int t = 0; t < C; ++t)
-                tot += sF[t][s];
-            float run = sGAe[s] - tot;
-            const float end = run;
+            float run = (float)sGAe[s];
             for (int t = C - 1; t >= 0; --t) {
                 run += sF[t][s];
                 sF[t][s] = run;
             }
-            sGAe[s] = end;
         }
         // gpK += V dS^T ; gv += pK dS  (dS = suffix after this sub-chunk)
 #pragma unroll

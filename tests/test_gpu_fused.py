@@ -182,7 +182,8 @@ def test_soft_hash_probs_golden(dev):
 @pytest.mark.parametrize("H,T,D,L,Kb", [(4, 256, 64, 2, 2), (8, 1024, 128, 3, 3), (4, 2048, 96, 4, 4),
                                         (2, 512, 64, 8, 4)])
 def test_module_e2e_fp32(dev, H, T, D, L, Kb):
-    """scaling/test_kernels.py:107-129: RaceCausalCuda (fp32) against the fp64 layer."""
+    """scaling/test_kernels.py:107-129: RaceCausalCuda (fp32) against the fp64 layer, at the north
+    star's fp32 bar 1e-4 for the gradients."""
     from race_attention_amd import RaceCausalCuda
     torch.manual_seed(H + T)
     Q, K, V = (torch.randn(1, H, T, D) for _ in range(3))
@@ -194,9 +195,9 @@ def test_module_e2e_fp32(dev, H, T, D, L, Kb):
     ref, dq, dk, dv = oracle_layer(Q, K, V, m.planes_T.cpu(), L, Kb, math.sqrt(D), EPS, go)
     assert oc.dtype == torch.float32
     check("e2e out", oc, ref, 2e-5)
-    check("e2e gradQ", qc.grad, dq, 2e-3)
-    check("e2e gradK", kc.grad, dk, 2e-3)
-    check("e2e gradV", vc.grad, dv, 2e-3)
+    check("e2e gradQ", qc.grad, dq, 1e-4)  # north-star fp32 bar (the reference's e2e test: 2e-3)
+    check("e2e gradK", kc.grad, dk, 1e-4)
+    check("e2e gradV", vc.grad, dv, 1e-4)
 
 
 def test_module_bf16_and_ensemble(dev):

@@ -1,11 +1,12 @@
 """Op-level causal RACE on the GPU (RaceCausalFn / race_fused_fwd / race_backward)
-against the fp64 oracle. Sweeps and tolerances follow the reference's
-scaling/test_kernels.py:132-158 (fwd 2e-5, grads 3e-3, 5e-3 in the T sweep),
-extended to S = 128 and 256 (K = 4)."""
+against the fp64 oracle. Sweeps follow the reference's scaling/test_kernels.py:132-158,
+extended to S = 128 and 256 (K = 4). Tolerances: the reference's forward bar 2e-5 and the
+north star's fp32 bar 1e-4 for every gradient (the reference's own sweep allows 3e-3 and 5e-3),
+with its tight absolute floor for the genuinely ~0 gradProbsK of a single token."""
 import pytest
 import torch
 
-from race_ref import check, make_probs, oracle_op
+from race_ref import check, fp32_formula_floor, make_probs, oracle_op
 
 pytestmark = pytest.mark.gpu
 
@@ -13,7 +14,7 @@ PARAM_SETS = [(2, 2), (3, 3), (4, 4), (8, 4)]  # (L, K) -> S = 8, 24, 64, 128
 EPS = 1e-6
 
 
-def run_case(dev, N, T, L, Kb, D, seed, dist="softmax", fwd_tol=2e-5, grad_tol=3e-3, blocks=(0, 64, 1024)):
+def run_case(dev, N, T, L, Kb, D, seed, dist="softmax", fwd_tol=2e-5, grad_tol=1e-4, blocks=(0, 64, 1024)):
     from race_attention_amd import RaceCausalFn, race_fused_fwd
     print(f"case N={N} T={T} L={L} K={Kb} D={D} dist={dist}", flush=True)
     R = 1 << Kb
@@ -29,9 +30,14 @@ def run_case(dev, N, T, L, Kb, D, seed, dist="softmax", fwd_tol=2e-5, grad_tol=3
     pkx, pqx, vx = (x.clone().requires_grad_(True) for x in (pkc, pqc, vc))
     out = RaceCausalFn.apply(pkx, pqx, vx, EPS)
     (out * go.float().to(dev)).sum().backward()
-    check("gradProbsK", pkx.grad, gpk_t, grad_tol)
-    check("gradProbsQ", pqx.grad, gpq_t, grad_tol)
-    check("gradV", vx.grad, gv_t, grad_tol)
+    # For the first tokens of a sequence gradProbsK is a difference of two O(1/pK) terms that
+    # cancel to O(eps/pK^2): there the bar is twice the fp32 floor of the reference formula itself
+    # (fp32 torch autograd of race_prefix_ref), never looser than grad_tol elsewhere.
+    floors = fp32_formula_floor(pk, pq, v, go, EPS, (gpk_t, gpq_t, gv_t)) if T <= 256 else [0.0] * 3
+    errs = [check(n, g, r, max(grad_tol, 2.0 * f))
+            for n, g, r, f in zip(("gradProbsK", "gradProbsQ", "gradV"), (pkx.grad, pqx.grad, vx.grad),
+                                  (gpk_t, gpq_t, gv_t), floors)]
+    print("relerr gpK %.2e gpQ %.2e gV %.2e (fp32 formula floor %.1e %.1e %.1e)" % (*errs, *floors), flush=True)
 
 
 @pytest.mark.parametrize("L,Kb", PARAM_SETS)
@@ -44,12 +50,12 @@ def test_shape_sweep(dev, L, Kb, N, D):
 @pytest.mark.parametrize("L,Kb", PARAM_SETS)
 @pytest.mark.parametrize("T", [1, 2, 7, 64, 256, 4096, 16384])
 def test_t_sweep(dev, L, Kb, T):
-    run_case(dev, 2, T, L, Kb, 64, seed=T, grad_tol=5e-3)
+    run_case(dev, 2, T, L, Kb, 64, seed=T)
 
 
 @pytest.mark.parametrize("L,Kb", [(4, 4)])
 def test_t_65536(dev, L, Kb):
-    run_case(dev, 2, 65536, L, Kb, 64, seed=65536, grad_tol=5e-3, blocks=(0,))
+    run_case(dev, 2, 65536, L, Kb, 64, seed=65536, blocks=(0,))
 
 
 @pytest.mark.parametrize("L,Kb", PARAM_SETS)
@@ -63,6 +69,14 @@ def test_raw_distribution(dev, L, Kb):
     run_case(dev, 2, 1024, L, Kb, 64, seed=7, dist="raw")
 
 
+@pytest.mark.parametrize("L,Kb,T", [(8, 4, 4096), (2, 2, 3000)])
+def test_sharp_distribution(dev, L, Kb, T):
+    """Sharp probabilities (softmax of 4 x N(0,1) logits): W = pQ/(A+eps) spans ~10 orders of
+    magnitude over a sequence's first block, so the backward's carried suffix states must not
+    lose the later tokens' terms next to the first tokens' (1e-4 bar on every gradient)."""
+    run_case(dev, 2, T, L, Kb, 64, seed=T + L, dist="sharp", blocks=(0, 256))
+
+
 def test_s256_tiled(dev):
     """S = 256 > the largest bucket tile: exercises the partial-sum reduction."""
     run_case(dev, 2, 700, 16, 4, 64, seed=11)
@@ -70,7 +84,7 @@ def test_s256_tiled(dev):
 
 def test_many_blocks(dev):
     """More blocks than one pass of the block-state scan covers (625 and 834 blocks, ragged)."""
-    run_case(dev, 1, 40000, 4, 4, 64, seed=40000, grad_tol=5e-3, blocks=(0, 48))
+    run_case(dev, 1, 40000, 4, 4, 64, seed=40000, blocks=(0, 48))
 
 
 def test_backward_from_kept_state(dev):
