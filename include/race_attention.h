@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RACE_ABI_VERSION 1
+#define RACE_ABI_VERSION 2  /* 2: kept-state entry points take the state's size */
 
 typedef enum {
     RACE_OK = 0,
@@ -96,17 +96,20 @@ int race_op_bwd(const float *pK, const float *pQ, const float *V, const float *g
 /* race_op_fwd that also leaves its scanned forward block states in `state`
  * (race_op_state_bytes bytes, 256-byte aligned), and race_op_bwd that reads them from there
  * instead of recomputing them (same pK, V, shape and block as the forward; the backward only
- * reads the state, so it serves any number of backward calls). No counterpart in the reference,
- * whose backward (kernels/gpu/backward_kernels.cu:174-215) recomputes the forward block states:
- * for autograd callers that keep the forward's state until the backward. */
+ * reads the state, so it serves any number of backward calls). `state_bytes` is the buffer's
+ * size; both calls fail with RACE_ERR_WORKSPACE when it is below race_op_state_bytes of their
+ * own (N, T, S, D, block), so a buffer sized for another shape or block is never overrun.
+ * No counterpart in the reference, whose backward (kernels/gpu/backward_kernels.cu:174-215)
+ * recomputes the forward block states: for autograd callers that keep the forward's state
+ * until the backward. */
 size_t race_op_state_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t block);
 int race_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N,
                      int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
-                     size_t workspace_bytes, float *state, race_stream stream);
+                     size_t workspace_bytes, float *state, size_t state_bytes, race_stream stream);
 int race_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK,
                      float *gpQ, float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps,
                      int64_t block, void *workspace, size_t workspace_bytes, const float *state,
-                     race_stream stream);
+                     size_t state_bytes, race_stream stream);
 
 /* ---------------------------------------------------------------- causal linear attention */
 /* Katharopoulos causal linear attention, the reference's comparison kernel
@@ -123,17 +126,19 @@ int race_causal_dot_backward(const float *Q, const float *K, const float *V, con
                              int64_t M, int64_t block, void *workspace, size_t workspace_bytes,
                              race_stream stream);
 /* The same pair keeping the forward's block states in `state` (race_op_state_bytes(N, L, E, M,
- * block) bytes, 256-byte aligned) for a backward that reads them instead of recomputing them;
- * bitwise the same results. No counterpart in the reference (linear_pref.cpp:138-213 recomputes
- * the running sums in its backward): for autograd callers that keep the state. */
+ * block) bytes, 256-byte aligned, its size in `state_bytes`, checked as for race_op_fwd_keep)
+ * for a backward that reads them instead of recomputing them; bitwise the same results. No
+ * counterpart in the reference (linear_pref.cpp:138-213 recomputes the running sums in its
+ * backward): for autograd callers that keep the state. */
 int race_causal_dot_product_keep(const float *Q, const float *K, const float *V, float *out,
                                  int64_t N, int64_t L, int64_t E, int64_t M, int64_t block,
                                  void *workspace, size_t workspace_bytes, float *state,
-                                 race_stream stream);
+                                 size_t state_bytes, race_stream stream);
 int race_causal_dot_backward_kept(const float *Q, const float *K, const float *V, const float *gO,
                                   float *gQ, float *gK, float *gV, int64_t N, int64_t L, int64_t E,
                                   int64_t M, int64_t block, void *workspace,
-                                  size_t workspace_bytes, const float *state, race_stream stream);
+                                  size_t workspace_bytes, const float *state, size_t state_bytes,
+                                  race_stream stream);
 
 /* ---------------------------------------------------------------- non-causal op */
 /* Non-causal RACE of BatchedACE (scaling/benchmark_time.py:139-160), replacing its
@@ -150,17 +155,19 @@ int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float
                    int64_t D, float eps, int64_t block, void *workspace,
                    size_t workspace_bytes, race_stream stream);
 /* The same pair keeping the forward's whole-sequence totals (sum pK, sum pK v) in `state`
- * (race_op_state_bytes bytes, 256-byte aligned) for a backward that reads them instead of
- * recomputing them; bitwise the same results. No counterpart in the reference, whose
- * BatchedACE backward (torch autograd, scaling/benchmark_time.py:139-160) keeps the totals as
- * saved tensors: for autograd callers that keep the state until the backward. */
+ * (race_op_state_bytes bytes, 256-byte aligned, its size in `state_bytes`, checked as for
+ * race_op_fwd_keep) for a backward that reads them instead of recomputing them; bitwise the
+ * same results. No counterpart in the reference, whose BatchedACE backward (torch autograd,
+ * scaling/benchmark_time.py:139-160) keeps the totals as saved tensors: for autograd callers
+ * that keep the state until the backward. */
 int race_nc_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N,
                         int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
-                        size_t workspace_bytes, float *state, race_stream stream);
+                        size_t workspace_bytes, float *state, size_t state_bytes, race_stream stream);
 int race_nc_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO,
                         float *gpK, float *gpQ, float *gV, int64_t N, int64_t T, int64_t S,
                         int64_t D, float eps, int64_t block, void *workspace,
-                        size_t workspace_bytes, const float *state, race_stream stream);
+                        size_t workspace_bytes, const float *state, size_t state_bytes,
+                        race_stream stream);
 
 /* ---------------------------------------------------------------- fused layer */
 typedef struct {

@@ -58,17 +58,17 @@ SIGNATURES = {
     "race_nc_op_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float,
                                       _i64, _vp, ctypes.c_size_t, _vp]),
     "race_nc_op_fwd_keep": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
-                                           ctypes.c_size_t, _vp, _vp]),
+                                           ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_nc_op_bwd_kept": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
-                                           ctypes.c_float, _i64, _vp, ctypes.c_size_t, _vp, _vp]),
+                                           ctypes.c_float, _i64, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_causal_dot_product": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp,
                                                ctypes.c_size_t, _vp]),
     "race_causal_dot_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                                 _vp, ctypes.c_size_t, _vp]),
     "race_causal_dot_product_keep": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp,
-                                                    ctypes.c_size_t, _vp, _vp]),
+                                                    ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_causal_dot_backward_kept": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
-                                                     _i64, _vp, ctypes.c_size_t, _vp, _vp]),
+                                                     _i64, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_op_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, ctypes.c_int]),
     "race_op_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
                                    ctypes.c_size_t, _vp]),
@@ -76,9 +76,9 @@ SIGNATURES = {
                                    _i64, _vp, ctypes.c_size_t, _vp]),
     "race_op_state_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
     "race_op_fwd_keep": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
-                                        ctypes.c_size_t, _vp, _vp]),
+                                        ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_op_bwd_kept": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float,
-                                        _i64, _vp, ctypes.c_size_t, _vp, _vp]),
+                                        _i64, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_qkv_state_bytes": (ctypes.c_size_t, [ctypes.POINTER(QKVShape)]),
     "race_qkv_scratch_bytes": (ctypes.c_size_t, [ctypes.POINTER(QKVShape), ctypes.c_int]),
     "race_qkv_fwd": (ctypes.c_int, [ctypes.POINTER(QKVShape), Tensor4, Tensor4, Tensor4, _vp, Tensor4,

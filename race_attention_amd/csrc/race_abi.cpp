@@ -242,10 +242,10 @@ struct ProfScope {
 };
 
 hipError_t prof_block_scan(float *wsB, int64_t elemsB, float *wsA, int64_t elemsA, int NB, int Z, int rev,
-                           hipStream_t s)
+                           hipStream_t s, float *loB = nullptr, float *loA = nullptr)
 {
     ProfScope ps(RACE_PROF_BLOCK_SCAN, s);
-    return launch_block_scan(wsB, elemsB, wsA, elemsA, NB, Z, rev, s);
+    return launch_block_scan(wsB, elemsB, wsA, elemsA, NB, Z, rev, s, loB, loA);
 }
 hipError_t prof_reduce(const float *part, int n_st, int64_t tile, const OutView &out, int B, int H, int T, int D,
                        hipStream_t s)
@@ -361,8 +361,8 @@ int race_soft_hash_bwd_scale(const race_hash_shape *sh, race_tensor x, int x_dty
 static size_t op_bytes(const Geo &g, int64_t T, int64_t D, int backward)
 {
     size_t b = align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
-    if (backward)
-        b += align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+    if (backward)  // the backward suffix states as double-floats (hi and lo arrays)
+        b += 2 * (align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4));
     if (g.n_st > 1)
         b += align256((size_t)g.n_st * g.Z * T * D * 4);
     return b;
@@ -415,6 +415,22 @@ static int op_check(const float *pK, const float *pQ, const float *V, float eps,
         return fail(RACE_ERR_INVALID, "%s: eps must be >= 0", who);
     if (!ws || ws_bytes < need)
         return fail(RACE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", who, need, ws ? ws_bytes : 0);
+    return RACE_OK;
+}
+
+// A kept-state buffer: present, 256-byte aligned and at least race_op_state_bytes of this call's
+// own geometry (a buffer sized for another shape or block would be overrun by the kernels).
+static int kept_state_check(const void *state, size_t state_bytes, int64_t N, int64_t T, int64_t S, int64_t D,
+                            int64_t block, const char *who)
+{
+    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
+        return fail(RACE_ERR_INVALID, "%s: state must be a 256-byte aligned buffer", who);
+    Geo g;
+    RACE_TRY(op_geometry(N, T, S, D, block, g));
+    const size_t need = align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+    if (state_bytes < need)
+        return fail(RACE_ERR_WORKSPACE, "%s: state of %zu bytes needed for this shape and block, got %zu", who, need,
+                    state_bytes);
     return RACE_OK;
 }
 
@@ -487,6 +503,8 @@ static int op_bwd_impl(const float *pK, const float *pQ, const float *V, const f
     P.wsA = cv.take(g.state_elems_A);
     P.ws2B = cv.take(g.state_elems_B);
     P.ws2A = cv.take(g.state_elems_A);
+    P.ws3B = cv.take(g.state_elems_B);
+    P.ws3A = cv.take(g.state_elems_A);
     float *part = g.n_st > 1 ? cv.take((size_t)g.n_st * N * T * D) : nullptr;
     P.dv = part ? OutView{part, T * D, 0, D, N * T * D, 1} : OutView{gV, T * D, 0, D, 0, 1};
     const hipStream_t s = hs(stream);
@@ -498,7 +516,9 @@ static int op_bwd_impl(const float *pK, const float *pQ, const float *V, const f
                            "block scan"));
     }
     RACE_TRY(run_scan_op(K_BWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s,
+                                       P.ws3B, P.ws3A),
+                       "block scan"));
     RACE_TRY(run_scan_op(K_BWD_MAIN, g, P, s));
     if (part)
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, N * T * D, OutView{gV, T * D, 0, D, 0, 1},
@@ -516,20 +536,19 @@ size_t race_op_state_bytes(int64_t N, int64_t T, int64_t S, int64_t D, int64_t b
 
 int race_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
                      int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
-                     float *state, race_stream stream)
+                     float *state, size_t state_bytes, race_stream stream)
 {
-    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
-        return fail(RACE_ERR_INVALID, "race_op_fwd_keep: state must be a 256-byte aligned buffer");
+    RACE_TRY(kept_state_check(state, state_bytes, N, T, S, D, block, "race_op_fwd_keep"));
     return op_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, 0,
                        "race_op_fwd_keep", state);
 }
 
 int race_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
                      float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
-                     void *workspace, size_t workspace_bytes, const float *state, race_stream stream)
+                     void *workspace, size_t workspace_bytes, const float *state, size_t state_bytes,
+                     race_stream stream)
 {
-    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
-        return fail(RACE_ERR_INVALID, "race_op_bwd_kept: state must be a 256-byte aligned buffer");
+    RACE_TRY(kept_state_check(state, state_bytes, N, T, S, D, block, "race_op_bwd_kept"));
     return op_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream, 0,
                        "race_op_bwd_kept", state);
 }
@@ -562,20 +581,19 @@ int race_causal_dot_backward(const float *Q, const float *K, const float *V, con
 
 int race_causal_dot_product_keep(const float *Q, const float *K, const float *V, float *out, int64_t N, int64_t L,
                                  int64_t E, int64_t M, int64_t block, void *workspace, size_t workspace_bytes,
-                                 float *state, race_stream stream)
+                                 float *state, size_t state_bytes, race_stream stream)
 {
-    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
-        return fail(RACE_ERR_INVALID, "race_causal_dot_product_keep: state must be a 256-byte aligned buffer");
+    RACE_TRY(kept_state_check(state, state_bytes, N, L, E, M, block, "race_causal_dot_product_keep"));
     return op_fwd_impl(K, Q, V, out, N, L, E, M, 0.0f, block, workspace, workspace_bytes, stream, 1,
                        "race_causal_dot_product_keep", state);
 }
 
 int race_causal_dot_backward_kept(const float *Q, const float *K, const float *V, const float *gO, float *gQ,
                                   float *gK, float *gV, int64_t N, int64_t L, int64_t E, int64_t M, int64_t block,
-                                  void *workspace, size_t workspace_bytes, const float *state, race_stream stream)
+                                  void *workspace, size_t workspace_bytes, const float *state, size_t state_bytes,
+                                  race_stream stream)
 {
-    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
-        return fail(RACE_ERR_INVALID, "race_causal_dot_backward_kept: state must be a 256-byte aligned buffer");
+    RACE_TRY(kept_state_check(state, state_bytes, N, L, E, M, block, "race_causal_dot_backward_kept"));
     return op_bwd_impl(K, Q, V, gO, gK, gQ, gV, N, L, E, M, 0.0f, block, workspace, workspace_bytes, stream, 1,
                        "race_causal_dot_backward_kept", state);
 }
@@ -693,19 +711,18 @@ int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float
 
 int race_nc_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
                         int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
-                        float *state, race_stream stream)
+                        float *state, size_t state_bytes, race_stream stream)
 {
-    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
-        return fail(RACE_ERR_INVALID, "race_nc_op_fwd_keep: state must be a 256-byte aligned buffer");
+    RACE_TRY(kept_state_check(state, state_bytes, N, T, S, D, block, "race_nc_op_fwd_keep"));
     return nc_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, state);
 }
 
 int race_nc_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
                         float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
-                        void *workspace, size_t workspace_bytes, const float *state, race_stream stream)
+                        void *workspace, size_t workspace_bytes, const float *state, size_t state_bytes,
+                        race_stream stream)
 {
-    if (!state || (reinterpret_cast<uintptr_t>(state) & 255))
-        return fail(RACE_ERR_INVALID, "race_nc_op_bwd_kept: state must be a 256-byte aligned buffer");
+    RACE_TRY(kept_state_check(state, state_bytes, N, T, S, D, block, "race_nc_op_bwd_kept"));
     return nc_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream,
                        state);
 }
@@ -719,13 +736,18 @@ size_t race_qkv_state_bytes(const race_qkv_shape *sh)
     return align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
 }
 
+// The fused kernels (race_fused.h) carry the backward suffix states in fp32; the generic ones
+// (race_scan_kernels.h, hash bits or tiles the fused set does not compile) as double-floats,
+// whose low parts need a second pair of arrays.
+static bool qkv_generic(const race_qkv_shape *sh, const Geo &g) { return !fused_variant_exists(g.ST, g.DP, sh->K); }
+
 static size_t qkv_scratch(const race_qkv_shape *sh, const Geo &g, int backward)
 {
     const size_t q_elems = (size_t)sh->B * sh->Hq * sh->T * sh->D;
     const size_t kv_elems = (size_t)sh->B * sh->Hkv * sh->T * sh->D;
     size_t b = 0;
     if (backward)
-        b += align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4);
+        b += (qkv_generic(sh, g) ? 2 : 1) * (align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4));
     if (g.n_st > 1) {
         b += align256((size_t)g.n_st * q_elems * 4);
         if (backward)
@@ -862,6 +884,11 @@ int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     Carver cw(scratch, scratch_bytes);
     P.ws2B = cw.take(g.state_elems_B);
     P.ws2A = cw.take(g.state_elems_A);
+    const bool generic = qkv_generic(sh, g);
+    if (generic) {
+        P.ws3B = cw.take(g.state_elems_B);
+        P.ws3A = cw.take(g.state_elems_A);
+    }
     const int64_t T = sh->T, D = sh->D;
     const int64_t q_elems = (int64_t)sh->B * sh->Hq * T * D, kv_elems = (int64_t)sh->B * sh->Hkv * T * D;
     float *pq = nullptr, *pk = nullptr, *pv = nullptr;
@@ -879,7 +906,9 @@ int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     }
     const hipStream_t s = hs(stream);
     RACE_TRY(run_scan_qkv(K_BWD_TOTALS, g, P, s));
-    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s), "block scan"));
+    RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1, s,
+                                       generic ? P.ws3B : nullptr, generic ? P.ws3A : nullptr),
+                       "block scan"));
     RACE_TRY(run_scan_qkv(K_BWD_MAIN, g, P, s));
     if (g.n_st > 1) {
         RACE_TRY(hip_check(prof_reduce(pq, g.n_st, q_elems, to_out(dq, 0), sh->B, sh->Hq, sh->T, sh->D, s),

@@ -12,6 +12,7 @@ import torch
 from torch.autograd import Function
 
 from . import _lib
+from .race_causal_cuda import state_arg, state_buffer
 
 
 def _flat(x):
@@ -35,7 +36,7 @@ def linear_state(queries, values):
     causal_dot_backward(..., state=)."""
     N, H, L, E = queries.shape
     n = _lib.lib().race_op_state_bytes(N * H, L, E, values.shape[3], 0)
-    return torch.empty((n + 3) // 4, dtype=torch.float32, device=queries.device)
+    return state_buffer(n, queries.device, "race_op_state_bytes")
 
 
 def causal_dot_product(queries, keys, values, product, state=None):
@@ -54,7 +55,7 @@ def causal_dot_product(queries, keys, values, product, state=None):
     if state is None:
         _lib.check(lib.race_causal_dot_product(*args, _lib.stream_of(Q)), "race_causal_dot_product")
     else:
-        _lib.check(lib.race_causal_dot_product_keep(*args, _lib.ptr(state), _lib.stream_of(Q)),
+        _lib.check(lib.race_causal_dot_product_keep(*args, *state_arg(state), _lib.stream_of(Q)),
                    "race_causal_dot_product_keep")
     if copy_out:
         product.copy_(out.view(N, H, L, M))
@@ -78,7 +79,7 @@ def causal_dot_backward(queries, keys, values, grad_out, grad_queries, grad_keys
     if state is None:
         _lib.check(lib.race_causal_dot_backward(*args, _lib.stream_of(Q)), "race_causal_dot_backward")
     else:
-        _lib.check(lib.race_causal_dot_backward_kept(*args, _lib.ptr(state), _lib.stream_of(Q)),
+        _lib.check(lib.race_causal_dot_backward_kept(*args, *state_arg(state), _lib.stream_of(Q)),
                    "race_causal_dot_backward_kept")
     for dst, buf, cp in ((grad_queries, gQ, cq), (grad_keys, gK, ck), (grad_values, gV, cv)):
         if cp:

@@ -18,7 +18,7 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import _lib
-from .race_causal_cuda import _op_inputs, op_state
+from .race_causal_cuda import _op_inputs, op_state, state_arg
 from .race_common import _hash_shape
 
 
@@ -36,7 +36,7 @@ def race_nc_fwd(probsK, probsQ, V2, eps, block=0, state=None):
     if state is None:
         _lib.check(lib.race_nc_op_fwd(*args, _lib.stream_of(pK)), "race_nc_op_fwd")
     else:
-        _lib.check(lib.race_nc_op_fwd_keep(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_nc_op_fwd_keep")
+        _lib.check(lib.race_nc_op_fwd_keep(*args, *state_arg(state), _lib.stream_of(pK)), "race_nc_op_fwd_keep")
     return out
 
 
@@ -53,7 +53,7 @@ def race_nc_bwd(probsK, probsQ, V2, grad_out, eps, block=0, state=None):
     if state is None:
         _lib.check(lib.race_nc_op_bwd(*args, _lib.stream_of(pK)), "race_nc_op_bwd")
     else:
-        _lib.check(lib.race_nc_op_bwd_kept(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_nc_op_bwd_kept")
+        _lib.check(lib.race_nc_op_bwd_kept(*args, *state_arg(state), _lib.stream_of(pK)), "race_nc_op_bwd_kept")
     return gpK, gpQ, gV
 
 

@@ -7,6 +7,7 @@
   fwd_chunk(T)                                                 race_causal_cuda.py:33-44
   RaceCausalFn.apply(probsK, probsQ, V2, eps) -> out [N,T,D]   race_causal_cuda.py:47-69
   race_cuda_fused(probsK, probsQ, V2, eps)                     race_causal_cuda.py:72-73
+  _ext() -> object with race_fused_fwd / race_backward         race_causal_cuda.py:26-30
   RaceCausalCuda(d_k, Kbits, L, M, device, share_planes, eps, seed)   race_causal_cuda.py:76-102
 
 The op-level functions run the fp32 chunked-scan HIP kernels (race_op_fwd /
@@ -46,12 +47,25 @@ def _op_inputs(probsK, probsQ, V2):
     return probsK.contiguous().float(), probsQ.contiguous().float(), V2.contiguous().float()
 
 
+def state_buffer(nbytes, device, what):
+    """A 256-byte aligned device buffer of `nbytes` for a kept forward state; nbytes = 0 means the
+    library rejected the geometry, whose reason is raised."""
+    if nbytes == 0:
+        raise _lib.RaceError(f"{what}: {_lib.lib().race_last_error().decode(errors='replace')}")
+    return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
+
+
 def op_state(probsK, V2, chunk=0):
     """A buffer for the forward block states that race_fused_fwd(..., state=) keeps for
     race_backward(..., state=)."""
     N, T, S = probsK.shape
     n = _lib.lib().race_op_state_bytes(N, T, S, V2.shape[2], max(int(chunk), 0))
-    return torch.empty((n + 3) // 4, dtype=torch.float32, device=probsK.device)
+    return state_buffer(n, probsK.device, "race_op_state_bytes")
+
+
+def state_arg(state):
+    """(pointer, size in bytes) of a kept-state buffer, as the *_keep / *_kept entry points take them."""
+    return _lib.ptr(state), state.numel() * state.element_size()
 
 
 def race_fused_fwd(probsK, probsQ, V2, eps, chunk=0, state=None):
@@ -70,7 +84,7 @@ def race_fused_fwd(probsK, probsQ, V2, eps, chunk=0, state=None):
     if state is None:
         _lib.check(L.race_op_fwd(*args, _lib.stream_of(pK)), "race_op_fwd")
     else:
-        _lib.check(L.race_op_fwd_keep(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_op_fwd_keep")
+        _lib.check(L.race_op_fwd_keep(*args, *state_arg(state), _lib.stream_of(pK)), "race_op_fwd_keep")
     return out
 
 
@@ -94,7 +108,7 @@ def race_backward(probsK, probsQ, V2, grad_out, eps, chunk=0, state=None):
     if state is None:
         _lib.check(L.race_op_bwd(*args, _lib.stream_of(pK)), "race_op_bwd")
     else:
-        _lib.check(L.race_op_bwd_kept(*args, _lib.ptr(state), _lib.stream_of(pK)), "race_op_bwd_kept")
+        _lib.check(L.race_op_bwd_kept(*args, *state_arg(state), _lib.stream_of(pK)), "race_op_bwd_kept")
     return [gpk, gpq, gv]
 
 
@@ -120,6 +134,25 @@ class RaceCausalFn(Function):
 
 def race_cuda_fused(probsK, probsQ, V2, eps=1e-6):
     return RaceCausalFn.apply(probsK, probsQ, V2, eps)
+
+
+class _Ext:
+    """The extension object the reference's _ext() returns (race_causal_cuda.py:26-30), whose
+    bound ops (race_cuda_binding.cpp:12-23) its tests call directly (scaling/test_kernels.py:87-89):
+    race_fused_fwd(pK, pQ, V2, eps, chunk) and race_backward(pK, pQ, V2, gO, eps, chunk), here the
+    HIP op kernels through the C ABI."""
+    race_fused_fwd = staticmethod(race_fused_fwd)
+    race_backward = staticmethod(race_backward)
+
+
+_EXT = _Ext()
+
+
+def _ext():
+    """The library's op entry points under the reference's accessor name (loads librace_amd.so;
+    raises if it is missing: there is no fallback)."""
+    _lib.lib()
+    return _EXT
 
 
 class RaceCausalCuda(nn.Module):

@@ -6,6 +6,12 @@
   soft_hash_probs(Q, K, V, planes_T, protos_T, L, Kbits, M, share_planes)
       -- scaling/race_common.py:36-73, computed by the HIP soft-hash kernel
          (differentiable: the backward is the HIP soft-hash backward).
+  race_prefix_ref(probsK, probsQ, V2, eps)
+      -- scaling/race_common.py:76-90: the reference's pure-torch cumsum specification of
+         the causal scan, (out, A_final, B_final). It materialises [N,T,S,D] and runs out of
+         memory at long T, as the reference's does; it is the comparison function the
+         reference's callers import (scaling/race_torch_cumsum.py:11, scaling/test_kernels.py:19),
+         never a path of the HIP kernels.
 
 The corner prototypes protos_T are accepted for signature compatibility; the
 kernel uses the closed form of the softmax over the 2^K corners
@@ -98,3 +104,13 @@ def soft_hash_probs(Q, K, V, planes_T, protos_T, L, Kbits, M, share_planes=True,
         pQ = pQ.unsqueeze(0).expand(M, -1, -1, -1).reshape(N, T, L * R)
     V2 = V.unsqueeze(0).expand(M, -1, -1, -1, -1).reshape(N, T, D)
     return pK, pQ, V2, N
+
+
+def race_prefix_ref(probsK, probsQ, V2, eps=1e-6):
+    """(out [N,T,D], A_final [N,S], B_final [N,S,D]) of probsK, probsQ [N,T,S], V2 [N,T,D] by
+    materialised torch cumsums, on the tensors' own device (scaling/race_common.py:76-90)."""
+    A_pref = probsK.cumsum(dim=1)
+    B_pref = (probsK.unsqueeze(-1) * V2.unsqueeze(2)).cumsum(dim=1)
+    E_pref = B_pref / (A_pref.unsqueeze(-1) + eps)
+    out = (probsQ.unsqueeze(-1) * E_pref).sum(dim=2)
+    return out, A_pref[:, -1].contiguous(), B_pref[:, -1].contiguous()

@@ -8,16 +8,7 @@ path in this package calls it. Its soft-hash is the HIP soft_hash_probs.
 """
 import torch.nn as nn
 
-from .race_common import build_planes_protos, soft_hash_probs
-
-
-def race_prefix_cumsum(probsK, probsQ, V2, eps=1e-6):
-    """(out, A_final, B_final) by materialised cumsum (race_common.py:76-90)."""
-    A_pref = probsK.cumsum(dim=1)
-    B_pref = (probsK.unsqueeze(-1) * V2.unsqueeze(2)).cumsum(dim=1)
-    E_pref = B_pref / (A_pref.unsqueeze(-1) + eps)
-    out = (probsQ.unsqueeze(-1) * E_pref).sum(dim=2)
-    return out, A_pref[:, -1].contiguous(), B_pref[:, -1].contiguous()
+from .race_common import build_planes_protos, race_prefix_ref, soft_hash_probs
 
 
 class RaceCumsumCausal(nn.Module):
@@ -35,5 +26,5 @@ class RaceCumsumCausal(nn.Module):
         B, H, T, D = Q.shape
         probsK, probsQ, V2, N = soft_hash_probs(Q, K, V, self.planes_T, self.protos_T,
                                                 self.L, self.Kbits, self.M, self.share_planes)
-        out_NTD, _, _ = race_prefix_cumsum(probsK, probsQ, V2.float(), self.eps)
+        out_NTD, _, _ = race_prefix_ref(probsK, probsQ, V2.float(), self.eps)
         return out_NTD.view(self.M, B, H, T, D).mean(dim=0)

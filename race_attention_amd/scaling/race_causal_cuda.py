@@ -8,5 +8,5 @@ _ROOT = _os.path.dirname(_os.path.dirname(_os.path.dirname(_os.path.abspath(__fi
 if _ROOT not in _sys.path:
     _sys.path.insert(0, _ROOT)
 
-from race_attention_amd.race_causal_cuda import (RaceCausalCuda, RaceCausalFn, fwd_chunk,  # noqa: E402,F401
+from race_attention_amd.race_causal_cuda import (RaceCausalCuda, RaceCausalFn, _ext, fwd_chunk,  # noqa: E402,F401
                                                  race_backward, race_cuda_fused, race_fused_fwd)

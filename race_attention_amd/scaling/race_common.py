@@ -8,4 +8,4 @@ _ROOT = _os.path.dirname(_os.path.dirname(_os.path.dirname(_os.path.abspath(__fi
 if _ROOT not in _sys.path:
     _sys.path.insert(0, _ROOT)
 
-from race_attention_amd.race_common import build_planes_protos, soft_hash_probs  # noqa: E402,F401
+from race_attention_amd.race_common import build_planes_protos, race_prefix_ref, soft_hash_probs  # noqa: E402,F401
