@@ -143,6 +143,7 @@ class HybridLM(nn.Module):
         B, T = idx.shape
         if pos is None:
             t0 = 0 if cache is None else cache.get_pos()
+            self.check_length(t0 + T)
             cos_sin = self.cos[:, t0:t0 + T], self.sin[:, t0:t0 + T]
         else:
             rows = pos + torch.arange(T, device=pos.device)
@@ -155,10 +156,17 @@ class HybridLM(nn.Module):
             return logits
         return F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1))
 
+    def check_length(self, total):
+        """Rotary tables cover cfg.max_seq_len positions: longer sequences are refused on the
+        host (a captured decode step reads its rows through a device-side position)."""
+        if total > self.cfg.max_seq_len:
+            raise ValueError(f"sequence of {total} tokens exceeds max_seq_len = {self.cfg.max_seq_len}")
+
     @torch.no_grad()
     def generate_graphed(self, idx, n_new):
         """Greedy decode as generate(idx, n_new), each token step one replay of a captured HIP
         graph (GraphedDecoder). Returns the same (tokens, logits) pair."""
+        self.check_length(idx.shape[1] + n_new - 1)  # the last token is not fed back
         dec = GraphedDecoder(self, idx)
         for _ in range(n_new - 1):
             dec.step()
@@ -168,6 +176,7 @@ class HybridLM(nn.Module):
     def generate(self, idx, n_new, use_cache=True):
         """Greedy decode: returns (tokens [B, n_new], per-step last-position logits [n_new, B, V]).
         use_cache=False re-runs the full forward per token (the reference's GPT.generate)."""
+        self.check_length(idx.shape[1] + n_new - 1)  # the last token is not fed back
         toks, steps = [], []
         if use_cache:
             cache = self.make_cache(idx.shape[0])
@@ -204,6 +213,8 @@ class GraphedDecoder:
     def __init__(self, model, idx):
         self.model = model
         B = idx.shape[0]
+        # the capture itself runs one step past the prompt (on a throwaway cache)
+        model.check_length(idx.shape[1] + 1)
         self.cache = model.make_cache(B)
         logits = model(idx, self.cache)[:, -1]
         self.tok = logits.argmax(-1, keepdim=True)
@@ -236,7 +247,9 @@ class GraphedDecoder:
         return out
 
     def step(self, keep=True):
-        """One token for every sequence (kept for finish() unless keep=False)."""
+        """One token for every sequence (kept for finish() unless keep=False). Refused on the
+        host once the position would pass the rotary tables (cfg.max_seq_len)."""
+        self.model.check_length(self.cache.pos + self.n + 1)
         self.graph.replay()
         self.n += 1
         if keep:

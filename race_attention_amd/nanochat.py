@@ -7,11 +7,19 @@ soft_hash_probs + RaceCausalFn in fp32 (gpt.py:132-140). It asserts n_kv_head ==
 
 This module keeps the same constructor, parameter and buffer names (c_q, c_k, c_v, c_proj,
 ve_gate, planes_T [head_dim, L*K], protos_T [K, 2^K]) so checkpoints load with strict=True,
-and replaces the attention core with the fused bf16 kernels:
-  * grouped-query attention: query head h reads kv head h // (n_head / n_kv_head);
+and runs the attention core on the HIP kernels:
+  * race_precision "fp32" (the default) is the reference's computation without a cache:
+    q, k, v cast to fp32, the soft-hash with fp32 planes (race_soft_hash_fwd) and the fp32
+    chunked scan (RaceCausalFn), the output cast back to the activation dtype (gpt.py:132-140);
+    any head dim and hash bits the soft-hash covers;
+  * race_precision "bf16" runs the fused bf16 kernels (race_qkv_fwd/bwd): planes and bucket
+    probabilities rounded to bf16 inside the kernels, bf16 output; head dim 64 or 128, K <= 4;
+  * grouped-query attention: query head h reads kv head h // (n_head / n_kv_head) (the fp32
+    path repeats k and v over each group, the fused kernels read the shared state);
   * the KV cache is the RACE bucket state (A [S], B [S, D] per kv head), carried by
     RaceStateCache: a prompt is prefilled by the fused forward, which leaves the state,
-    and each further token is one race_decode_step kernel.
+    and each further token is one race_decode_step kernel. The reference has no cache path
+    (gpt.py:143-146), so this one always runs the fused bf16 kernels.
 With share_planes=True every ensemble copy of the reference uses the same planes, so its
 mean over race_m copies equals one copy (race_common.py:49-57); race_m is kept as a field.
 """
@@ -24,7 +32,8 @@ import torch.nn.functional as F
 
 from .attention import race_causal_attention
 from .decode import RaceDecodeState
-from .race_common import build_planes_protos
+from .race_causal_cuda import RaceCausalFn
+from .race_common import build_planes_protos, soft_hash_probs
 
 
 @dataclass
@@ -41,6 +50,7 @@ class GPTConfig:
     race_k: int = 3
     race_m: int = 1
     race_eps: float = 1e-6
+    race_precision: str = "fp32"  # "fp32": gpt.py:132-140 exactly; "bf16": the fused kernels
 
 
 def norm(x):
@@ -98,14 +108,35 @@ class RaceStateCache:
         self.prev_embedding = None
 
 
-def race_attend(q, k, v, planes_T, L, Kbits, eps, state=None):
-    """Causal RACE over [B,T,H,D] activations (bf16): q with Hq heads, k/v with Hkv heads.
+def race_attend_fp32(q, k, v, planes_T, protos_T, L, Kbits, eps):
+    """The reference seam's attention core (gpt.py:132-140) on [B,T,H,D] activations: fp32
+    soft-hash (fp32 planes) and fp32 causal scan on the HIP kernels, k and v repeated over each
+    query-head group; returns y [B,T,Hq,D] in q's dtype."""
+    B, T, Hq, D = q.shape
+    rep = Hq // k.shape[2]
+    qf = q.transpose(1, 2).contiguous().float()
+    kf = k.transpose(1, 2).contiguous().float()
+    vf = v.transpose(1, 2).contiguous().float()
+    if rep > 1:
+        kf, vf = kf.repeat_interleave(rep, 1), vf.repeat_interleave(rep, 1)
+    probsK, probsQ, V2, N = soft_hash_probs(qf, kf, vf, planes_T, protos_T, L, Kbits, 1, True)
+    y = RaceCausalFn.apply(probsK, probsQ, V2, eps).view(B, Hq, T, D)
+    return y.transpose(1, 2).to(q.dtype)
 
-    state None: the fused forward over the whole sequence (autograd-capable).
-    state fresh and T > 1: prefill; the state is left at the end of the sequence.
+
+def race_attend(q, k, v, planes_T, L, Kbits, eps, state=None, precision="bf16", protos_T=None):
+    """Causal RACE over [B,T,H,D] activations: q with Hq heads, k/v with Hkv heads.
+
+    state None: the whole sequence, autograd-capable: precision "bf16" runs the fused kernels,
+      "fp32" the reference's fp32 soft-hash + scan (race_attend_fp32; needs protos_T).
+    state fresh and T > 1: prefill (fused); the state is left at the end of the sequence.
     otherwise: one decode step per token, updating the state in place.
     Returns y [B,T,Hq,D] in q's dtype.
     """
+    if state is None and precision == "fp32":
+        return race_attend_fp32(q, k, v, planes_T, protos_T, L, Kbits, eps)
+    if precision not in ("fp32", "bf16"):
+        raise ValueError(f"race precision must be 'fp32' or 'bf16', got {precision!r}")
     qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
     if state is None:
         return race_causal_attention(qt, kt, vt, planes_T, L, Kbits, eps=eps, out_dtype=q.dtype).transpose(1, 2)
@@ -144,6 +175,7 @@ class CausalSelfAttention(nn.Module):
         self.race_K = config.race_k
         self.race_M = config.race_m
         self.race_eps = config.race_eps
+        self.race_precision = config.race_precision
         self.race_share_planes = True
         self.register_buffer("planes_T", torch.empty(self.head_dim, self.race_L * self.race_K))
         self.register_buffer("protos_T", torch.empty(self.race_K, 1 << self.race_K))
@@ -171,7 +203,8 @@ class CausalSelfAttention(nn.Module):
         q, k = norm(q) * 1.2, norm(k) * 1.2
         # RACE has no sliding window: window_size is ignored, as in the reference (gpt.py:132)
         state = None if kv_cache is None else kv_cache.layers[self.layer_idx]
-        y = race_attend(q, k, v, self.planes_T, self.race_L, self.race_K, self.race_eps, state)
+        y = race_attend(q, k, v, self.planes_T, self.race_L, self.race_K, self.race_eps, state,
+                        precision=self.race_precision, protos_T=self.protos_T)
         if kv_cache is not None and self.layer_idx == self.n_layer - 1:
             kv_cache.advance(T)
         return self.c_proj(y.reshape(B, T, -1))

@@ -4,8 +4,16 @@
       inputs/outputs [M, B, T, H, d_k]; argument order (K, V, Q); eps 1e-6 and
       scale sqrt(d_k) as misc/race.py:67,110; planes drawn from the global RNG
       (misc/race.py:41,48).
-  RACEAttention(d, h, K, L, M, drop, qkv_bias, device)                    misc/race.py:144-173
-  RACEBlock(cfg, device)                                                  misc/race.py:176-206
+  RACEAttention(d, h, K, L, M, drop, qkv_bias, device, merge)             misc/race.py:144-173
+  RACEBlock(cfg, device, merge)                                           misc/race.py:176-206
+
+RACEAttention merges ensembles and heads as the reference does by default
+(merge="reference": out_h.mean(0).permute(0,2,1,3).contiguous().view(B,T,-1),
+misc/race.py:171). That reinterprets the [B,H,T,d_k] buffer as [B,T,H*d_k]: output row t
+holds head floor(t*H/T)'s tokens t*H .. t*H+H-1, so heads and tokens mix and the layer is
+not causal. It is reproduced because a checkpoint trained with the reference learned its
+output projection on that layout. merge="heads" concatenates the heads of each token
+([B,T,H*d_k], causal), the layout a new model wants.
 
 The scan runs on the HIP kernels: bf16 activations (head dim 64/128) take the
 fused q/k/v kernels, everything else the HIP soft-hash + fp32 chunked scan.
@@ -68,11 +76,15 @@ class BatchedACE(nn.Module):
 
 
 class RACEAttention(nn.Module):
-    """Multi-head wrapper around BatchedACE (misc/race.py:144-173)."""
+    """Multi-head wrapper around BatchedACE (misc/race.py:144-173); `merge` as in the module
+    docstring ("reference", the default, or "heads")."""
 
-    def __init__(self, d, h, K, L, M, drop=0.1, qkv_bias=False, device="cpu"):
+    def __init__(self, d, h, K, L, M, drop=0.1, qkv_bias=False, device="cpu", merge="reference"):
         super().__init__()
         assert d % h == 0
+        if merge not in ("reference", "heads"):
+            raise ValueError(f"merge must be 'reference' or 'heads', got {merge!r}")
+        self.merge = merge
         self.h, self.d_k, self.M = h, d // h, M
         self.q = nn.Linear(d, d, bias=qkv_bias)
         self.k = nn.Linear(d, d, bias=qkv_bias)
@@ -87,18 +99,21 @@ class RACEAttention(nn.Module):
         K = self.k(x).view(B, T, self.h, self.d_k)
         V = self.v(x).view(B, T, self.h, self.d_k)
         pack = lambda z: z.unsqueeze(0).expand(self.M, -1, -1, -1, -1)  # noqa: E731
-        out_h = self.ace(pack(K), pack(V), pack(Q))
-        out = out_h.mean(0).contiguous().view(B, T, -1)
+        out_h = self.ace(pack(K), pack(V), pack(Q))  # [M, B, T, H, d_k]
+        if self.merge == "reference":
+            out = out_h.mean(0).permute(0, 2, 1, 3).contiguous().view(B, T, -1)
+        else:
+            out = out_h.mean(0).contiguous().view(B, T, -1)
         return self.drop(self.o(out))
 
 
 class RACEBlock(nn.Module):
     """Pre-norm transformer block with RACEAttention (misc/race.py:176-206)."""
 
-    def __init__(self, cfg, device="cpu"):
+    def __init__(self, cfg, device="cpu", merge="reference"):
         super().__init__()
         self.att = RACEAttention(d=cfg["emb_dim"], h=cfg["n_heads"], K=cfg["K"], L=cfg["L"], M=cfg["M"],
-                                 drop=cfg["drop_rate"], qkv_bias=cfg["qkv_bias"], device=device)
+                                 drop=cfg["drop_rate"], qkv_bias=cfg["qkv_bias"], device=device, merge=merge)
         self.norm1 = nn.LayerNorm(cfg["emb_dim"])
         self.norm2 = nn.LayerNorm(cfg["emb_dim"])
         self.ff = nn.Sequential(nn.Linear(cfg["emb_dim"], 4 * cfg["emb_dim"]), nn.GELU(),

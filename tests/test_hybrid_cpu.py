@@ -64,3 +64,51 @@ def test_hybrid_lm_shapes():
     assert (cfg.n_layer, cfg.n_embd, cfg.n_head, cfg.n_kv_head, cfg.mlp_hidden, cfg.vocab_size) == \
         (16, 2048, 32, 8, 8192, 128256)
     assert cfg.n_embd // cfg.n_head == 64 and (cfg.race_l, cfg.race_k) == (8, 4)
+
+
+def _cpu_lm(max_seq_len):
+    from race_attention_amd.hybrid import HybridConfig, HybridLM
+    cfg = HybridConfig(vocab_size=50, n_layer=1, n_embd=64, n_head=1, n_kv_head=1, mlp_hidden=64,
+                       max_seq_len=max_seq_len)
+    return HybridLM(cfg)
+
+
+def test_generation_refuses_positions_past_the_rotary_tables():
+    """Decoding past cfg.max_seq_len is refused on the host, before any kernel runs: eager and
+    graphed generation, a graphed decoder's construction and each of its steps (whose rotary
+    rows come from a device-side position the host no longer reads)."""
+    from race_attention_amd.hybrid import GraphedDecoder
+    m = _cpu_lm(32)
+    idx = torch.zeros(1, 30, dtype=torch.long)
+    for fn in (lambda: m.generate(idx, 4), lambda: m.generate(idx, 4, use_cache=False),
+               lambda: m.generate_graphed(idx, 4), lambda: GraphedDecoder(m, torch.zeros(1, 32, dtype=torch.long)),
+               lambda: m(torch.zeros(1, 33, dtype=torch.long))):
+        with pytest.raises(ValueError, match="max_seq_len"):
+            fn()
+    m.check_length(32)  # exactly the table length is allowed
+
+    class _Cache:
+        pos = 30
+    dec = object.__new__(GraphedDecoder)  # 2 replays past a 30-token prompt: next position is 32
+    dec.model, dec.cache, dec.n = m, _Cache(), 2
+    dec.graph = None  # never reached: the refusal comes first
+    with pytest.raises(ValueError, match="max_seq_len"):
+        dec.step()
+
+
+def test_seam_precision_option():
+    """The nanochat seam defaults to the reference's fp32 soft-hash + scan (gpt.py:132-140) and
+    accepts only the two precisions."""
+    from race_attention_amd.nanochat import CausalSelfAttention, GPTConfig, race_attend
+    assert GPTConfig().race_precision == "fp32"
+    assert CausalSelfAttention(GPTConfig(race_precision="bf16"), 0).race_precision == "bf16"
+    x = torch.zeros(1, 2, 1, 64)
+    with pytest.raises(ValueError, match="precision"):
+        race_attend(x, x, x, torch.zeros(64, 9), 3, 3, 1e-6, precision="fp16")
+
+
+def test_race_attention_merge_option():
+    from race_attention_amd import RACEAttention
+    assert RACEAttention(64, 2, 2, 2, 1).merge == "reference"
+    with pytest.raises(ValueError, match="merge"):
+        RACEAttention(64, 2, 2, 2, 1, merge="mean")

@@ -367,6 +367,31 @@ def test_batched_ace_nc_temperature_gradcheck():
     assert torch.allclose(a, b, rtol=1e-12, atol=1e-12)
 
 
+def test_batched_ace_nc_distinct_member_planes():
+    """Per-member planes with a DIFFERENT matrix for every member: member m of
+    batched_ace_nc_ref equals race_noncausal_ref on the probabilities of member m's own
+    [B,H,T,dk] slice hashed with planes[m] (so a wrong member-to-planes mapping fails), and the
+    [M,B,T,H,dk] output layout holds it at [m, :, t, h]."""
+    g = torch.Generator().manual_seed(9)
+    M, B, T, H, dk, L, K = 3, 2, 7, 2, 8, 2, 3
+    Kh, Vh, Qh = (torch.randn(M, B, T, H, dk, generator=g, dtype=F64) for _ in range(3))
+    planes = torch.randn(M, dk, L * K, generator=g, dtype=F64)
+    _, protos = orc.build_planes_protos(dk, K, L)
+    lt = torch.tensor(-0.4, dtype=F64)
+    out = orc.batched_ace_nc_ref(Kh, Vh, Qh, planes, protos, L, K, False, lt)
+    scale = float(lt.exp())
+    for m in range(M):
+        q, k, v = (X[m].permute(0, 2, 1, 3) for X in (Qh, Kh, Vh))  # [B,H,T,dk]
+        pK, pQ, V2, N = orc.soft_hash_probs(q, k, v, planes[m], protos, L, K, scale=scale)
+        ref = orc.race_noncausal_ref(pK, pQ, V2).view(B, H, T, dk).permute(0, 2, 1, 3)
+        assert torch.allclose(out[m], ref, rtol=1e-12, atol=1e-12), m
+        for m2 in range(M):  # another member's planes give a different answer
+            if m2 != m:
+                pK2, pQ2, _, _ = orc.soft_hash_probs(q, k, v, planes[m2], protos, L, K, scale=scale)
+                other = orc.race_noncausal_ref(pK2, pQ2, V2).view(B, H, T, dk).permute(0, 2, 1, 3)
+                assert (other - out[m]).abs().max().item() > 1e-6
+
+
 # ------------------------------------------------------------------ causal linear attention
 def _lin_inputs(N, H, L, E, M, seed):
     g = torch.Generator().manual_seed(seed)
