@@ -190,6 +190,18 @@ int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
                  race_tensor go, const float *planes_T, const void *state, size_t state_bytes,
                  race_tensor dq, race_tensor dk, race_tensor dv, void *scratch,
                  size_t scratch_bytes, race_stream stream);
+/* race_qkv_bwd without a scratch argument: no counterpart in the reference; for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops). The scratch lives
+ * in a static device array of race_static_scratch_bytes() = RACE_STATIC_SCRATCH_BYTES bytes on
+ * each GPU the library runs on, held until the process ends. Shapes whose backward scratch
+ * (race_qkv_scratch_bytes(sh, 1)) exceeds it fail with RACE_ERR_WORKSPACE (e.g. more than 128
+ * buckets at D = 64, whose partial outputs need a workspace); nothing is allocated either way.
+ * Calls that overlap on one GPU share the array and race: serialise them (one stream). */
+#define RACE_STATIC_SCRATCH_BYTES (32u << 20)
+size_t race_static_scratch_bytes(void);
+int race_qkv_bwd_static(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v,
+                        race_tensor go, const float *planes_T, const void *state, size_t state_bytes,
+                        race_tensor dq, race_tensor dk, race_tensor dv, race_stream stream);
 /* Final bucket state after the forward: A [B*Hkv][S], Bs [B*Hkv][S][D] fp32. */
 int race_qkv_final_state(const race_qkv_shape *sh, const void *state, size_t state_bytes,
                          float *A, float *Bs, race_stream stream);

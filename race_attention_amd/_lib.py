@@ -86,6 +86,9 @@ SIGNATURES = {
     "race_qkv_bwd": (ctypes.c_int, [ctypes.POINTER(QKVShape), Tensor4, Tensor4, Tensor4, Tensor4, _vp, _vp,
                                     ctypes.c_size_t, Tensor4, Tensor4, Tensor4, _vp, ctypes.c_size_t, _vp]),
     "race_qkv_final_state": (ctypes.c_int, [ctypes.POINTER(QKVShape), _vp, ctypes.c_size_t, _vp, _vp, _vp]),
+    "race_static_scratch_bytes": (ctypes.c_size_t, []),
+    "race_qkv_bwd_static": (ctypes.c_int, [ctypes.POINTER(QKVShape), Tensor4, Tensor4, Tensor4, Tensor4, _vp, _vp,
+                                           ctypes.c_size_t, Tensor4, Tensor4, Tensor4, _vp]),
     "race_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeShape), _vp, _vp, _vp, ctypes.c_int, _vp, _vp,
                                         _vp, _vp, _vp]),
     "race_profile_enable": (ctypes.c_int, [ctypes.c_int]),

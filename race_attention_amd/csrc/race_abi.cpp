@@ -810,7 +810,7 @@ static int qkv_inputs(const race_qkv_shape *sh, const race_tensor &q, const race
 }
 
 int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v, const float *planes_T,
-                 race_tensor out, int out_dtype, void *state, size_t state_bytes, void *scratch,
+                 race_tensor out, int out_dtype, void *state, size_t state_bytes, void *scratch_buf,
                  size_t scratch_bytes, race_stream stream)
 {
     Geo g;
@@ -823,9 +823,9 @@ int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     if (!state || state_bytes < need_state)
         return fail(RACE_ERR_WORKSPACE, "race_qkv_fwd: state of %zu bytes needed, got %zu", need_state,
                     state ? state_bytes : 0);
-    if (need_scr && (!scratch || scratch_bytes < need_scr))
+    if (need_scr && (!scratch_buf || scratch_bytes < need_scr))
         return fail(RACE_ERR_WORKSPACE, "race_qkv_fwd: scratch of %zu bytes needed, got %zu", need_scr,
-                    scratch ? scratch_bytes : 0);
+                    scratch_buf ? scratch_bytes : 0);
     ScanParams P = qkv_params(sh, g);
     P.q = to_view(q);
     P.k = to_view(k);
@@ -838,7 +838,7 @@ int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     const int64_t q_elems = (int64_t)sh->B * sh->Hq * T * D;
     float *part = nullptr;
     if (g.n_st > 1) {
-        Carver cw(scratch, scratch_bytes);
+        Carver cw(scratch_buf, scratch_bytes);
         part = cw.take((size_t)g.n_st * q_elems);
         P.out = OutView{part, (int64_t)sh->Hq * T * D, T * D, D, q_elems, 1};
     } else {
@@ -854,24 +854,46 @@ int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     return RACE_OK;
 }
 
-int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v, race_tensor go,
-                 const float *planes_T, const void *state, size_t state_bytes, race_tensor dq, race_tensor dk,
-                 race_tensor dv, void *scratch, size_t scratch_bytes, race_stream stream)
+// Everything of race_qkv_bwd after its argument checks; `scr` holds qkv_scratch(sh, g, 1) bytes.
+static int qkv_bwd_run(const race_qkv_shape *sh, const Geo &g, race_tensor q, race_tensor k, race_tensor v,
+                       race_tensor go, const float *planes_T, const void *state, size_t state_bytes, race_tensor dq,
+                       race_tensor dk, race_tensor dv, void *scr, size_t scr_bytes, race_stream stream);
+
+static int qkv_bwd_checks(const race_qkv_shape *sh, Geo &g, race_tensor q, race_tensor k, race_tensor v,
+                          race_tensor go, const float *planes_T, const void *state, size_t state_bytes,
+                          race_tensor dq, race_tensor dk, race_tensor dv, const char *who)
 {
-    Geo g;
     RACE_TRY(qkv_geometry(sh, g));
-    RACE_TRY(qkv_inputs(sh, q, k, v, planes_T, "race_qkv_bwd"));
+    RACE_TRY(qkv_inputs(sh, q, k, v, planes_T, who));
     RACE_TRY(check_view(go, "race_qkv_bwd: go", true));
     RACE_TRY(check_view(dq, "race_qkv_bwd: dq", false));
     RACE_TRY(check_view(dk, "race_qkv_bwd: dk", false));
     RACE_TRY(check_view(dv, "race_qkv_bwd: dv", false));
-    const size_t need_state = race_qkv_state_bytes(sh), need_scr = qkv_scratch(sh, g, 1);
+    const size_t need_state = race_qkv_state_bytes(sh);
     if (!state || state_bytes < need_state)
-        return fail(RACE_ERR_WORKSPACE, "race_qkv_bwd: state of %zu bytes needed, got %zu", need_state,
+        return fail(RACE_ERR_WORKSPACE, "%s: state of %zu bytes needed, got %zu", who, need_state,
                     state ? state_bytes : 0);
-    if (!scratch || scratch_bytes < need_scr)
+    return RACE_OK;
+}
+
+int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v, race_tensor go,
+                 const float *planes_T, const void *state, size_t state_bytes, race_tensor dq, race_tensor dk,
+                 race_tensor dv, void *scratch_buf, size_t scratch_bytes, race_stream stream)
+{
+    Geo g;
+    RACE_TRY(qkv_bwd_checks(sh, g, q, k, v, go, planes_T, state, state_bytes, dq, dk, dv, "race_qkv_bwd"));
+    const size_t need_scr = qkv_scratch(sh, g, 1);
+    if (!scratch_buf || scratch_bytes < need_scr)
         return fail(RACE_ERR_WORKSPACE, "race_qkv_bwd: scratch of %zu bytes needed, got %zu", need_scr,
-                    scratch ? scratch_bytes : 0);
+                    scratch_buf ? scratch_bytes : 0);
+    return qkv_bwd_run(sh, g, q, k, v, go, planes_T, state, state_bytes, dq, dk, dv, scratch_buf, scratch_bytes,
+                       stream);
+}
+
+static int qkv_bwd_run(const race_qkv_shape *sh, const Geo &g, race_tensor q, race_tensor k, race_tensor v,
+                       race_tensor go, const float *planes_T, const void *state, size_t state_bytes, race_tensor dq,
+                       race_tensor dk, race_tensor dv, void *scr, size_t scr_bytes, race_stream stream)
+{
     ScanParams P = qkv_params(sh, g);
     P.q = to_view(q);
     P.k = to_view(k);
@@ -881,7 +903,7 @@ int race_qkv_bwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     Carver cs(const_cast<void *>(state), state_bytes);
     P.wsB = cs.take(g.state_elems_B);
     P.wsA = cs.take(g.state_elems_A);
-    Carver cw(scratch, scratch_bytes);
+    Carver cw(scr, scr_bytes);
     P.ws2B = cw.take(g.state_elems_B);
     P.ws2A = cw.take(g.state_elems_A);
     const bool generic = qkv_generic(sh, g);
@@ -937,6 +959,71 @@ int race_qkv_final_state(const race_qkv_shape *sh, const void *state, size_t sta
     const int S = sh->L << sh->K;
     return hip_check(launch_state_extract(wsB, wsA, (int)g.NB, g.S_pad, g.DP, (int)g.Z, S, sh->D, A, Bs, hs(stream)),
                      "race_qkv_final_state");
+}
+
+// ============================================================================ backward without a workspace
+// race_qkv_bwd_static: race_qkv_bwd with its scratch (the suffix-state block sums of the
+// backward) in a file-scope device array instead of a caller's buffer, for callers that cannot
+// allocate device memory (code under HIP graph capture, serving loops). The array lives on
+// every GPU the library runs on until the process ends; its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) and only that address reaches the
+// kernels. Calls on one GPU share the array, so calls that overlap on one GPU (other streams,
+// other threads) race; every element a call reads it has first written in the same call, so
+// nothing needs clearing between calls.
+static __device__ __align__(256) char scratch[RACE_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_addr[MAX_DEVICES] = {};
+
+// Device address of `scratch` on the device that runs `stream` (the current device for the null
+// stream), looked up on the first call for that device.
+int static_scratch(race_stream stream, void **out)
+{
+    int cur = 0;
+    RACE_TRY(hip_check(hipGetDevice(&cur), "race_qkv_bwd_static: hipGetDevice"));
+    int dev = cur;
+    if (stream)
+        RACE_TRY(hip_check(hipStreamGetDevice(hs(stream), &dev), "race_qkv_bwd_static: hipStreamGetDevice"));
+    if (dev < 0 || dev >= MAX_DEVICES)
+        return fail(RACE_ERR_UNSUPPORTED, "race_qkv_bwd_static: device %d beyond %d", dev, MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        if (dev != cur)
+            RACE_TRY(hip_check(hipSetDevice(dev), "race_qkv_bwd_static: hipSetDevice"));
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur)
+            (void)hipSetDevice(cur);
+        RACE_TRY(hip_check(e, "race_qkv_bwd_static: hipGetSymbolAddress"));
+        if (!p)
+            return fail(RACE_ERR_HIP, "race_qkv_bwd_static: no device address for the scratch array");
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return RACE_OK;
+}
+}  // namespace
+
+size_t race_static_scratch_bytes(void) { return RACE_STATIC_SCRATCH_BYTES; }
+
+int race_qkv_bwd_static(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_tensor v, race_tensor go,
+                        const float *planes_T, const void *state, size_t state_bytes, race_tensor dq, race_tensor dk,
+                        race_tensor dv, race_stream stream)
+{
+    Geo g;
+    RACE_TRY(qkv_bwd_checks(sh, g, q, k, v, go, planes_T, state, state_bytes, dq, dk, dv, "race_qkv_bwd_static"));
+    const size_t need = qkv_scratch(sh, g, 1);
+    if (need > RACE_STATIC_SCRATCH_BYTES)
+        return fail(RACE_ERR_WORKSPACE,
+                    "race_qkv_bwd_static: this shape needs %zu bytes of scratch, beyond the static %zu (use "
+                    "race_qkv_bwd with a workspace)",
+                    need, (size_t)RACE_STATIC_SCRATCH_BYTES);
+    void *p = nullptr;
+    RACE_TRY(static_scratch(stream, &p));
+    return qkv_bwd_run(sh, g, q, k, v, go, planes_T, state, state_bytes, dq, dk, dv, p, RACE_STATIC_SCRATCH_BYTES,
+                       stream);
 }
 
 // ============================================================================ decode

@@ -156,3 +156,19 @@ def test_full_size_tests_know_the_block_geometry(B, Hq, Hkv, T, D, L, Kb):
     a256 = lambda n: (n + 255) // 256 * 256
     assert lib.race_qkv_state_bytes(sh) == a256(slots * D * 4) + a256(slots * 4)
     assert (NB - 1) * CB < T <= NB * CB and CB % 32 == 0
+
+
+def test_qkv_bwd_static_refuses_oversize_on_the_host():
+    """race_qkv_bwd_static checks the shape's backward scratch against its static array on the
+    host before any HIP call: S = 256 at D = 64 (two bucket tiles' partial outputs) is refused."""
+    lib = _lib.load_library()
+    assert lib.race_static_scratch_bytes() == 32 << 20
+    sh = _lib.QKVShape(1, 2, 2, 65536, 64, 16, 4, 8.0, 1e-6, 0)
+    assert lib.race_qkv_scratch_bytes(sh, 1) > lib.race_static_scratch_bytes()
+    t = _lib.Tensor4(256, 0, 0, 64)
+    rc = lib.race_qkv_bwd_static(sh, t, t, t, t, ctypes.c_void_p(256), ctypes.c_void_p(256), 1 << 40, t, t, t, None)
+    assert rc == 3 and "beyond the static" in lib.race_last_error().decode()
+    # cfg3 (B=1, H=4, T=2^20) and cfg5's layer (B=8, 32/8 heads, T=8192) fit the array
+    for shape in ((1, 4, 4, 1 << 20, 64, 8, 4), (8, 32, 8, 8192, 64, 8, 4)):
+        s2 = _lib.QKVShape(*shape, 8.0, 1e-6, 0)
+        assert 0 < lib.race_qkv_scratch_bytes(s2, 1) <= lib.race_static_scratch_bytes()
