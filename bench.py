@@ -44,12 +44,16 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-T", type=int, default=8192)
+    ap.add_argument("--cpu-T", type=int, default=16384)
     ap.add_argument("--sweep", action="store_true",
                     help="cfg3 long-context sweep instead of the headline line: tokens/s for "
                          "T = 2^20 .. --sweep-max, GPU and CPU-path memory per token and the "
                          "largest T each fits")
     ap.add_argument("--sweep-max", type=int, default=1 << 24)
+    ap.add_argument("--max-context", action="store_true",
+                    help="measure the longest cfg3 sequence (B=1, H=4, D=64, L=8, K=4) one layer fwd+bwd "
+                         "runs at on this GPU (T doubled, then bisected, until torch reports out of memory) "
+                         "and, in the same run, the longest the CPU path runs within a host-memory budget")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (x3), the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -120,6 +124,9 @@ def main():
         return
     if args.sweep:
         print(json.dumps(bench_sweep(torch, args, build_planes_protos, race_causal_attention)))
+        return
+    if args.max_context:
+        print(json.dumps(bench_max_context(torch, args, build_planes_protos, race_causal_attention)))
         return
     if args.workload == "cfg5":
         print(json.dumps(bench_hybrid(torch, args)))
@@ -286,6 +293,113 @@ def bench_sweep(torch, args, build_planes_protos, race_causal_attention):
                          "host_bytes": host, "cpu_max_T_estimate": int(host // cpu_per_tok)}}
 
 
+def _randn_bf16(torch, shape, gen, std, dev, chunk=1 << 26):
+    """bf16 tensor of N(0, std^2) values drawn in fp32 chunks (no full-size fp32 temporary)."""
+    t = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    flat = t.view(-1)
+    for i in range(0, flat.numel(), chunk):
+        n = min(chunk, flat.numel() - i)
+        flat[i:i + n] = (torch.randn(n, generator=gen, device=dev) * std).to(torch.bfloat16)
+    return t
+
+
+def bench_max_context(torch, args, build_planes_protos, race_causal_attention):
+    """Longest sequence of one cfg3 layer fwd+bwd (B=1, H=4, D=64, L=8, K=4, bf16; q, k, v, go, out,
+    dq, dk, dv resident in HBM, plus the library's block state and scratch) that runs on this GPU:
+    T doubles from 2^22 until torch's allocator reports out of memory (an ordinary Python
+    exception: nothing is launched on memory that was not allocated), then bisects to 2^20 tokens.
+    In the same run the CPU path (oracle/race_cpu_port.py, the reference's memory behaviour) runs
+    doubling T while its projected peak stays within a host-memory budget (half of the host, at
+    most 160 GiB), and its largest T and the host-memory limit implied by its bytes per token are
+    reported beside the GPU's."""
+    import resource
+    dev = torch.device("cuda:0")
+    B, H, D, L, K = 1, args.H, 64, args.L, 4
+    planes_T, _ = build_planes_protos(D, K, L, 1, device=dev, seed=0)
+    std = 1.0 / math.sqrt(D)
+
+    def try_T(T):
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats(dev)
+        box = {}
+        try:
+            g = torch.Generator(device=dev).manual_seed(1)
+            for name, sd in (("q", std), ("k", std), ("v", std), ("go", 1.0)):
+                box[name] = _randn_bf16(torch, (B, H, T, D), g, sd, dev)
+            for name in ("q", "k", "v"):
+                box[name].requires_grad_(True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            box["out"] = race_causal_attention(box["q"], box["k"], box["v"], planes_T, L, K)
+            box["out"].backward(box["go"])
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3
+            ok = bool(torch.isfinite(box["q"].grad[0, 0, -1].float()).all())
+            row = {"T": T, "ok": ok, "ms_fwd_bwd": round(ms, 1), "tokens_per_s": round(B * T / (ms / 1e3), 1),
+                   "peak_hbm_bytes": torch.cuda.max_memory_allocated(dev)}
+        except torch.cuda.OutOfMemoryError:
+            row = {"T": T, "ok": False, "oom": True}
+        box.clear()
+        torch.cuda.empty_cache()
+        print(json.dumps(row), file=sys.stderr, flush=True)
+        return row
+
+    rows = []
+    T, good, bad = 1 << 22, None, None
+    while T <= (1 << 30):
+        r = try_T(T)
+        rows.append(r)
+        if r["ok"]:
+            good = T
+            T *= 2
+        else:
+            bad = T
+            break
+    step = 1 << 20
+    while good is not None and bad is not None and bad - good > step:
+        mid = (good + bad) // 2 // step * step
+        if mid <= good:
+            break
+        r = try_T(mid)
+        rows.append(r)
+        if r["ok"]:
+            good = mid
+        else:
+            bad = mid
+    gpu = {"max_T_ran": good, "first_T_out_of_memory": bad,
+           "gpu_total_bytes": torch.cuda.get_device_properties(dev).total_memory, "trials": rows}
+
+    from oracle import race_cpu_port
+    from oracle import race_oracle as orc
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    host = os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES")
+    budget = min(host // 2, 160 << 30)
+    pl_c, pr_c = orc.build_planes_protos(D, K, L, seed=0)
+    base = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss * 1024
+    cpu_rows, per_tok, Tc = [], None, 4096
+    while per_tok is None or per_tok * Tc * 1.25 <= budget:
+        gc = torch.Generator().manual_seed(1)
+        qc, kc, vc = ((torch.randn(1, H, Tc, D, generator=gc) * std).requires_grad_(True) for _ in range(3))
+        goc = torch.randn(1, H, Tc, D, generator=gc)
+        t0 = time.perf_counter()
+        race_cpu_port.race_layer_cpu(qc, kc, vc, pl_c, pr_c, L, K).backward(goc)
+        sec = time.perf_counter() - t0
+        peak = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss * 1024 - base
+        per_tok = peak / Tc
+        cpu_rows.append({"T": Tc, "seconds_fwd_bwd": round(sec, 3), "tokens_per_s": round(Tc / sec, 1),
+                         "peak_rss_growth_bytes": peak})
+        print(json.dumps(cpu_rows[-1]), file=sys.stderr, flush=True)
+        del qc, kc, vc, goc
+        Tc *= 2
+    cpu = {"max_T_ran": cpu_rows[-1]["T"], "bytes_per_token": round(per_tok, 1), "host_bytes": host,
+           "budget_bytes": budget, "host_limit_T": int(host // per_tok), "cores": cores, "runs": cpu_rows}
+    return {"workload": "cfg3 maximum context: one causal RACE layer fwd+bwd, B=1, H=4, D=64, L=8, K=4, bf16 "
+                        "(GPU) / fp32 reference CPU path (host)",
+            "gpu": gpu, "cpu_path": cpu,
+            "gpu_over_cpu_max_T": round(good / cpu["host_limit_T"], 1) if good else None}
+
+
 def bench_hybrid(torch, args, B=8, T=8192, n_new=256):
     """cfg5: HybridLM (16 layers, hidden 2048, 32/8 heads of 64, SwiGLU 8192, vocab 128256,
     RACE L=8 K=4), bf16 random-init weights, uniform synthetic token ids (seed 1).
@@ -352,7 +466,7 @@ def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6, name="cf
     GPU: the reference's fp32 op path (soft_hash_probs + RaceCausalFn, forward and backward) at the
     reference's scale sqrt(D) and at 1.0; CPU: the reference CPU path (the port, whose soft-hash
     fixes sqrt(D)) on the same inputs (their first cpu_T tokens when given), all host cores,
-    median of 3. The same function serves the `op` workload (the op path at 2^20 (token, head)
+    median of 10 after 2 warm-ups. The same function serves the `op` workload (the op path at 2^20 (token, head)
     pairs) with per-kernel times from the library's HIP events."""
     from oracle import race_cpu_port
     from oracle import race_oracle as orc
@@ -403,15 +517,9 @@ def bench_cfg1(torch, args, B=2, H=8, T=2048, D=64, L=8, K=4, eps=1e-6, name="cf
         qc.grad = kc.grad = vc.grad = None
         race_cpu_port.race_layer_cpu(qc, kc, vc, pl_c, pr_c, L, K).backward(goc)
 
-    run_cpu()
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run_cpu()
-        ts.append(time.perf_counter() - t0)
-    sec = sorted(ts)[1]
-    sample = (f"the whole {name} layer fwd+bwd (scale sqrt(D)), median of 3" if Tc == T else
-              f"the {name} layer fwd+bwd on its first {Tc} tokens (scale sqrt(D)), median of 3")
+    sec = _cpu_median(run_cpu)
+    sample = (f"the whole {name} layer fwd+bwd (scale sqrt(D)), median of 10 after 2 warm-ups" if Tc == T else
+              f"the {name} layer fwd+bwd on its first {Tc} tokens (scale sqrt(D)), median of 10 after 2 warm-ups")
     r = {"metric": f"{name} fp32 layer fwd+bwd tokens/sec", "workload": name, "dtype": "f32",
          "config": {"B": B, "H": H, "T": T, "D": D, "L": L, "K": K, "S": S, "path": "soft_hash_probs + RaceCausalFn"},
          "gpu": gpu,
@@ -446,8 +554,11 @@ def _kernel_split(torch, _lib, step, steps):
     return {n: round(v[0] / steps, 4) for n, v in kern.items()}
 
 
-def _cpu_median(fn, reps=3):
-    fn()
+def _cpu_median(fn, reps=10, warmup=2):
+    """Median wall time of `reps` runs of fn after `warmup` untimed ones (the reference's
+    bench_cpu_kernels.py:27-35 method, with the repetition counts of the CPU-baseline plan)."""
+    for _ in range(warmup):
+        fn()
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -462,7 +573,8 @@ def bench_noncausal(torch, args, B=1, H=4, T=1 << 20, D=128, L=3, K=3, M=1, eps=
     [M,B,T,H,D] ~ N(0,1), one step = forward + backward incl. d loss / d temperature.
     Per (token, head): 12 S D flops for the state contractions plus the soft-hash term of the layer
     count; 11 fp32 rows of HBM traffic (q, k, v, out, go, dq, dk, dv with q, k, v read twice).
-    CPU: the fp64 restatement (oracle) fwd+bwd on all host cores on a T = 2^16 sample."""
+    CPU: the reference's BatchedACE sequence (soft-hash, pK^T V, normalisation, pQ E; torch
+    autograd) in fp32 on all host cores, on a T = 2^16 sample."""
     from oracle import race_oracle as orc
     from race_attention_amd import _lib
     from race_attention_amd.noncausal import BatchedACE
@@ -490,15 +602,15 @@ def bench_noncausal(torch, args, B=1, H=4, T=1 << 20, D=128, L=3, K=3, M=1, eps=
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     gc = torch.Generator().manual_seed(1)
-    Kc, Vc, Qc = (torch.randn(M, B, Tc, H, D, generator=gc, dtype=torch.float64).requires_grad_(True) for _ in range(3))
-    goc = torch.randn(M, B, Tc, H, D, generator=gc, dtype=torch.float64)
-    lt = torch.zeros((), dtype=torch.float64, requires_grad=True)
+    Kc, Vc, Qc = (torch.randn(M, B, Tc, H, D, generator=gc).requires_grad_(True) for _ in range(3))
+    goc = torch.randn(M, B, Tc, H, D, generator=gc)
+    lt = torch.zeros((), requires_grad=True)
     pl, pr = ace.planes_T.cpu(), ace.protos_T.cpu()
 
     def run_cpu():
         for x in (Kc, Vc, Qc, lt):
             x.grad = None
-        orc.batched_ace_nc_ref(Kc, Vc, Qc, pl, pr, L, K, True, lt, eps).backward(goc)
+        orc.batched_ace_nc_ref(Kc, Vc, Qc, pl, pr, L, K, True, lt, eps, dtype=torch.float32).backward(goc)
 
     sec = _cpu_median(run_cpu)
     return {"metric": "non-causal RACE (BatchedACE) fwd+bwd tokens/sec", "value": round(B * T / (ms / 1e3), 1),
@@ -509,7 +621,8 @@ def bench_noncausal(torch, args, B=1, H=4, T=1 << 20, D=128, L=3, K=3, M=1, eps=
                                "t_bound_ms": round(t_bound * 1e3, 4), "frac": round(t_bound * 1e3 / ms, 4)},
             "kernels_ms_per_step": split,
             "cpu_baseline": {"value": round(B * Tc / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
-                             "sample": f"fp64 restatement fwd+bwd at T = 2^16 (same B, H, D, L, K), median of 3",
+                             "sample": "the reference's fp32 BatchedACE sequence fwd+bwd (torch autograd) at T = 2^16 "
+                                       "(same B, H, D, L, K), median of 10 after 2 warm-ups",
                              "seconds_per_step": round(sec, 3)}}
 
 
@@ -517,7 +630,9 @@ def bench_linear(torch, args, B=1, H=4, T=1 << 20, D=64):
     """Causal linear attention (kernels/cpu/linear_pref.cpp:87-226, the comparison baseline) on the
     chunked scan kernels: Q, K, V [B,H,T,D] fp32, Q, K ~ U(0,1) (positive features), V ~ N(0,1);
     one step = forward + backward. Per (token, head): 12 D^2 flops, 11 fp32 rows of HBM traffic.
-    CPU: the fp64 cumulative-sum restatement (oracle) fwd+bwd on a T = 2^12 sample."""
+    CPU: the reference's own kernels/cpu/linear_pref.cpp (causal_dot_product + causal_dot_backward,
+    compiled from its source into oracle/_ref, fp32, OpenMP over the B*H sequences) on a T = 2^17
+    sample; the fp64 cumulative-sum restatement (oracle) at T = 2^12 where that build is absent."""
     from oracle import race_oracle as orc
     from race_attention_amd import _lib
     from race_attention_amd.linear_attention import causal_linear_attention
@@ -539,20 +654,39 @@ def bench_linear(torch, args, B=1, H=4, T=1 << 20, D=64):
     flops = 12 * D * D * n
     nbytes = 11 * D * 4 * n
     t_bound = max(flops / FP32_PEAK, nbytes / HBM_PEAK)
-    Tc = 1 << 12
+    from oracle import oracle_c
+    ext = oracle_c.ref_linear_ext()
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     gc = torch.Generator().manual_seed(1)
-    Qc = torch.rand(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
-    Kc = torch.rand(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
-    Vc = torch.randn(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
-    goc = torch.randn(B, H, Tc, D, generator=gc, dtype=torch.float64)
+    if ext is not None:
+        Tc = 1 << 17
+        Qc, Kc = torch.rand(B, H, Tc, D, generator=gc), torch.rand(B, H, Tc, D, generator=gc)
+        Vc, goc = torch.randn(B, H, Tc, D, generator=gc), torch.randn(B, H, Tc, D, generator=gc)
+        outc, gq, gk, gv = (torch.zeros(B, H, Tc, D) for _ in range(4))
 
-    def run_cpu():
-        for x in (Qc, Kc, Vc):
-            x.grad = None
-        orc.causal_linear_ref(Qc, Kc, Vc).backward(goc)
+        def run_cpu():
+            outc.zero_()
+            ext.causal_dot_product(Qc, Kc, Vc, outc)
+            for t in (gq, gk, gv):
+                t.zero_()
+            ext.causal_dot_backward(Qc, Kc, Vc, goc, gq, gk, gv)
 
+        kind, what = "reference", "the reference's compiled linear_pref.cpp fwd+bwd (fp32)"
+    else:
+        Tc = 1 << 12
+        Qc = torch.rand(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
+        Kc = torch.rand(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
+        Vc = torch.randn(B, H, Tc, D, generator=gc, dtype=torch.float64).requires_grad_(True)
+        goc = torch.randn(B, H, Tc, D, generator=gc, dtype=torch.float64)
+
+        def run_cpu():
+            for x in (Qc, Kc, Vc):
+                x.grad = None
+            orc.causal_linear_ref(Qc, Kc, Vc).backward(goc)
+
+        kind, what = "port", "fp64 cumulative-sum restatement fwd+bwd"
     sec = _cpu_median(run_cpu)
     return {"metric": "causal linear attention fwd+bwd tokens/sec", "value": round(B * T / (ms / 1e3), 1),
             "unit": "tokens/s", "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "f32",
@@ -561,9 +695,9 @@ def bench_linear(torch, args, B=1, H=4, T=1 << 20, D=64):
             "layer_roofline": {"bound": "hbm" if nbytes / HBM_PEAK >= flops / FP32_PEAK else "fp32 compute",
                                "t_bound_ms": round(t_bound * 1e3, 4), "frac": round(t_bound * 1e3 / ms, 4)},
             "kernels_ms_per_step": split,
-            "cpu_baseline": {"value": round(B * Tc / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
-                             "sample": f"fp64 cumulative-sum restatement fwd+bwd at T = 2^12 (same B, H, D), median of 3",
-                             "seconds_per_step": round(sec, 3)}}
+            "cpu_baseline": {"value": round(B * Tc / sec, 1), "unit": "tokens/s", "cores": cores, "kind": kind,
+                             "sample": f"{what} at T = {Tc} (same B, H, D), median of 10 after 2 warm-ups",
+                             "seconds_per_step": round(sec, 4)}}
 
 
 def bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, steps):
@@ -610,9 +744,10 @@ def bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, steps):
                          "algorithmic_bytes_per_launch": bytes_step, "avg_launch_ms": round(k_ms, 5)}}
 
 
-def bench_cpu(torch, T, H, D, L, K, reps=3):
+def bench_cpu(torch, T, H, D, L, K, reps=10, warmup=2):
     """The reference CPU path (soft-hash + RaceCausalCPUFn, fp32, fp64 prefix-mean
-    kernel on OpenMP threads) on the same layer shape with a bounded T."""
+    kernel on OpenMP threads) on the same layer shape with a bounded T: median of `reps`
+    timed runs after `warmup` untimed ones."""
     from oracle import race_cpu_port
     from oracle import race_oracle as orc
     cores = len(os.sched_getaffinity(0))
@@ -628,16 +763,10 @@ def bench_cpu(torch, T, H, D, L, K, reps=3):
         out = race_cpu_port.race_layer_cpu(q, k, v, planes_T, protos_T, L, K)
         out.backward(go)
 
-    run()
-    ts = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        run()
-        ts.append(time.perf_counter() - t0)
-    ts.sort()
-    sec = ts[len(ts) // 2]
+    sec = _cpu_median(run, reps, warmup)
     return {"value": round(T / sec, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"one layer fwd+bwd, B=1 H={H} T={T} D={D} L={L} K={K} fp32, median of {reps}",
+            "sample": f"one layer fwd+bwd, B=1 H={H} T={T} D={D} L={L} K={K} fp32, median of {reps} "
+                      f"after {warmup} warm-up runs",
             "seconds_per_step": round(sec, 3)}
 
 

@@ -243,8 +243,10 @@ def race_noncausal_brute(probsK, probsQ, V2, eps=1e-6):
     return out
 
 
-def batched_ace_nc_ref(Khf, Vhf, Qhf, planes_T, protos_T, L, Kbits, share_planes, logit_temp, eps=1e-6):
-    """BatchedACE.forward of scaling/benchmark_time.py:111-166 in fp64.
+def batched_ace_nc_ref(Khf, Vhf, Qhf, planes_T, protos_T, L, Kbits, share_planes, logit_temp, eps=1e-6,
+                       dtype=F64):
+    """BatchedACE.forward of scaling/benchmark_time.py:111-166 in fp64 (or, as bench.py's CPU
+    baseline, in the reference's own fp32 with dtype=torch.float32).
 
     Khf, Vhf, Qhf [M,B,T,H,dk]; planes_T [dk, L*K] (shared) or [M, dk, L*K];
     logit_temp a 0-d tensor: scale = exp(logit_temp).clamp(1e-2, 10) divides the
@@ -252,14 +254,14 @@ def batched_ace_nc_ref(Khf, Vhf, Qhf, planes_T, protos_T, L, Kbits, share_planes
     M, B, T, H, dk = Khf.shape
     N = M * B * H
     S = L << Kbits
-    scale = logit_temp.to(F64).exp().clamp(1e-2, 10.0)
+    scale = logit_temp.to(dtype).exp().clamp(1e-2, 10.0)
 
     def flat(X):
-        return X.to(F64).permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
+        return X.to(dtype).permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
 
     Kh, Qh, Vh = flat(Khf), flat(Qhf), flat(Vhf)
-    P = planes_T.to(F64)
-    pr = protos_T.to(F64)
+    P = planes_T.to(dtype)
+    pr = protos_T.to(dtype)
 
     def probs(Xh):
         proj = Xh @ P if share_planes else torch.einsum("mbtd,mds->mbts", Xh, P)
