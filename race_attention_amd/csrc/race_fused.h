@@ -1027,9 +1027,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             if (tail)
                 store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
             f32x4 accW[TPW_A], accG[TPW_A];
+            // (REG_ST) pK^T of the wave's bucket tile: the operand of the A scan, gW and St, read once
+            const bf16x8 fPK = ld_tr(&sPK[0][0], LDS, 0, (REG_ST ? wave : 0) * 16, lane);
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
-                const int t = wave + i * NW;
                 accW[i] = f32x4{0.f, 0.f, 0.f, 0.f};
                 accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
                 if (a_ok(i)) {
@@ -1037,7 +1038,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
-                        EngBF16::mma(a, ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
+                        EngBF16::mma(a, REG_ST ? fPK : ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
                         if (tt == MTC - 1 && (lane & 15) == 15)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
@@ -1078,11 +1079,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             // ---- P3: gW^T += pK^T Mg^T ; gpQ^T -> sGP ; gA ; dS^T += go^T W ; St^T += V^T pK (last head)
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
-                const int t = wave + i * NW;
                 if (a_ok(i)) {
                     const int ts = a_ts(i), tt = a_tt(i);
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                    EngBF16::mma(accG[i], ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane),
+                    EngBF16::mma(accG[i], REG_ST ? fPK : ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane),
                                  ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
                     f32x4 gpq;
 #pragma unroll
@@ -1093,16 +1093,18 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                     *reinterpret_cast<f32x4 *>(&sGP[tok][s]) = gpq;
                 }
             }
+            // (REG_ST) W^T of the wave's bucket tile, read once for its dS tiles
+            const bf16x8 fW = ld_tr(&sW[0][0], LDS, 0, (REG_ST ? wave : 0) * 16, lane);
 #pragma unroll
             for (int i = 0; i < TPW_S; ++i) {
                 const int t = wave + i * NW;
                 if (t < CF::NTS * CF::NTD) {
                     const int td = t / CF::NTS, ts = t % CF::NTS;
                     EngBF16::mma(accD[i], ld_tr(&sGO[0][0], LDX, 0, td * 16, lane),
-                                 ld_tr(&sW[0][0], LDS, 0, ts * 16, lane));
+                                 REG_ST ? fW : ld_tr(&sW[0][0], LDS, 0, ts * 16, lane));
                     if (g == G - 1)
                         EngBF16::mma(accS[i], ld_tr(&sV[0][0], LDX, 0, td * 16, lane),
-                                     ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane));
+                                     REG_ST ? fPK : ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane));
                 }
             }
             prev_t0 = t0;
@@ -1427,6 +1429,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             if (g == 0 && tail)
                 tail7();
             f32x4 accW[TPW_A], accG[TPW_A];
+            // (REG_ST) pK^T of the wave's bucket tile: the operand of the A scan, gW and St, read once
+            const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, (REG_ST ? wave : 0) * 16, lane);
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 accW[i] = accG[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1435,7 +1439,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
-                        EngBF16::mma(a, ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
+                        EngBF16::mma(a, REG_ST ? fPK : ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
                         if (tt == MTC - 1 && (lane & 15) == 15)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
@@ -1481,16 +1485,18 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
                 store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
             }
+            // (REG_ST) W^T of the wave's bucket tile: the operand of gpK and dS, read once
+            const bf16x8 fW = ld_tr(&sW[0][0], LDS, 0, (REG_ST ? wave : 0) * 16, lane);
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 if (a_ok(i)) {
                     const int ts = a_ts(i), tt = a_tt(i);
-                    EngBF16::mma(accG[i], ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane),
+                    EngBF16::mma(accG[i], REG_ST ? fPK : ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane),
                                  ld_tr(&sMg[0][0], LDC, 0, tt * 16, lane));
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         accGA[i][e] -= accG[i][e] * accI[i][e] * accW[i][e];
-                    EngBF16::mma(accPK[i], ld_tr(&sW[0][0], LDS, 0, ts * 16, lane),
+                    EngBF16::mma(accPK[i], REG_ST ? fW : ld_tr(&sW[0][0], LDS, 0, ts * 16, lane),
                                  ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
                 }
             }
@@ -1510,18 +1516,19 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     st_vec4(&sMp[c0][r0], acc);
                 }
             }
+            const bf16x8 fWn = EngBF16::neg(fW);
 #pragma unroll
             for (int i = 0; i < TPW_S; ++i) {
                 const int t = wave + i * NW;
                 if (t < CF::NTS * CF::NTD) {
                     const int td = t / CF::NTS, ts = t % CF::NTS;
                     // dS[s][d] -= sum_t W[t][s] go[t][d]   (accD: rows s of tile ts, cols d of td)
-                    EngBF16::mma(accD[i], EngBF16::neg(ld_tr(&sW[0][0], LDS, 0, ts * 16, lane)),
+                    EngBF16::mma(accD[i], REG_ST ? fWn : EngBF16::neg(ld_tr(&sW[0][0], LDS, 0, ts * 16, lane)),
                                  ld_tr(&sGO[0][0], LDX, 0, td * 16, lane));
                     // St^T[d][s] += sum_t V[t][d] pK[t][s]
                     if (g == G - 1)
                         EngBF16::mma(accS[i], ld_tr(&sV[cur][0][0], LDX, 0, td * 16, lane),
-                                     ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane));
+                                     REG_ST ? fPK : ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane));
                 }
             }
             if constexpr (REG_ST) {

@@ -37,6 +37,11 @@ FUSED_CASES = [  # B, Hq, Hkv, T, D, L, K, scale
     (2, 2, 2, 31, 64, 8, 4, None),        # shorter than one 32-token sub-chunk
     (1, 8, 2, 200, 64, 16, 4, None),      # grouped-query heads with two bucket tiles
     (1, 8, 1, 97, 128, 16, 3, 1.0),       # 8 query heads per kv head, K=3 at 128 buckets
+    (1, 2, 2, 600, 64, 4, 4, None),       # S = 64 at head dim 64: 64-bucket tile
+    (1, 2, 2, 700, 64, 16, 3, None),      # K=3 at 128 buckets, head dim 64
+    (1, 2, 2, 400, 64, 32, 2, 1.0),       # K=2 at 128 buckets
+    (2, 6, 2, 450, 64, 8, 3, None),       # S = 64, K=3, grouped-query heads
+    (1, 3, 1, 2000, 64, 16, 4, None),     # grouped-query heads, many sub-chunks per block
 ]
 
 
