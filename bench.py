@@ -42,6 +42,9 @@ def parse():
     ap.add_argument("--H", type=int, default=4)
     ap.add_argument("--L", type=int, default=8)
     ap.add_argument("--decode-steps", type=int, default=1024)
+    ap.add_argument("--decode-seqs", type=int, default=256,
+                    help="sequences of the decode line (cfg4: 256; e.g. 2048 puts the carried state beyond "
+                         "the 256 MB Infinity Cache)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-T", type=int, default=16384)
@@ -226,7 +229,8 @@ def main():
     del q, k, v, go
     torch.cuda.empty_cache()
     if not args.no_decode:
-        result["decode"] = bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, args.decode_steps)
+        result["decode"] = bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, args.decode_steps,
+                                        args.decode_seqs)
     if not args.no_cpu:
         result["cpu_baseline"] = bench_cpu(torch, args.cpu_T, H, D, L, K)
     print(json.dumps(result))
@@ -700,10 +704,10 @@ def bench_linear(torch, args, B=1, H=4, T=1 << 20, D=64):
                              "seconds_per_step": round(sec, 4)}}
 
 
-def bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, steps):
-    """cfg4: 256 sequences with a 512-token prefilled state, 32 q / 8 kv heads, D=64,
+def bench_decode(torch, dev, RaceDecodeState, build_planes_protos, _lib, steps, Bs=256):
+    """cfg4: `Bs` (256) sequences with a 512-token prefilled state, 32 q / 8 kv heads, D=64,
     L=8, K=4; `steps` single-token decode steps updating the fp32 state in place."""
-    Bs, Hq, Hkv, D, L, K, T0 = 256, 32, 8, 64, 8, 4, 512
+    Hq, Hkv, D, L, K, T0 = 32, 8, 64, 8, 4, 512
     S = L << K
     planes_T, _ = build_planes_protos(D, K, L, 1, device=dev, seed=0)
     g = torch.Generator(device=dev).manual_seed(1)
