@@ -1184,7 +1184,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     __shared__ __align__(16) __bf16 sK[C][LDX];
     __shared__ __align__(16) __bf16 sQ[C][LDX];
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
-    __shared__ __align__(16) __bf16 sGO[C][LDX];
+    // go rows; two buffers by step parity where the go^T Mp^T product of a step is deferred to
+    // the next step's first phase (one wave per bucket tile)
+    __shared__ __align__(16) __bf16 sGO[CF::NTS == NW ? 2 : 1][C][LDX];
     __shared__ __align__(16) __bf16 sPK[2][C][LDS];  // by sub-chunk parity
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
     __shared__ __align__(16) __bf16 sW[C][LDS];
@@ -1208,6 +1210,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     // and the bucket tiles match one to one (REG_ST), wave w owns bucket tile w for every token
     // tile and every head-dim tile of the state, so gW = go St^T takes St from registers.
     constexpr bool REG_ST = CF::NTS == NW;
+    // REG_ST: dS^T goes to LDS at the end of H3 and gv += go^T Mp^T runs in the next step's H0,
+    // so a step has four barrier phases; otherwise H4 holds both and the MFMA gA suffix scan
+    constexpr bool DEFER_GV = REG_ST;
     auto a_ts = [&](int i) { return REG_ST ? wave : (wave + i * NW) / MTC; };
     auto a_tt = [&](int i) { return REG_ST ? i : (wave + i * NW) % MTC; };
     auto a_ok = [&](int i) { return REG_ST || (wave + i * NW) < CF::NTS * MTC; };
@@ -1270,6 +1275,16 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     for (int i = 0; i < TPW_V; ++i)
         accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // ---- gv^T += go^T Mp^T of a step (go rows in buffer gbuf)
+    auto gv_mp = [&](int gbuf) {
+#pragma unroll
+        for (int i = 0; i < TPW_V; ++i) {
+            const int t = wv + i * GVW;
+            if (wv >= 0 && t < CF::NTD * MTC)
+                EngBF16::mma(accV[i], ld_tr(&sGO[gbuf][0][0], LDX, 0, (t / MTC) * 16, lane),
+                             ld_k(&sMp[0][0], LDC, (t % MTC) * 16, 0, lane));
+        }
+    };
     // ---- T5 (sub-chunk buffer pb): gpK^T += dS V^T + gAhat -> sF ; St -> sStS
     auto tail5 = [&](int pb) {
 #pragma unroll
@@ -1364,7 +1379,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
         }
     };
 
-    int prev_t0 = -1, prev_nv = 0;
+    int prev_t0 = -1, prev_nv = 0, gb = 0;
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -1378,8 +1393,12 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                 tile_store_rows<CF>(&sV[cur][0][0], pf.v, nv, tid);
             }
             tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
-            tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
+            tile_store_rows<CF>(&sGO[gb][0][0], pf.g, nv, tid);
             pf.advance(P, c, t0, g, tid);
+            if constexpr (DEFER_GV) {
+                if (sc > 0 || g > 0)
+                    gv_mp(gb ^ 1);  // the previous step's go^T Mp^T
+            }
             if (g == 0 && tail)
                 tail5(nxt);
             __syncthreads();
@@ -1455,9 +1474,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
 #pragma unroll
                         for (int kd = 0; kd < DP / 32; ++kd)
                             EngBF16::mma(accG[i], acc_pair(accS[2 * kd], accS[2 * kd + 1]),
-                                         ld_pair(&sGO[0][0], LDX, tt * 16, 32 * kd, lane));
+                                         ld_pair(&sGO[gb][0][0], LDX, tt * 16, 32 * kd, lane));
                     } else {
-                        mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[0][0], tt * 16, lane);
+                        mma_ab<DP, LDX, LDX>(accG[i], &sStS[0][0], ts * 16, &sGO[gb][0][0], tt * 16, lane);
                     }
                 }
             }
@@ -1468,7 +1487,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     // Mg[t][tau] = go_t . v_tau (tau <= t): rows t (tile ta), cols tau (tile tb)
                     const int ta = t / MTC, tb = t % MTC;
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<DP, LDX, LDX>(acc, &sGO[0][0], ta * 16, &sV[cur][0][0], tb * 16, lane);
+                    mma_ab<DP, LDX, LDX>(acc, &sGO[gb][0][0], ta * 16, &sV[cur][0][0], tb * 16, lane);
                     const int r0 = ta * 16 + ((lane >> 4) << 2), c0 = tb * 16 + (lane & 15);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -1524,7 +1543,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     const int td = t / CF::NTS, ts = t % CF::NTS;
                     // dS[s][d] -= sum_t W[t][s] go[t][d]   (accD: rows s of tile ts, cols d of td)
                     EngBF16::mma(accD[i], REG_ST ? fWn : EngBF16::neg(ld_tr(&sW[0][0], LDS, 0, ts * 16, lane)),
-                                 ld_tr(&sGO[0][0], LDX, 0, td * 16, lane));
+                                 ld_tr(&sGO[gb][0][0], LDX, 0, td * 16, lane));
                     // St^T[d][s] += sum_t V[t][d] pK[t][s]
                     if (g == G - 1)
                         EngBF16::mma(accS[i], ld_tr(&sV[cur][0][0], LDX, 0, td * 16, lane),
@@ -1573,15 +1592,25 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     }
                 }
             }
-            __syncthreads();
-            // ---- H4: gv^T += go^T Mp^T ; (last head) dS^T -> sdSt, gAhat scan
+            if (DEFER_GV && g == G - 1) {
+                // dS^T -> sdSt (last read in H1, two barriers ago; next read in T5)
 #pragma unroll
-            for (int i = 0; i < TPW_V; ++i) {
-                const int t = wv + i * GVW;
-                if (wv >= 0 && t < CF::NTD * MTC)
-                    EngBF16::mma(accV[i], ld_tr(&sGO[0][0], LDX, 0, (t / MTC) * 16, lane),
-                                 ld_k(&sMp[0][0], LDC, (t % MTC) * 16, 0, lane));
+                for (int i = 0; i < TPW_S; ++i) {
+                    const int t = wave + i * NW;
+                    if (t < CF::NTS * CF::NTD) {
+                        const int td = t / CF::NTS, ts = t % CF::NTS;
+                        const int s2 = ts * 16 + ((lane >> 4) << 2), d2 = td * 16 + (lane & 15);
+                        st_vec4(&sdSt[d2][s2], accD[i]);
+                    }
+                }
             }
+            __syncthreads();
+            if constexpr (DEFER_GV) {
+                gb ^= 1;
+                continue;
+            }
+            // ---- H4: gv^T += go^T Mp^T ; (last head) dS^T -> sdSt, gAhat scan
+            gv_mp(0);
             if (g == G - 1) {
 #pragma unroll
                 for (int i = 0; i < TPW_S; ++i) {
@@ -1624,6 +1653,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     }
     // tail of the last sub-chunk
     const int pb = (nsub - 1) & 1;
+    if constexpr (DEFER_GV)
+        gv_mp(gb ^ 1);  // the last step's go^T Mp^T
     tail5(pb);
     __syncthreads();
     tail6(pb, prev_nv, thk);
