@@ -69,6 +69,9 @@ int64_t resolve_block(int64_t T, int64_t streams, int C, int64_t req, int64_t ta
 // ------------------------------------------------------------------ geometry
 struct Geo {
     int ST, DP, C, n_st, S_pad;
+    // fused layer with n_st > 1: the kernels that write outputs run one launch per bucket tile,
+    // each adding the earlier tiles' fp32 sum in its store (no partial-sum reduction pass)
+    bool seq = false;
     int64_t CB, NB;
     int64_t Z;               // kv streams
     size_t state_elems_B;    // per workspace array
@@ -155,7 +158,8 @@ int qkv_geometry(const race_qkv_shape *sh, Geo &g)
     // ~768 workgroups per launch: whole rounds on MI355X's 256 CUs both for the backward kernels
     // (one workgroup per CU: 3 rounds) and for the bf16 readout (three per CU: 1 round), with
     // few enough blocks to keep the block-state traffic and per-block set-up low
-    g.CB = resolve_block(sh->T, g.Z * g.n_st, g.C, sh->block, 768);
+    g.seq = g.n_st > 1 && fused_variant_exists(g.ST, g.DP, sh->K);
+    g.CB = resolve_block(sh->T, g.Z * (g.seq ? 1 : g.n_st), g.C, sh->block, 768);
     g.NB = cdiv(sh->T, g.CB);
     fill_ws_sizes(g);
     return RACE_OK;
@@ -748,10 +752,11 @@ static size_t qkv_scratch(const race_qkv_shape *sh, const Geo &g, int backward)
     size_t b = 0;
     if (backward)
         b += (qkv_generic(sh, g) ? 2 : 1) * (align256(g.state_elems_B * 4) + align256(g.state_elems_A * 4));
-    if (g.n_st > 1) {
-        b += align256((size_t)g.n_st * q_elems * 4);
+    if (g.n_st > 1) {  // fp32 partial sums: one per tile, or one running sum (seq)
+        const size_t m = g.seq ? 1 : g.n_st;
+        b += align256(m * q_elems * 4);
         if (backward)
-            b += 2 * align256((size_t)g.n_st * kv_elems * 4);
+            b += 2 * align256(m * kv_elems * 4);
     }
     return b;
 }
@@ -787,10 +792,26 @@ static ScanParams qkv_params(const race_qkv_shape *sh, const Geo &g)
     return P;
 }
 
+// Output view of bucket tile j of n when the tiles run one launch after another: every tile but
+// the last writes the fp32 running sum `run` (contiguous [B][H][T][D]); every tile but the first
+// adds the running sum in its store; the last writes the caller's output.
+static OutView tile_out(int j, int n, float *run, const OutView &final_out, int H, int64_t T, int64_t D)
+{
+    OutView o = j == n - 1 ? final_out : OutView{run, H * T * D, T * D, D, 0, 1};
+    o.acc = j > 0 ? run : nullptr;
+    o.acc_sb = H * T * D;
+    o.acc_sh = T * D;
+    o.acc_st = D;
+    o.stage_f32 = 1;
+    return o;
+}
+
 static int run_scan_qkv(ScanKernel k, const Geo &g, const ScanParams &P, hipStream_t s)
 {
     ProfScope ps(RACE_PROF_QKV_FWD_TOTALS + (int)k, s);
-    const dim3 grid((unsigned)g.NB, (unsigned)g.n_st, (unsigned)g.Z);
+    // (seq) the output kernels cover the one bucket tile P.st_base per launch
+    const unsigned tiles = g.seq && k != K_FWD_TOTALS ? 1u : (unsigned)g.n_st;
+    const dim3 grid((unsigned)g.NB, tiles, (unsigned)g.Z);
     // kernels specialised on the hash bits where compiled (K = 2..4), generic ones otherwise
     if (fused_variant_exists(g.ST, g.DP, P.K))
         return hip_check(launch_fused(k, g.ST, g.DP, P.K, P, grid, s), "race_qkv fused kernel launch");
@@ -839,7 +860,7 @@ int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     float *part = nullptr;
     if (g.n_st > 1) {
         Carver cw(scratch_buf, scratch_bytes);
-        part = cw.take((size_t)g.n_st * q_elems);
+        part = cw.take((size_t)(g.seq ? 1 : g.n_st) * q_elems);
         P.out = OutView{part, (int64_t)sh->Hq * T * D, T * D, D, q_elems, 1};
     } else {
         P.out = to_out(out, out_dtype == RACE_F32);
@@ -847,6 +868,14 @@ int race_qkv_fwd(const race_qkv_shape *sh, race_tensor q, race_tensor k, race_te
     const hipStream_t s = hs(stream);
     RACE_TRY(run_scan_qkv(K_FWD_TOTALS, g, P, s));
     RACE_TRY(hip_check(prof_block_scan(P.wsB, (int64_t)g.S_pad * g.DP, P.wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan"));
+    if (g.seq) {
+        for (int j = 0; j < g.n_st; ++j) {
+            P.st_base = j;
+            P.out = tile_out(j, g.n_st, part, to_out(out, out_dtype == RACE_F32), sh->Hq, T, D);
+            RACE_TRY(run_scan_qkv(K_FWD_READOUT, g, P, s));
+        }
+        return RACE_OK;
+    }
     RACE_TRY(run_scan_qkv(K_FWD_READOUT, g, P, s));
     if (part)
         RACE_TRY(hip_check(prof_reduce(part, g.n_st, q_elems, to_out(out, out_dtype == RACE_F32), sh->B,
@@ -914,6 +943,28 @@ static int qkv_bwd_run(const race_qkv_shape *sh, const Geo &g, race_tensor q, ra
     const int64_t T = sh->T, D = sh->D;
     const int64_t q_elems = (int64_t)sh->B * sh->Hq * T * D, kv_elems = (int64_t)sh->B * sh->Hkv * T * D;
     float *pq = nullptr, *pk = nullptr, *pv = nullptr;
+    if (g.seq) {
+        pq = cw.take(q_elems);
+        pk = cw.take(kv_elems);
+        pv = cw.take(kv_elems);
+        const hipStream_t s = hs(stream);
+        for (int j = 0; j < g.n_st; ++j) {
+            P.st_base = j;
+            P.dq = tile_out(j, g.n_st, pq, to_out(dq, 0), sh->Hq, T, D);
+            RACE_TRY(run_scan_qkv(K_BWD_TOTALS, g, P, s));
+        }
+        P.st_base = 0;
+        RACE_TRY(hip_check(prof_block_scan(P.ws2B, (int64_t)g.S_pad * g.DP, P.ws2A, g.S_pad, (int)g.NB, (int)g.Z, 1,
+                                           s),
+                           "block scan"));
+        for (int j = 0; j < g.n_st; ++j) {
+            P.st_base = j;
+            P.dk = tile_out(j, g.n_st, pk, to_out(dk, 0), sh->Hkv, T, D);
+            P.dv = tile_out(j, g.n_st, pv, to_out(dv, 0), sh->Hkv, T, D);
+            RACE_TRY(run_scan_qkv(K_BWD_MAIN, g, P, s));
+        }
+        return RACE_OK;
+    }
     if (g.n_st > 1) {
         pq = cw.take((size_t)g.n_st * q_elems);
         pk = cw.take((size_t)g.n_st * kv_elems);

@@ -313,6 +313,104 @@ RACE_DEV const __bf16 *row_ptr(const View &v, int b, int h, int t)
     return reinterpret_cast<const __bf16 *>(v.p) + (b * v.sb + h * v.sh + (int64_t)t * v.st);
 }
 
+// Bucket tiles launched one after another (OutView::stage_f32): each thread owns E consecutive
+// elements of one row of a staged C x DP output tile. The earlier tiles' fp32 sum for those
+// elements (OutView::acc) is loaded into registers some barrier phases before the tile is stored,
+// so that the store does not wait on HBM; zeros when there is no earlier tile.
+template <int C, int DP, int NTH>
+struct AccRows {
+    static constexpr int E = C * DP / NTH;  // elements per thread
+    static constexpr int RPT = DP / E;      // threads per row
+    static_assert(E % 4 == 0 && E <= 16 && RPT * E == DP, "accumulated store layout");
+    f32x4 a[E / 4];
+
+    RACE_DEV void load(const OutView &o, int b, int h, int t0, int nv, int tid)
+    {
+        const int row = tid / RPT, col = (tid % RPT) * E;
+#pragma unroll
+        for (int i = 0; i < E / 4; ++i)
+            a[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (o.acc && row < nv) {
+            const float *p = o.acc + b * o.acc_sb + h * o.acc_sh + (int64_t)(t0 + row) * o.acc_st + col;
+#pragma unroll
+            for (int i = 0; i < E / 4; ++i)
+                a[i] = *reinterpret_cast<const f32x4 *>(p + 4 * i);
+        }
+    }
+};
+
+// Store of an fp32-staged tile in that mode: staged values plus the loaded earlier-tile sum, as
+// fp32 (the running sum, or an fp32 output) or rounded once to bf16 (the last tile).
+template <int C, int DP, int LDO, int NTH>
+RACE_DEV void store_staged_acc(const OutView &o, int b, int h, int st, int t0, int nv, const float (*sO)[LDO],
+                               const AccRows<C, DP, NTH> &ar, int tid)
+{
+    using AR = AccRows<C, DP, NTH>;
+    constexpr int E = AR::E;
+    const int row = tid / AR::RPT, col = (tid % AR::RPT) * E;
+    if (row >= nv)
+        return;
+    f32x4 x[E / 4];
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i)
+        x[i] = *reinterpret_cast<const f32x4 *>(&sO[row][col + 4 * i]) + ar.a[i];
+    const int64_t off = (int64_t)st * o.tile + b * o.sb + h * o.sh + (int64_t)(t0 + row) * o.st + col;
+    if (o.f32) {
+        float *dst = reinterpret_cast<float *>(o.p) + off;
+#pragma unroll
+        for (int i = 0; i < E / 4; ++i)
+            *reinterpret_cast<f32x4 *>(dst + 4 * i) = x[i];
+    } else if constexpr (E == 4) {
+        bf16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = (__bf16)x[0][e];
+        *reinterpret_cast<bf16x4 *>(reinterpret_cast<__bf16 *>(o.p) + off) = w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < E / 8; ++i) {
+            bf16x8 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                w[e] = (__bf16)x[2 * i][e];
+                w[4 + e] = (__bf16)x[2 * i + 1][e];
+            }
+            *reinterpret_cast<bf16x8 *>(reinterpret_cast<__bf16 *>(o.p) + off + 8 * i) = w;
+        }
+    }
+}
+
+// Coalesced store of a staged C x DP tile (rows < nv) to a [B][H][T][D] output view.
+template <class OT, int C, int DP, int LDO, int NTH>
+RACE_DEV void store_staged(const OutView &o, int b, int h, int st, int t0, int nv, const OT (*sO)[LDO], int tid)
+{
+    constexpr int EPC = 16 / (int)sizeof(OT);  // elements per 16-byte chunk
+    constexpr int OCH = DP / EPC;
+    for (int i = tid; i < C * OCH; i += NTH) {
+        const int row = i / OCH, ch = i % OCH;
+        if (row < nv) {
+            OT *dst = reinterpret_cast<OT *>(o.p) + (int64_t)st * o.tile + b * o.sb + h * o.sh +
+                      (int64_t)(t0 + row) * o.st + ch * EPC;
+            *reinterpret_cast<u32x4 *>(dst) = *reinterpret_cast<const u32x4 *>(&sO[row][ch * EPC]);
+        }
+    }
+}
+
+// Store of a staged output tile: the accumulating form when the bucket tiles run one launch
+// after another (fp32 staging only), the plain one otherwise.
+template <class OT, int C, int DP, int LDO, int NTH>
+RACE_DEV void store_out(const OutView &o, int b, int h, int st, int t0, int nv, const OT (*sO)[LDO],
+                        const AccRows<C, DP, NTH> &ar, int tid)
+{
+    if constexpr (std::is_same<OT, float>::value) {
+        if (o.stage_f32) {  // uniform branch
+            store_staged_acc<C, DP, LDO, NTH>(o, b, h, st, t0, nv, sO, ar, tid);
+            return;
+        }
+    }
+    store_staged<OT, C, DP, LDO, NTH>(o, b, h, st, t0, nv, sO, tid);
+}
+
 // ============================================================================ forward totals
 template <int ST, int DP, int KB, int NW>
 __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParams P)
@@ -528,6 +626,7 @@ void race_fused_fwd_readout(const ScanParams P)
 
     f32x4 accA[TPW_A];  // 1/(A+eps), transposed tiles, kept across query heads
     int prev_t0 = -1, prev_nv = 0, prev_h = 0;
+    AccRows<C, DP, NTH> arO;
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -583,22 +682,16 @@ void race_fused_fwd_readout(const ScanParams P)
                     }
                 }
             }
-            if (prev_t0 >= 0) {
-                // coalesced store of the previous (sub-chunk, head) output from sO
-                constexpr int OCH = DP * (int)sizeof(OT) / 16;  // 16-byte chunks per row
-                for (int i = tid; i < C * OCH; i += NTH) {
-                    const int row = i / OCH, ch = i % OCH;
-                    if (row < prev_nv) {
-                        OT *dst = reinterpret_cast<OT *>(P.out.p) +
-                                  (int64_t)c.st * P.out.tile + c.b * P.out.sb + prev_h * P.out.sh +
-                                  (int64_t)(prev_t0 + row) * P.out.st + ch * (16 / (int)sizeof(OT));
-                        *reinterpret_cast<u32x4 *>(dst) =
-                            *reinterpret_cast<const u32x4 *>(&sO[row][ch * (16 / (int)sizeof(OT))]);
-                    }
-                }
-            }
+            if (prev_t0 >= 0)  // coalesced store of the previous (sub-chunk, head) output from sO
+                store_out<OT, C, DP, LDO, NTH>(P.out, c.b, prev_h, c.st, prev_t0, prev_nv, sO, arO, tid);
             __syncthreads();
             // ---- P2: A^T = A0 + pK^T Tri^T (first head); W^T = pQ^T / (A + eps) -> sW
+            //          | (tiles one launch after another) the earlier tiles' sum of this step's
+            //          output rows into registers, for the store in the next step's P1
+            if constexpr (OUT_F32) {
+                if (P.out.stage_f32)
+                    arO.load(P.out, c.b, hq, t0, nv, tid);
+            }
 #pragma unroll
             for (int i = 0; i < TPW_A; ++i) {
                 const int t = wave + i * NW;
@@ -694,17 +787,7 @@ void race_fused_fwd_readout(const ScanParams P)
         }
     }
     // last output rows
-    {
-        constexpr int OCH = DP * (int)sizeof(OT) / 16;
-        for (int i = tid; i < C * OCH; i += NTH) {
-            const int row = i / OCH, ch = i % OCH;
-            if (row < prev_nv) {
-                OT *dst = reinterpret_cast<OT *>(P.out.p) + (int64_t)c.st * P.out.tile + c.b * P.out.sb +
-                          prev_h * P.out.sh + (int64_t)(prev_t0 + row) * P.out.st + ch * (16 / (int)sizeof(OT));
-                *reinterpret_cast<u32x4 *>(dst) = *reinterpret_cast<const u32x4 *>(&sO[row][ch * (16 / (int)sizeof(OT))]);
-            }
-        }
-    }
+    store_out<OT, C, DP, LDO, NTH>(P.out, c.b, prev_h, c.st, prev_t0, prev_nv, sO, arO, tid);
 }
 
 
@@ -768,22 +851,6 @@ RACE_DEV void softhash_bwd_ct(const float *th, const float *p, const float *gp, 
             z[i] = z[2 * i] + z[2 * i + 1];
         }
         gproj[k] = gu * inv_scale * (1.0f - th[k] * th[k]);
-    }
-}
-
-// Coalesced store of a staged C x DP tile (rows < nv) to a [B][H][T][D] output view.
-template <class OT, int C, int DP, int LDO, int NTH>
-RACE_DEV void store_staged(const OutView &o, int b, int h, int st, int t0, int nv, const OT (*sO)[LDO], int tid)
-{
-    constexpr int EPC = 16 / (int)sizeof(OT);  // elements per 16-byte chunk
-    constexpr int OCH = DP / EPC;
-    for (int i = tid; i < C * OCH; i += NTH) {
-        const int row = i / OCH, ch = i % OCH;
-        if (row < nv) {
-            OT *dst = reinterpret_cast<OT *>(o.p) + (int64_t)st * o.tile + b * o.sb + h * o.sh +
-                      (int64_t)(t0 + row) * o.st + ch * EPC;
-            *reinterpret_cast<u32x4 *>(dst) = *reinterpret_cast<const u32x4 *>(&sO[row][ch * EPC]);
-        }
     }
 }
 
@@ -897,6 +964,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     const int G = G1 ? 1 : P.G;  // G1: one query head per kv head, the head loop folds away
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     int prev_t0 = -1, prev_nv = 0, prev_h = 0;
+    AccRows<C, DP, NTH> arQ;
     RowPrefetch<CF> pf;
     pf.load(P, c, c.t_begin, c.hk * G, true, tid);
     wait_vmem_all();
@@ -982,6 +1050,13 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             }
             tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
             tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
+            // (tiles one launch after another) the earlier tiles' sum of the previous step's dq
+            // rows, stored in P2; issued before the row prefetch so that waiting for it does not
+            // wait for the prefetch
+            if constexpr (OUT_F32) {
+                if (tail && P.dq.stage_f32)
+                    arQ.load(P.dq, c.b, prev_h, prev_t0, prev_nv, tid);
+            }
             pf.advance(P, c, t0, g, tid);
             if (tail)
                 tail4(g == 0);
@@ -1025,7 +1100,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             // ---- P2: A^T scan (first head) -> 1/(A+eps); W -> sW ; Mg -> sMg ; gW^T = St go^T
             //          | the previous step's dq rows out
             if (tail)
-                store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
+                store_out<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, arQ, tid);
             f32x4 accW[TPW_A], accG[TPW_A];
             // (REG_ST) pK^T of the wave's bucket tile: the operand of the A scan, gW and St, read once
             const bf16x8 fPK = ld_tr(&sPK[0][0], LDS, 0, (REG_ST ? wave : 0) * 16, lane);
@@ -1117,8 +1192,12 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     tail4(false);
     __syncthreads();
     tail5();
+    if constexpr (OUT_F32) {
+        if (P.dq.stage_f32)
+            arQ.load(P.dq, c.b, prev_h, prev_t0, prev_nv, tid);
+    }
     __syncthreads();
-    store_staged<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, tid);
+    store_out<OT, C, DP, LDO, NTH>(P.dq, c.b, prev_h, c.st, prev_t0, prev_nv, sO, arQ, tid);
 
     // block totals: dS^T -> ws2B [s][d] ; gA (sum over tokens) -> ws2A
     float *wB = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
@@ -1380,6 +1459,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     };
 
     int prev_t0 = -1, prev_nv = 0, gb = 0;
+    AccRows<C, DP, NTH> arK, arV;
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
         const int nv = min(C, c.t_end - t0);
@@ -1394,6 +1474,14 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             }
             tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
             tile_store_rows<CF>(&sGO[gb][0][0], pf.g, nv, tid);
+            // (tiles one launch after another) the earlier tiles' sums of the previous sub-chunk's
+            // dk and dv rows, stored in H3; issued before the row prefetch
+            if constexpr (OUT_F32) {
+                if (g == 0 && tail && P.dk.stage_f32) {
+                    arK.load(P.dk, c.b, c.hk, prev_t0, prev_nv, tid);
+                    arV.load(P.dv, c.b, c.hk, prev_t0, prev_nv, tid);
+                }
+            }
             pf.advance(P, c, t0, g, tid);
             if constexpr (DEFER_GV) {
                 if (sc > 0 || g > 0)
@@ -1501,8 +1589,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             //          dS -= W^T go ; St^T += V^T pK (last head) ; gA^T hi/lo -> [tau][s] ;
             //          previous sub-chunk's dk, dv out
             if (g == 0 && tail) {
-                store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
-                store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
+                store_out<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, arK, tid);
+                store_out<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, arV, tid);
             }
             // (REG_ST) W^T of the wave's bucket tile: the operand of gpK and dS, read once
             const bf16x8 fW = ld_tr(&sW[0][0], LDS, 0, (REG_ST ? wave : 0) * 16, lane);
@@ -1660,9 +1748,15 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     tail6(pb, prev_nv, thk);
     __syncthreads();
     tail7();
+    if constexpr (OUT_F32) {
+        if (P.dk.stage_f32) {
+            arK.load(P.dk, c.b, c.hk, prev_t0, prev_nv, tid);
+            arV.load(P.dv, c.b, c.hk, prev_t0, prev_nv, tid);
+        }
+    }
     __syncthreads();
-    store_staged<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, tid);
-    store_staged<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, tid);
+    store_out<OT, C, DP, LDO, NTH>(P.dk, c.b, c.hk, c.st, prev_t0, prev_nv, sOk, arK, tid);
+    store_out<OT, C, DP, LDO, NTH>(P.dv, c.b, c.hk, c.st, prev_t0, prev_nv, sOv, arV, tid);
 }
 
 }  // namespace race

@@ -26,17 +26,17 @@ static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStr
             hipLaunchKernelGGL((race_fused_fwd_totals<ST, DP, KB, NW>), grid, block, 0, s, P);
         else
             return hipErrorInvalidValue;
-    } else if (k == K_FWD_READOUT && P.out.f32)
+    } else if (k == K_FWD_READOUT && (P.out.f32 || P.out.stage_f32))
         hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, true, G1>), grid, block, 0, s, P);
     else if (k == K_FWD_READOUT)
         hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, false, G1>), grid, block, 0, s, P);
-    else if (k == K_BWD_TOTALS && P.dq.f32)
+    else if (k == K_BWD_TOTALS && (P.dq.f32 || P.dq.stage_f32))
         hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, true, G1>), grid, block, 0, s, P);
     else if (k == K_BWD_TOTALS)
         hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, false, G1>), grid, block, 0, s, P);
-    else if (k == K_BWD_MAIN && P.dk.f32 != P.dv.f32)
+    else if (k == K_BWD_MAIN && (P.dk.f32 || P.dk.stage_f32) != (P.dv.f32 || P.dv.stage_f32))
         return hipErrorInvalidValue;
-    else if (k == K_BWD_MAIN && P.dk.f32)
+    else if (k == K_BWD_MAIN && (P.dk.f32 || P.dk.stage_f32))
         hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, true, G1>), grid, block, 0, s, P);
     else if (k == K_BWD_MAIN)
         hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, false, G1>), grid, block, 0, s, P);

@@ -17,6 +17,13 @@ struct OutView {
     int64_t sb, sh, st;
     int64_t tile;   // element offset added per s-tile (partial-sum buffers)
     int f32;        // 1: float32 elements, 0: bfloat16 elements
+    // Bucket tiles launched one after another (fused kernels): a non-null acc holds the fp32 sum
+    // of the earlier tiles' contributions ([B][H][T][D] with its own element strides), added to
+    // this tile's before the store; stage_f32 asks for the kernel variant that stages rows in
+    // fp32, so that the sum is rounded once, when the last tile writes it.
+    const float *acc;
+    int64_t acc_sb, acc_sh, acc_st;
+    int stage_f32;
 };
 
 // One launch of the chunked causal scan.
@@ -28,6 +35,7 @@ struct ScanParams {
     int G, Hkv;            // query heads per kv head, kv heads (qkv mode)
     int CB, NB;            // tokens per block, blocks
     int n_st, S_pad;       // bucket tiles per stream, n_st * tile
+    int st_base;           // bucket tile of grid row blockIdx.y = 0 (tiles launched one at a time)
     int DPw;               // padded head dim used by the state workspaces
     float eps, scale, inv_scale;
     // qkv mode (bf16 activations; planes_T fp32 [D][L*K], shared by all heads)

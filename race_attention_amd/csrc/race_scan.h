@@ -87,7 +87,7 @@ RACE_DEV Ctx make_ctx(const ScanParams &P, int ST)
     c.lane = c.tid & 63;
     c.wave = c.tid >> 6;
     c.blk = blockIdx.x;
-    c.st = blockIdx.y;
+    c.st = blockIdx.y + P.st_base;
     c.z = blockIdx.z;
     c.t_begin = c.blk * P.CB;
     c.t_end = min(P.T, c.t_begin + P.CB);

@@ -157,6 +157,9 @@ def qkv_blocks(T, Z, L, Kb, D=64, C=32, target=768):
     st_max = 128 if D == 64 else 64
     st = next((x for x in (32, 64, 128) if st_max >= x >= S), st_max)
     n_st = -(-S // st)
+    # the fused kernels (K = 2..4) launch one bucket tile at a time: ~target workgroups per tile
+    if 2 <= Kb <= 4:
+        n_st = 1
     nb = max(1, -(-target // (Z * n_st)))
     cb = max(4 * C, -(-(-(-T // nb)) // C) * C)
     cb = min(cb, -(-T // C) * C)
