@@ -292,6 +292,12 @@ RACE_DEV float row_scan16(float v)
     return v;
 }
 
+// Value of lane 15 of each 16-lane DPP row, in every lane of that row (row_newbcast:15).
+RACE_DEV float row_bcast15(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x15F, 0xF, 0xF, false));
+}
+
 // s_waitcnt vmcnt(0): every vector-memory operation of the wave has completed. Issued once
 // after a kernel's prologue loads, so that the uses of those registers inside the sub-chunk
 // loop need no wait there (such a wait would also cover the loop's own prefetch loads).
@@ -1607,6 +1613,30 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                                  ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
                 }
             }
+            if constexpr (REG_ST) {
+                if (g == G - 1) {
+                    // gAhat_t = gAhat_start - sum_{tau < t} gA_tau. Wave w holds bucket tile w for
+                    // both token tiles, and a token tile's 16 tokens lie along the 16 lanes of a DPP
+                    // row: fp32 row scans, with token tile 0's row total carried into tile 1; the
+                    // sub-chunk total seeds the next sub-chunk.
+                    const int s = wave * 16 + ((lane >> 4) << 2);
+                    const f32x4 g0 = *reinterpret_cast<const f32x4 *>(&sGAe[cur][s]);
+                    f32x4 carry = {0.f, 0.f, 0.f, 0.f}, gend;
+#pragma unroll
+                    for (int i = 0; i < TPW_A; ++i) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float inc = row_scan16(accGA[i][e]) + carry[e];
+                            gend[e] = g0[e] - inc;
+                            accGA[i][e] += gend[e];
+                            if (i + 1 < TPW_A)
+                                carry[e] = row_bcast15(inc);
+                        }
+                    }
+                    if ((lane & 15) == 15)
+                        *reinterpret_cast<f32x4 *>(&sGAe[nxt][s]) = gend;
+                }
+            }
 #pragma unroll
             for (int i = 0; i < TPW_M; ++i) {
                 const int t = wave + i * NW;
@@ -1638,30 +1668,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                                      REG_ST ? fPK : ld_tr(&sPK[cur][0][0], LDS, 0, ts * 16, lane));
                 }
             }
-            if constexpr (REG_ST) {
-                if (g == G - 1) {
-                    // gAhat_t = gAhat_start - sum_{tau < t} gA_tau. Wave w holds bucket tile w for
-                    // both token tiles, and a token tile's 16 tokens lie along the 16 lanes of a DPP
-                    // row: fp32 row scans, with token tile 0's row total carried into tile 1; the
-                    // sub-chunk total seeds the next sub-chunk.
-                    const int s = wave * 16 + ((lane >> 4) << 2);
-                    const f32x4 g0 = *reinterpret_cast<const f32x4 *>(&sGAe[cur][s]);
-                    f32x4 carry = {0.f, 0.f, 0.f, 0.f}, gend;
-#pragma unroll
-                    for (int i = 0; i < TPW_A; ++i) {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float inc = row_scan16(accGA[i][e]) + carry[e];
-                            gend[e] = g0[e] - inc;
-                            accGA[i][e] += gend[e];
-                            if (i + 1 < TPW_A)
-                                carry[e] = __shfl(inc, (lane & 48) | 15, 64);
-                        }
-                    }
-                    if ((lane & 15) == 15)
-                        *reinterpret_cast<f32x4 *>(&sGAe[nxt][s]) = gend;
-                }
-            } else {
+            if constexpr (!REG_ST) {
 #pragma unroll
                 for (int i = 0; i < TPW_A; ++i) {
                     if (a_ok(i) && g == G - 1) {
