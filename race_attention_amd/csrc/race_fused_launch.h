@@ -3,6 +3,7 @@
 // which compile the two specialisations in separate translation units.
 #pragma once
 #include "race_fused.h"
+#include "race_fused_ws.h"
 #include "race_launch.h"
 
 namespace race {
@@ -30,7 +31,12 @@ static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStr
         hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, true, G1>), grid, block, 0, s, P);
     else if (k == K_FWD_READOUT)
         hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, false, G1>), grid, block, 0, s, P);
-    else if (k == K_BWD_TOTALS && (P.dq.f32 || P.dq.stage_f32))
+    else if (k == K_BWD_TOTALS && G1 && ST == 128 && DP == 64 && KB == 4 && !P.dq.f32 && !P.dq.stage_f32) {
+        // wave-specialised variant, bf16 dq: eight state waves and four helper waves (race_fused_ws.h);
+        // its fp32-staging form does not fit three waves per SIMD without spilling in the loop
+        if constexpr (G1 && ST == 128 && DP == 64 && KB == 4)
+            hipLaunchKernelGGL((race_fused_bwd_totals_ws<ST, DP, KB, false>), grid, dim3(768), 0, s, P);
+    } else if (k == K_BWD_TOTALS && (P.dq.f32 || P.dq.stage_f32))
         hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, true, G1>), grid, block, 0, s, P);
     else if (k == K_BWD_TOTALS)
         hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, false, G1>), grid, block, 0, s, P);

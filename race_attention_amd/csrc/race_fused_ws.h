@@ -1,0 +1,424 @@
+// Wave-specialised backward totals kernel of the fused layer: one query head per kv head,
+// 128-bucket tiles, head dim 64, K = 4 bits (the shape of the long-context benchmark).
+//
+// Same results as race_fused_bwd_totals (race_fused.h): dq, and the block totals of W^T go and
+// of gA. The workgroup is split by role instead of by tile set:
+//  * eight state waves, wave w owning bucket tile w with its share of the bucket state St in
+//    registers: the A scan, W = pQ/(A+eps), gW = go St^T + pK^T Mg^T, gpQ, gA and the state
+//    products (St += V^T pK, dS^T += go^T W);
+//  * four helper waves: the soft-hash of q one sub-chunk ahead of the state waves, the soft-hash
+//    backward of q, dq = planes gproj^T and the dq stores;
+//  * the state waves also move the rows (loads two sub-chunks ahead, staging into LDS: k and q
+//    by waves 0-3, v and go by waves 4-7), and waves 0-3 soft-hash the next sub-chunk's k rows
+//    (one projection tile each): work that fits their idle time in the second phase. (Hashing
+//    q on waves 4-7 as well measured 0.6 % slower: it leaves the helpers idle in that phase.)
+// A sub-chunk costs two barrier phases (X0, X1) and each SIMD runs three waves (two state, one
+// helper), so the helpers' soft-hash arithmetic overlaps the state waves' MFMA and LDS latency.
+//
+// Pipeline of sub-chunk s (helpers work on s - 1 and s + 1 around the state waves' s):
+//   X0  state: rows of s + 1 into LDS, loads of s + 3;
+//              A scan, W -> sW, gW = St go^T, Mg -> sMg                        (sub-chunk s)
+//       help:  dq rows of s - 2 out; soft-hash backward of q -> sGU            (sub-chunk s - 1)
+//   X1  state: gW += pK^T Mg^T, gpQ -> sGP, gA, dS^T += go^T W, St += V^T pK    (sub-chunk s)
+//              soft-hash of k -> pK (waves 0-3)                                 (sub-chunk s + 1)
+//       help:  dq^T = P gproj^T -> sO (s - 1); soft-hash of q -> pQ              (sub-chunk s + 1)
+// Arrays that the two roles use in the same phase are double buffered by sub-chunk parity
+// (v and go rows, pK, pQ, the A carry); every other array is written and read in different
+// phases.
+#pragma once
+#include "race_fused.h"
+
+namespace race {
+
+template <int ST, int DP, int KB, bool OUT_F32>
+__global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams P)
+{
+    constexpr int NWS = ST / 16;  // state waves: one 16-bucket tile each
+    constexpr int NWH = 4;        // helper waves
+    constexpr int NTH = (NWS + NWH) * 64;
+    constexpr int NTHH = NWH * 64;
+    using CF = FCfg<ST, DP, KB, NWS>;  // tile constants
+    using CH = FCfg<ST, DP, KB, NWH>;  // row loads and staging: 256 threads per pair of row arrays
+    constexpr int C = CF::C, R = CF::R, MTC = CF::MTC, NTD = CF::NTD;
+    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG;
+    using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
+    constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
+    static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised totals: 128-bucket tiles, D = 64, K = 4");
+    static_assert(CF::NPT == 4, "one projection tile of k per wave 0-3 and of q per helper wave");
+    static_assert(CF::LKP == 32, "one MFMA k step for the dq product");
+    static_assert(CH::CHUNKS == NTHH && CH::PF == 1, "one 16-byte chunk of each row tile per mover thread");
+    static_assert((NTD * MTC) % NWH == 0, "dq tiles split evenly over the helper waves");
+    static_assert(CF::LT == 8, "every (token, table) lane of a helper tile is a table of the bucket tile");
+    constexpr int TPH_O = NTD * MTC / NWH;  // dq tiles per helper wave
+
+    __shared__ __align__(16) __bf16 sK[C][LDX];
+    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
+    __shared__ __align__(16) __bf16 sGO[2][C][LDX];  // by sub-chunk parity
+    __shared__ __align__(16) __bf16 sPK[2][C][LDS];  // rows [t][s], by sub-chunk parity
+    __shared__ __align__(16) __bf16 sPQ[2][C][LDS];
+    __shared__ __align__(16) __bf16 sW[C][LDS];
+    __shared__ __align__(16) __bf16 sMg[C][LDC];     // Mg as [t][tau]
+    __shared__ __align__(16) float sGP[C][ST + 4];   // gpQ rows [t][s]
+    __shared__ __align__(16) __bf16 sGU[C][LDG];     // projection gradients of q [t][j]
+    __shared__ __align__(16) OT sO[C][LDO];          // dq staging
+    __shared__ __align__(16) float sA0[2][ST];
+    __shared__ float sGAred[ST];
+    // lane-ordered constant MFMA fragments (read back 16 bytes per lane, conflict-free): the
+    // triangle of the A scan (state waves) and each helper wave's planes fragments
+    __shared__ __align__(16) bf16x8 sTri[MTC][64];
+    __shared__ __align__(16) bf16x8 sProj[NWH][DP / 32][64];
+    __shared__ __align__(16) bf16x8 sBack[NWH][TPH_O][64];
+    // tanh of the q projections, from the soft-hash forward (X1) to its backward two phases later,
+    // by sub-chunk parity: [parity][token][table*4 + bit]
+    __shared__ __align__(16) float sThQ[2][C][CF::LKP];
+
+    const Ctx c = make_ctx(P, ST);
+    const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
+    const int tid = c.tid, lane = c.lane, wave = c.wave;
+    const bool helper = wave >= NWS;
+    const bool movkq = wave < NWH;
+    const int mid = tid & (NTHH - 1);  // thread index within its group of four waves
+    const int hw = wave - NWS, hid = tid - NWS * 64;  // helper wave / thread index
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    auto nv_of = [&](int s) { return min(C, c.t_end - (c.t_begin + s * C)); };
+    zero_lds_bf16(&sPK[0][0][0], 2 * C * LDS, tid, NTH);
+    zero_lds_bf16(&sPQ[0][0][0], 2 * C * LDS, tid, NTH);
+    zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
+    for (int i = tid; i < ST; i += NTH)
+        sGAred[i] = 0.0f;
+
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    const int LKtot = P.L * P.K;
+
+    // ---- state waves: St^T at the block start (lane: col s, rows d), dS^T and gA totals
+    f32x4 accS[NTD], accD[NTD], accGA[MTC], accI[MTC], accG[MTC];
+    if (!helper) {
+        const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < NTD; ++i) {
+            const int d = i * 16 + ((lane >> 4) << 2), s = wave * 16 + (lane & 15);
+            accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + d);
+            accD[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int tt = 0; tt < MTC; ++tt)
+            accGA[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (wave < MTC) {
+            const int t = wave * 16 + (lane & 15);
+            bf16x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                f[e] = (__bf16)(((lane >> 4) * 8 + e <= t) ? 1.0f : 0.0f);
+            sTri[wave][lane] = f;
+        }
+    }
+    {
+        const float *wA = P.wsA + slot * P.S_pad + c.s0;
+        for (int s = tid; s < ST; s += NTH)
+            sA0[0][s] = wA[s];
+    }
+
+    // ---- helper waves: planes fragments of projection tile hw (k and q share the rows j; the state
+    // waves hash with the fragments of tile wave % 4) and of their dq tiles
+    // movers: k, q rows (waves 0-3) or v, go rows (waves 4-7) of a sub-chunk; two sets, loaded two
+    // sub-chunks ahead of their staging
+    struct MoveRegs {
+        u32x4 a[1], b[1];
+    };
+    MoveRegs mA, mB;
+    AccRows<C, DP, NTHH> arQ;
+    const int hjt = hw / MTC, htt = hw % MTC;  // the helper's projection tile
+    if (helper) {
+        const int j = hjt * 16 + (lane & 15);
+        const int table = j >> 2, bit = j & 3;
+#pragma unroll
+        for (int kb = 0; kb < DP / 32; ++kb) {
+            bf16x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int d = kb * 32 + (lane >> 4) * 8 + e;
+                float x = 0.0f;
+                if (bit < P.K && table < c.Lt && d < P.D)
+                    x = P.planes[d * LKtot + (c.l0 + table) * P.K + bit];
+                f[e] = (__bf16)x;
+            }
+            sProj[hw][kb][lane] = f;
+        }
+#pragma unroll
+        for (int i = 0; i < TPH_O; ++i) {
+            const int td = (hw + NWH * i) / MTC;
+            const int d = td * 16 + (lane & 15);
+            bf16x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int jj = (lane >> 4) * 8 + e;
+                const int table = jj >> 2, bit = jj & 3;
+                float x = 0.0f;
+                if (bit < P.K && table < c.Lt && d < P.D)
+                    x = P.planes[d * LKtot + (c.l0 + table) * P.K + bit];
+                f[e] = (__bf16)x;
+            }
+            sBack[hw][i][lane] = f;
+        }
+    }
+    auto load_rows = [&](MoveRegs &m, int s) {  // movers: rows of sub-chunk s into registers (2 loads)
+        const int t0 = c.t_begin + s * C, nv = nv_of(s);
+        if (movkq) {
+            tile_load<CH>(m.a, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, mid);
+            tile_load<CH>(m.b, row_ptr(P.q, c.b, c.hk, t0), P.q.st, nv, mid);
+        } else {
+            tile_load<CH>(m.a, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, mid);
+            tile_load<CH>(m.b, row_ptr(P.go, c.b, c.hk, t0), P.go.st, nv, mid);
+        }
+    };
+    auto stage_rows = [&](const MoveRegs &m, int s) {  // movers: registers into LDS (v, go by parity)
+        const int nv = nv_of(s), pb = s & 1;
+        if (movkq) {
+            tile_store_rows<CH>(&sK[0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sQ[0][0], m.b, nv, mid);
+        } else {
+            tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
+        }
+    };
+    // movers at the top of a sub-chunk: wait for the set holding the rows of the next sub-chunk,
+    // loaded two sub-chunks earlier. The movers issue no other vector-memory operation in the loop
+    // and exactly two loads per sub-chunk (past the end they re-read the last sub-chunk), and
+    // operations retire in issue order, so "at most two outstanding" is exactly the older set.
+    auto wait_rows = [&]() { wait_vmem_older<2>(); };
+    // soft-hash of projection tile tw (token tile tw % MTC, tables 4 (tw / MTC) ..) of the rows in sX
+    // for sub-chunk s -> probability rows of dst; keep_th: the tanh of the projections into
+    // sThQ[s & 1] for the backward. (q: helper wave tw; k: state wave tw.)
+    auto hash_fwd = [&](const __bf16 *sX, __bf16 *dst, int tw, int s, bool keep_th) {
+        const int jt = tw / MTC, tt = tw % MTC;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * LDX + (lane >> 4) * 8;
+#pragma unroll
+        for (int kb = 0; kb < DP / 32; ++kb)
+            EngBF16::mma(acc, sProj[tw][kb][lane], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+        const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+        const bool ok = tok < nv_of(s) && table < c.Lt;
+        float th[4], p[R];
+        softhash_fwd_ct<KB>(acc, coef, ok, th, p);
+        if (keep_th)
+            *reinterpret_cast<f32x4 *>(&sThQ[s & 1][tok][table * 4]) = f32x4{th[0], th[1], th[2], th[3]};
+        __bf16 *row = dst + tok * LDS + table * R;
+#pragma unroll
+        for (int h = 0; h < R / 8; ++h) {
+            bf16x8 w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                w[e] = (__bf16)p[8 * h + e];
+            *reinterpret_cast<bf16x8 *>(row + 8 * h) = w;
+        }
+    };
+    // helpers: soft-hash backward of q for sub-chunk s (gpQ rows in sGP) -> sGU
+    auto hash_bwd_q = [&](int s) {
+        const int tok = htt * 16 + (lane & 15), table = hjt * 4 + (lane >> 4);
+        {
+            float gp[R], p[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int h = 0; h < R / 4; ++h) {
+                const f32x4 x = *reinterpret_cast<const f32x4 *>(&sGP[tok][table * R + 4 * h]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    gp[4 * h + e] = x[e];
+            }
+            const f32x4 t4 = *reinterpret_cast<const f32x4 *>(&sThQ[s & 1][tok][table * 4]);
+            const float th[4] = {t4[0], t4[1], t4[2], t4[3]};
+            probs_from_th<KB>(th, coef, tok < nv_of(s) && table < c.Lt ? 1.0f : 0.0f, p);
+            softhash_bwd_ct<KB>(th, p, gp, P.inv_scale, gproj);
+            bf16x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
+            *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
+        }
+    };
+    // helpers: dq^T = P gproj^T -> sO
+    auto dq_mma = [&]() {
+#pragma unroll
+        for (int i = 0; i < TPH_O; ++i) {
+            const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            EngBF16::mma(acc, sBack[hw][i][lane], *reinterpret_cast<const bf16x8 *>(&sGU[tt * 16 + (lane & 15)][(lane >> 4) * 8]));
+            const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+            if constexpr (OUT_F32)
+                *reinterpret_cast<f32x4 *>(&sO[tok][d]) = acc;
+            else
+                st_vec4(&sO[tok][d], acc);
+        }
+    };
+    auto dq_store = [&](int s) {  // helpers: the staged dq rows of sub-chunk s to HBM
+        store_out<OT, C, DP, LDO, NTHH>(P.dq, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sO, arQ, hid);
+    };
+    auto acc_load = [&](int s) {  // helpers (tiles launched one after another): earlier tiles' dq sum
+        if constexpr (OUT_F32) {
+            if (P.dq.stage_f32)
+                arQ.load(P.dq, c.b, c.hk, c.t_begin + s * C, nv_of(s), hid);
+        }
+    };
+
+    // The two roles run separate loops with the same sequence of barriers (2 before the loop, 2
+    // per sub-chunk, 3 after it): the role is uniform within a wave, so every wave of the
+    // workgroup reaches each barrier, and each role's memory-counter waits see only its own
+    // operations.
+    if (helper) {
+        // ================================================================ helper waves
+        __syncthreads();  // rows of sub-chunk 0 in LDS
+        hash_fwd(&sQ[0][0], &sPQ[0][0][0], hw, 0, true);
+        __syncthreads();
+        for (int s = 0; s < nsub; ++s) {
+            // X0: dq rows of s - 2 out; soft-hash backward of q of s - 1
+            if (s >= 2)
+                dq_store(s - 2);
+            if (s >= 1) {
+                acc_load(s - 1);
+                hash_bwd_q(s - 1);
+            }
+            __syncthreads();
+            // X1: dq of s - 1; soft-hash of q of s + 1 (k: state waves 0-3)
+            if (s >= 1)
+                dq_mma();
+            if (s + 1 < nsub)
+                hash_fwd(&sQ[0][0], &sPQ[(s & 1) ^ 1][0][0], hw, s + 1, true);
+            __syncthreads();
+        }
+        // tail: the last sub-chunk's q backward and dq
+        if (nsub >= 2)
+            dq_store(nsub - 2);
+        acc_load(nsub - 1);
+        hash_bwd_q(nsub - 1);
+        __syncthreads();
+        dq_mma();
+        __syncthreads();
+        wait_vmem_all();
+        dq_store(nsub - 1);
+        __syncthreads();
+    } else {
+        // ================================================================ state waves
+        // rows of sub-chunk 0 into LDS; those of sub-chunks 1 and 2 in flight
+        load_rows(mA, 0);
+        wait_vmem_all();
+        stage_rows(mA, 0);
+        load_rows(mA, min(1, nsub - 1));
+        load_rows(mB, min(2, nsub - 1));
+        __syncthreads();
+        if (movkq)
+            hash_fwd(&sK[0][0], &sPK[0][0][0], wave, 0, false);
+        __syncthreads();
+        // sub-chunk s; set u holds the rows of s + 1 and is refilled with those of s + 3
+        auto body = [&](int s, MoveRegs &u) {
+            const int cur = s & 1, nxt = cur ^ 1;
+            // X0: rows of s + 1 into LDS, loads of s + 3; A scan, W, gW = St go^T, Mg
+            wait_rows();
+            if (s + 1 < nsub)
+                stage_rows(u, s + 1);
+            load_rows(u, min(s + 3, nsub - 1));
+            {
+                const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, wave * 16, lane);
+#pragma unroll
+                for (int tt = 0; tt < MTC; ++tt) {
+                    const int sb = wave * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                    f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][sb]);
+                    EngBF16::mma(a, fPK, sTri[tt][lane]);
+                    if (tt == MTC - 1 && (lane & 15) == 15)
+                        *reinterpret_cast<f32x4 *>(&sA0[nxt][sb]) = a;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accI[tt][e] = frcp(a[e] + P.eps);
+                    const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[cur][tok][sb]);
+                    f32x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = (float)q4[e] * accI[tt][e];
+                    st_vec4(&sW[tok][sb], w);
+                    accG[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kd = 0; kd < DP / 32; ++kd)
+                        EngBF16::mma(accG[tt], acc_pair(accS[2 * kd], accS[2 * kd + 1]),
+                                     ld_pair(&sGO[cur][0][0], LDX, tt * 16, 32 * kd, lane));
+                }
+                if (wave < MTC * MTC) {
+                    // Mg[t][tau] = go_t . v_tau (tau <= t): rows tau (tile tu), cols t (tile tt)
+                    const int tu = wave / MTC, tt = wave % MTC;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<DP, LDX, LDX>(acc, &sV[cur][0][0], tu * 16, &sGO[cur][0][0], tt * 16, lane);
+                    const int tau = tu * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (tau + e > tok)
+                            acc[e] = 0.0f;
+                    st_vec4(&sMg[tok][tau], acc);
+                }
+            }
+            __syncthreads();
+            // X1: gW += pK^T Mg^T, gpQ, gA, dS^T += go^T W, St += V^T pK
+            // pK^T fragment and W (the same bf16 pQ times the same reciprocal as in X0) read again
+            // rather than kept in registers across the barrier
+            const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, wave * 16, lane);
+#pragma unroll
+            for (int tt = 0; tt < MTC; ++tt) {
+                const int sb = wave * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+                EngBF16::mma(accG[tt], fPK, ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
+                const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[cur][tok][sb]);
+                f32x4 gpq;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    gpq[e] = accG[tt][e] * accI[tt][e];
+                    accGA[tt][e] -= gpq[e] * ((float)q4[e] * accI[tt][e]);
+                }
+                *reinterpret_cast<f32x4 *>(&sGP[tok][sb]) = gpq;
+            }
+            const bf16x8 fW = ld_tr(&sW[0][0], LDS, 0, wave * 16, lane);
+#pragma unroll
+            for (int i = 0; i < NTD; ++i) {
+                EngBF16::mma(accD[i], ld_tr(&sGO[cur][0][0], LDX, 0, i * 16, lane), fW);
+                EngBF16::mma(accS[i], ld_tr(&sV[cur][0][0], LDX, 0, i * 16, lane), fPK);
+            }
+            // waves 0-3: soft-hash of k of s + 1 (its rows were staged in X0)
+            if (movkq && s + 1 < nsub)
+                hash_fwd(&sK[0][0], &sPK[nxt][0][0], wave, s + 1, false);
+            __syncthreads();
+        };
+        // unrolled by two, both halves unconditional inside the loop: each register set is named
+        // statically and the loop edge sees the same loads on every path
+        int s = 0;
+        for (; s + 1 < nsub; s += 2) {
+            body(s, mA);
+            body(s + 1, mB);
+        }
+        if (s < nsub)
+            body(s, mA);
+        wait_vmem_all();  // (the re-read rows past the end)
+        __syncthreads();
+        __syncthreads();
+        // block totals: dS^T -> ws2B [s][d] ; gA (sum over tokens) -> ws2A
+        float *wB = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+#pragma unroll
+        for (int i = 0; i < NTD; ++i) {
+            const int d = i * 16 + ((lane >> 4) << 2), s = wave * 16 + (lane & 15);
+            *reinterpret_cast<f32x4 *>(wB + (int64_t)s * P.DPw + d) = accD[i];
+        }
+#pragma unroll
+        for (int tt = 0; tt < MTC; ++tt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = accGA[tt][e];
+                v += __shfl_xor(v, 1);
+                v += __shfl_xor(v, 2);
+                v += __shfl_xor(v, 4);
+                v += __shfl_xor(v, 8);
+                if ((lane & 15) == 0)
+                    atomicAdd(&sGAred[wave * 16 + ((lane >> 4) << 2) + e], v);
+            }
+        }
+        __syncthreads();
+    }
+    float *wA = P.ws2A + slot * P.S_pad + c.s0;
+    for (int s = tid; s < ST; s += NTH)
+        wA[s] = sGAred[s];
+}
+
+}  // namespace race
