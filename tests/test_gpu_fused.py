@@ -74,6 +74,27 @@ def test_fused_forward_backward(dev, case):
     check("dv", vx.grad, ref_dv, BF16_TOL)
 
 
+@pytest.mark.parametrize("block", [32, 64, 96, 160])
+def test_fused_headline_shape_short_blocks(dev, block):
+    """The headline head shape (one query head per kv head, D=64, L=8, K=4, bf16) with blocks of
+    1, 2, 3 and 5 sub-chunks and a ragged last one: the wave-specialised backward totals kernel's
+    prologue, its loop unrolled by two and the trailing odd sub-chunk, against the fp64 oracle."""
+    from race_attention_amd import build_planes_protos, race_causal_attention
+    B, H, T, D, L, Kb = 1, 2, 333, 64, 8, 4
+    print("headline shape, block", block, flush=True)
+    scale = math.sqrt(D)
+    planes_T, _ = build_planes_protos(D, Kb, L, 1, device=dev, seed=3)
+    q, k, v, go = qkv(B, H, H, T, D, seed=block, dev=dev)
+    qx, kx, vx = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out = race_causal_attention(qx, kx, vx, planes_T, L, Kb, scale=scale, eps=EPS, block=block)
+    out.backward(go)
+    ref_out, ref_dq, ref_dk, ref_dv = oracle_layer(q, k, v, bf16_planes(planes_T), L, Kb, scale, EPS, go)
+    check("out", out, ref_out, BF16_TOL)
+    check("dq", qx.grad, ref_dq, BF16_TOL)
+    check("dk", kx.grad, ref_dk, BF16_TOL)
+    check("dv", vx.grad, ref_dv, BF16_TOL)
+
+
 def test_fused_block_invariance_and_determinism(dev):
     from race_attention_amd import build_planes_protos, race_causal_attention
     planes_T, _ = build_planes_protos(64, 4, 8, 1, device=dev, seed=0)
