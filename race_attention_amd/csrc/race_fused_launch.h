@@ -42,6 +42,11 @@ static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStr
         hipLaunchKernelGGL((race_fused_bwd_totals<ST, DP, KB, NWB, false, G1>), grid, block, 0, s, P);
     else if (k == K_BWD_MAIN && (P.dk.f32 || P.dk.stage_f32) != (P.dv.f32 || P.dv.stage_f32))
         return hipErrorInvalidValue;
+    else if (k == K_BWD_MAIN && G1 && ST == 128 && DP == 64 && KB == 4 && !P.dk.f32 && !P.dk.stage_f32) {
+        // wave-specialised variant, bf16 dk and dv: eight state waves and four helper waves
+        if constexpr (G1 && ST == 128 && DP == 64 && KB == 4)
+            hipLaunchKernelGGL((race_fused_bwd_main_ws<ST, DP, KB>), grid, dim3(768), 0, s, P);
+    }
     else if (k == K_BWD_MAIN && (P.dk.f32 || P.dk.stage_f32))
         hipLaunchKernelGGL((race_fused_bwd_main<ST, DP, KB, NWB, true, G1>), grid, block, 0, s, P);
     else if (k == K_BWD_MAIN)

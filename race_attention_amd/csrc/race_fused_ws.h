@@ -421,4 +421,473 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
         wA[s] = sGAred[s];
 }
 
+// Wave-specialised backward main kernel of the fused layer (same shape as the totals kernel
+// above: one query head per kv head, 128-bucket tiles, head dim 64, K = 4, bf16 dk and dv).
+//
+// Same results as race_fused_bwd_main (race_fused.h): dk and dv from the suffix states. Roles:
+//  * eight state waves, wave w owning bucket tile w with its share of St^T and of the suffix
+//    state dS^T in registers (both as [d][s] accumulator tiles): the A scan, W, gW = go St^T +
+//    pK^T Mg^T, gA and its suffix scan, gpK = gAhat + V dS^T + W^T Mg (dS straight from
+//    registers), Mg, Mp and the state updates; they also move the rows (k and q by waves 0-3,
+//    v and go by waves 4-7, two sub-chunks ahead);
+//  * four helper waves: the soft-hash of q one sub-chunk ahead, the soft-hash backward of k one
+//    behind, dk = planes gproj^T, dv = dS^T pK^T + go^T Mp^T and the dk and dv stores (hashing k
+//    on the helpers as well measured 2 % slower: they then set the length of the second phase).
+// Two barrier phases per sub-chunk (the generic kernel has four), three waves per SIMD.
+//
+// Pipeline of sub-chunk s (state waves on s, helpers on s - 1 and s + 1 around it):
+//   X0  state: k, q rows of s + 1 into LDS (waves 0-3); A scan, W -> sW, gW = St go^T,
+//              dS^T -= go^T W (own bucket tile, W read back by the same wave) -> sdS, Mg -> sMg
+//       help:  dk rows of s - 2 out; dv of s - 1 += go^T Mp^T -> sOv; soft-hash backward of k of
+//              s - 1 (gpK rows in sF) -> sGU
+//   X1  state: v, go rows of s + 1 into LDS (waves 4-7); gW += pK^T Mg^T, gA, gpK = W^T Mg +
+//              dS V^T, the gA suffix scan, gpK + gAhat -> sF, Mp -> sMp, St += V^T pK;
+//              soft-hash of k of s + 1 (waves 0-3)
+//       help:  dv rows of s - 1 out; dk of s - 1 -> sOk; dv of s = dS^T pK^T (registers);
+//              soft-hash of q of s + 1
+// Arrays both roles touch in one phase are double buffered by sub-chunk parity (v and go rows,
+// pK, the tanh of the k projections); every other array is written and read in different phases.
+template <int ST, int DP, int KB>
+__global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P)
+{
+    constexpr int NWS = ST / 16;  // state waves: one 16-bucket tile each
+    constexpr int NWH = 4;        // helper waves
+    constexpr int NTH = (NWS + NWH) * 64;
+    constexpr int NTHH = NWH * 64;
+    using CF = FCfg<ST, DP, KB, NWS>;
+    using CH = FCfg<ST, DP, KB, NWH>;
+    constexpr int C = CF::C, R = CF::R, MTC = CF::MTC, NTD = CF::NTD;
+    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG, LDF = ST + 4;
+    constexpr int LDO = DP + 8;
+    static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised backward: 128-bucket tiles, D = 64, K = 4");
+    static_assert(CF::NPT == NWH, "one projection tile of k and of q per helper wave");
+    static_assert(CF::LKP == 32, "one MFMA k step for the dk product");
+    static_assert(CH::CHUNKS == NTHH && CH::PF == 1, "one 16-byte chunk of each row tile per mover thread");
+    static_assert(MTC * MTC == NWH && NWS == 2 * NWH, "Mg on state waves 0-3, Mp on waves 4-7");
+    constexpr int TPH = NTD * MTC / NWH;  // dk and dv tiles per helper wave
+    static_assert(TPH * NWH == NTD * MTC, "dk, dv tiles split evenly over the helper waves");
+
+    __shared__ __align__(16) __bf16 sK[C][LDX];
+    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
+    __shared__ __align__(16) __bf16 sGO[2][C][LDX];  // by sub-chunk parity
+    __shared__ __align__(16) __bf16 sPK[2][C][LDS];  // rows [t][s], by sub-chunk parity
+    __shared__ __align__(16) __bf16 sPQ[C][LDS];
+    __shared__ __align__(16) __bf16 sW[C][LDS];
+    __shared__ __align__(16) __bf16 sdS[ST][LDX];    // dS rows [s][d] after the sub-chunk
+    __shared__ __align__(16) __bf16 sMg[C][LDC];     // Mg as [t][tau]
+    __shared__ __align__(16) __bf16 sMp[C][LDC];     // Mp as [tau][t]
+    __shared__ __align__(16) float sF[C][LDF];       // gpK rows [t][s]
+    __shared__ __align__(16) __bf16 sGU[C][LDG];     // projection gradients of k [t][j]
+    __shared__ __align__(16) __bf16 sOk[C][LDO];     // dk staging
+    __shared__ __align__(16) __bf16 sOv[C][LDO];     // dv staging
+    __shared__ __align__(16) bf16x8 sTri[MTC][64];   // lane-ordered triangle of the A scan
+    // tanh of the k projections, from the soft-hash forward to its backward two phases later, by
+    // sub-chunk parity: [parity][token][table*4 + bit]
+    __shared__ __align__(16) float sThK[2][C][CF::LKP];
+    // planes fragments of state waves 0-3 for their k projection tile, lane-ordered
+    __shared__ __align__(16) bf16x8 sProjK[NWH][DP / 32][64];
+
+    const Ctx c = make_ctx(P, ST);
+    const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
+    const int tid = c.tid, lane = c.lane, wave = c.wave;
+    const bool helper = wave >= NWS;
+    const bool movkq = wave < NWH;
+    const int mid = tid & (NTHH - 1);  // thread index within its group of four waves
+    const int hw = wave - NWS, hid = tid - NWS * 64;  // helper wave / thread index
+    const int nsub = (c.t_end - c.t_begin + C - 1) / C;
+    auto nv_of = [&](int s) { return min(C, c.t_end - (c.t_begin + s * C)); };
+    zero_lds_bf16(&sPK[0][0][0], 2 * C * LDS, tid, NTH);
+    zero_lds_bf16(&sPQ[0][0], C * LDS, tid, NTH);
+    zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
+
+    const int64_t slot = (int64_t)c.z * (P.NB + 1) + c.blk;
+    const int LKtot = P.L * P.K;
+    const int g4 = (lane >> 4) << 2;  // first of the lane's four accumulator rows
+
+    // soft-hash of projection tile tw (token tile tw % MTC, tables 4 (tw / MTC) ..) of the rows in
+    // sX for sub-chunk s -> probability rows of dst, with the planes fragments fp; keep_th: the tanh
+    // of the projections into sThK[s & 1] for the backward
+    auto hash_fwd = [&](const bf16x8 (&fp)[DP / 32], const __bf16 *sX, __bf16 *dst, int tw, int s, bool keep_th) {
+        const int jt = tw / MTC, tt = tw % MTC;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * LDX + (lane >> 4) * 8;
+#pragma unroll
+        for (int kb = 0; kb < DP / 32; ++kb)
+            EngBF16::mma(acc, fp[kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+        const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
+        const bool ok = tok < nv_of(s) && table < c.Lt;
+        float th[4], p[R];
+        softhash_fwd_ct<KB>(acc, coef, ok, th, p);
+        if (keep_th)
+            *reinterpret_cast<f32x4 *>(&sThK[s & 1][tok][table * 4]) = f32x4{th[0], th[1], th[2], th[3]};
+        __bf16 *row = dst + tok * LDS + table * R;
+#pragma unroll
+        for (int h = 0; h < R / 8; ++h) {
+            bf16x8 w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                w[e] = (__bf16)p[8 * h + e];
+            *reinterpret_cast<bf16x8 *>(row + 8 * h) = w;
+        }
+    };
+    // planes fragments of projection tile tw: A operand rows j = table*4 + bit, k = d
+    auto load_proj = [&](bf16x8 (&fp)[DP / 32], int tw) {
+        const int j = (tw / MTC) * 16 + (lane & 15);
+        const int table = j >> 2, bit = j & 3;
+#pragma unroll
+        for (int kb = 0; kb < DP / 32; ++kb) {
+            bf16x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int d = kb * 32 + (lane >> 4) * 8 + e;
+                float x = 0.0f;
+                if (bit < P.K && table < c.Lt && d < P.D)
+                    x = P.planes[d * LKtot + (c.l0 + table) * P.K + bit];
+                f[e] = (__bf16)x;
+            }
+            fp[kb] = f;
+        }
+    };
+
+    // movers: k, q rows (waves 0-3) or v, go rows (waves 4-7) of a sub-chunk; two sets, loaded
+    // two sub-chunks ahead of their staging
+    struct MoveRegs {
+        u32x4 a[1], b[1];
+    };
+    auto load_rows = [&](MoveRegs &m, int s) {
+        const int t0 = c.t_begin + s * C, nv = nv_of(s);
+        if (movkq) {
+            tile_load<CH>(m.a, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, mid);
+            tile_load<CH>(m.b, row_ptr(P.q, c.b, c.hk, t0), P.q.st, nv, mid);
+        } else {
+            tile_load<CH>(m.a, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, mid);
+            tile_load<CH>(m.b, row_ptr(P.go, c.b, c.hk, t0), P.go.st, nv, mid);
+        }
+    };
+    auto stage_rows = [&](const MoveRegs &m, int s) {
+        const int nv = nv_of(s), pb = s & 1;
+        if (movkq) {
+            tile_store_rows<CH>(&sK[0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sQ[0][0], m.b, nv, mid);
+        } else {
+            tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
+        }
+    };
+
+    if (helper) {
+        // ================================================================ helper waves
+        // planes fragments: projection tile hw (k and q), and the dk tiles t = hw + NWH i
+        bf16x8 fp[DP / 32], fb[TPH];
+        load_proj(fp, hw);
+#pragma unroll
+        for (int i = 0; i < TPH; ++i) {
+            const int d = ((hw + NWH * i) / MTC) * 16 + (lane & 15);
+            bf16x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int j = (lane >> 4) * 8 + e;
+                const int table = j >> 2, bit = j & 3;
+                float x = 0.0f;
+                if (bit < P.K && table < c.Lt && d < P.D)
+                    x = P.planes[d * LKtot + (c.l0 + table) * P.K + bit];
+                f[e] = (__bf16)x;
+            }
+            fb[i] = f;
+        }
+        const int hjt = hw / MTC, htt = hw % MTC;
+        f32x4 accV[TPH];
+        AccRows<C, DP, NTHH> ar;  // (bf16 outputs: unused)
+        auto hash_q = [&](int s) { hash_fwd(fp, &sQ[0][0], &sPQ[0][0], hw, s, false); };
+        // soft-hash backward of k for sub-chunk s (gpK rows in sF) -> sGU
+        auto bwd_k = [&](int s) {
+            const int tok = htt * 16 + (lane & 15), table = hjt * 4 + (lane >> 4);
+            float gp[R], p[R], gproj[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int h = 0; h < R / 4; ++h) {
+                const f32x4 x = *reinterpret_cast<const f32x4 *>(&sF[tok][table * R + 4 * h]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    gp[4 * h + e] = x[e];
+            }
+            const f32x4 t4 = *reinterpret_cast<const f32x4 *>(&sThK[s & 1][tok][table * 4]);
+            const float th[4] = {t4[0], t4[1], t4[2], t4[3]};
+            probs_from_th<KB>(th, coef, tok < nv_of(s) && table < c.Lt ? 1.0f : 0.0f, p);
+            softhash_bwd_ct<KB>(th, p, gp, P.inv_scale, gproj);
+            bf16x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = (__bf16)(e < KB ? gproj[e] : 0.0f);
+            *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
+        };
+        // dv^T of sub-chunk s = dS^T pK^T (dS after the sub-chunk) into registers
+        auto dv_part = [&](int s) {
+#pragma unroll
+            for (int i = 0; i < TPH; ++i) {
+                const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
+                accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < ST; kk += 32)
+                    EngBF16::mma(accV[i], ld_tr(&sdS[0][0], LDX, kk, td * 16, lane),
+                                 ld_k(&sPK[s & 1][0][0], LDS, tt * 16, kk, lane));
+            }
+        };
+        // dv^T of sub-chunk s += go^T Mp^T -> sOv
+        auto dv_fin = [&](int s) {
+#pragma unroll
+            for (int i = 0; i < TPH; ++i) {
+                const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
+                EngBF16::mma(accV[i], ld_tr(&sGO[s & 1][0][0], LDX, 0, td * 16, lane),
+                             ld_k(&sMp[0][0], LDC, tt * 16, 0, lane));
+                st_vec4(&sOv[tt * 16 + (lane & 15)][td * 16 + g4], accV[i]);
+            }
+        };
+        // dk^T = P gproj^T -> sOk
+        auto dk_mma = [&]() {
+#pragma unroll
+            for (int i = 0; i < TPH; ++i) {
+                const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                EngBF16::mma(acc, fb[i], *reinterpret_cast<const bf16x8 *>(&sGU[tt * 16 + (lane & 15)][(lane >> 4) * 8]));
+                st_vec4(&sOk[tt * 16 + (lane & 15)][td * 16 + g4], acc);
+            }
+        };
+        auto store_k = [&](int s) {
+            store_out<__bf16, C, DP, LDO, NTHH>(P.dk, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sOk, ar, hid);
+        };
+        auto store_v = [&](int s) {
+            store_out<__bf16, C, DP, LDO, NTHH>(P.dv, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sOv, ar, hid);
+        };
+
+        // the same barrier sequence as the state waves: 2 before the loop, 2 per sub-chunk, 2 after
+        __syncthreads();  // rows of sub-chunk 0 in LDS
+        hash_q(0);
+        __syncthreads();
+        for (int s = 0; s < nsub; ++s) {
+            // X0: dk rows of s - 2 out; dv of s - 1 -> sOv; soft-hash backward of k of s - 1
+            if (s >= 2)
+                store_k(s - 2);
+            if (s >= 1) {
+                dv_fin(s - 1);
+                bwd_k(s - 1);
+            }
+            __syncthreads();
+            // X1: dv rows of s - 1 out; dk of s - 1; dv of s (dS part); soft-hash of s + 1
+            if (s >= 1) {
+                store_v(s - 1);
+                dk_mma();
+            }
+            dv_part(s);
+            if (s + 1 < nsub)
+                hash_q(s + 1);
+            __syncthreads();
+        }
+        if (nsub >= 2)
+            store_k(nsub - 2);
+        dv_fin(nsub - 1);
+        bwd_k(nsub - 1);
+        __syncthreads();
+        store_v(nsub - 1);
+        dk_mma();
+        __syncthreads();
+        store_k(nsub - 1);
+    } else {
+        // ================================================================ state waves
+        const int sb = wave * 16 + g4;  // the lane's four bucket rows
+        // St^T and dS^T at the block start (lane: col s, rows d), A and gAhat at the block start
+        // for the lane's bucket rows (broadcast over the token lanes)
+        f32x4 accS[NTD], accD[NTD];
+        {
+            const float *wB = P.wsB + (slot * P.S_pad + c.s0) * P.DPw;
+            const float *wB2 = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
+            const int s = wave * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < NTD; ++i) {
+                accS[i] = *reinterpret_cast<const f32x4 *>(wB + (int64_t)s * P.DPw + i * 16 + g4);
+                accD[i] = *reinterpret_cast<const f32x4 *>(wB2 + (int64_t)s * P.DPw + i * 16 + g4);
+            }
+        }
+        f32x4 a0 = *reinterpret_cast<const f32x4 *>(P.wsA + slot * P.S_pad + c.s0 + sb);
+        f32x4 ga0 = *reinterpret_cast<const f32x4 *>(P.ws2A + slot * P.S_pad + c.s0 + sb);
+        if (wave < MTC) {
+            const int t = wave * 16 + (lane & 15);
+            bf16x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                f[e] = (__bf16)(((lane >> 4) * 8 + e <= t) ? 1.0f : 0.0f);
+            sTri[wave][lane] = f;
+        }
+        if (movkq) {
+            bf16x8 fp[DP / 32];
+            load_proj(fp, wave);
+#pragma unroll
+            for (int kb = 0; kb < DP / 32; ++kb)
+                sProjK[wave][kb][lane] = fp[kb];
+        }
+        // state waves 0-3: soft-hash of k for sub-chunk s, planes fragments read from LDS
+        auto hash_k = [&](int s) {
+            bf16x8 fp[DP / 32];
+#pragma unroll
+            for (int kb = 0; kb < DP / 32; ++kb)
+                fp[kb] = sProjK[wave][kb][lane];
+            hash_fwd(fp, &sK[0][0], &sPK[s & 1][0][0], wave, s, true);
+        };
+        f32x4 accI[MTC], accW[MTC], accG[MTC], accPK[MTC], accGA[MTC];
+        MoveRegs mA, mB;
+        // rows of sub-chunk 0 into LDS; those of sub-chunks 1 and 2 in flight
+        load_rows(mA, 0);
+        wait_vmem_all();
+        stage_rows(mA, 0);
+        load_rows(mA, min(1, nsub - 1));
+        load_rows(mB, min(2, nsub - 1));
+        __syncthreads();
+        if (movkq)
+            hash_k(0);
+        __syncthreads();
+        // sub-chunk s; set u holds the rows of s + 1 and is refilled with those of s + 3. The
+        // movers issue exactly two loads per sub-chunk and no other vector-memory operation in the
+        // loop, so "at most two outstanding" is exactly the older set.
+        auto body = [&](int s, MoveRegs &u) {
+            const int cur = s & 1, nxt = cur ^ 1;
+            // ---- X0
+            if (movkq) {
+                wait_vmem_older<2>();
+                if (s + 1 < nsub)
+                    stage_rows(u, s + 1);
+                load_rows(u, min(s + 3, nsub - 1));
+            }
+            {
+                const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, wave * 16, lane);
+#pragma unroll
+                for (int tt = 0; tt < MTC; ++tt) {
+                    const int tok = tt * 16 + (lane & 15);
+                    f32x4 a = a0;
+                    EngBF16::mma(a, fPK, sTri[tt][lane]);
+                    if (tt == MTC - 1) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            a0[e] = row_bcast15(a[e]);  // A after the sub-chunk
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accI[tt][e] = frcp(a[e] + P.eps);
+                    const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][sb]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accW[tt][e] = (float)q4[e] * accI[tt][e];
+                    st_vec4(&sW[tok][sb], accW[tt]);
+                    accG[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kd = 0; kd < DP / 32; ++kd)
+                        EngBF16::mma(accG[tt], acc_pair(accS[2 * kd], accS[2 * kd + 1]),
+                                     ld_pair(&sGO[cur][0][0], LDX, tt * 16, 32 * kd, lane));
+                }
+                // dS^T[d][s] -= sum_t go[t][d] W[t][s] over the wave's own bucket tile: W^T read back
+                // from LDS by the wave that wrote it (in-order LDS within a wave)
+                const bf16x8 fWn = EngBF16::neg(ld_tr(&sW[0][0], LDS, 0, wave * 16, lane));
+#pragma unroll
+                for (int i = 0; i < NTD; ++i) {
+                    EngBF16::mma(accD[i], ld_tr(&sGO[cur][0][0], LDX, 0, i * 16, lane), fWn);
+                    st_vec4(&sdS[wave * 16 + (lane & 15)][i * 16 + g4], accD[i]);
+                }
+                if (wave < MTC * MTC) {
+                    // Mg[t][tau] = go_t . v_tau (tau <= t): rows tau (tile tu), cols t (tile tt)
+                    const int tu = wave / MTC, tt = wave % MTC;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<DP, LDX, LDX>(acc, &sV[cur][0][0], tu * 16, &sGO[cur][0][0], tt * 16, lane);
+                    const int tau = tu * 16 + g4, tok = tt * 16 + (lane & 15);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (tau + e > tok)
+                            acc[e] = 0.0f;
+                    st_vec4(&sMg[tok][tau], acc);
+                }
+            }
+            __syncthreads();
+            // ---- X1
+            if (!movkq) {
+                wait_vmem_older<2>();
+                if (s + 1 < nsub)
+                    stage_rows(u, s + 1);
+                load_rows(u, min(s + 3, nsub - 1));
+            }
+            {
+                const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, wave * 16, lane);
+                const bf16x8 fW = ld_tr(&sW[0][0], LDS, 0, wave * 16, lane);
+#pragma unroll
+                for (int tt = 0; tt < MTC; ++tt) {
+                    // gW^T += pK^T Mg^T ; gA = -gW W / (A + eps) ; gpK^T = W^T Mg
+                    EngBF16::mma(accG[tt], fPK, ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        accGA[tt][e] = -(accG[tt][e] * accI[tt][e]) * accW[tt][e];
+                    accPK[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    EngBF16::mma(accPK[tt], fW, ld_tr(&sMg[0][0], LDC, 0, tt * 16, lane));
+                }
+                // gAhat_t = gAhat_start - sum_{tau < t} gA_tau: a token tile's 16 tokens lie along the
+                // 16 lanes of a DPP row, so fp32 row scans, with token tile 0's row total carried into
+                // tile 1; the sub-chunk's end value seeds the next sub-chunk
+                {
+                    f32x4 carry = {0.f, 0.f, 0.f, 0.f}, gend;
+#pragma unroll
+                    for (int tt = 0; tt < MTC; ++tt) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float inc = row_scan16(accGA[tt][e]) + carry[e];
+                            gend[e] = ga0[e] - inc;
+                            accGA[tt][e] += gend[e];
+                            if (tt + 1 < MTC)
+                                carry[e] = row_bcast15(inc);
+                        }
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        ga0[e] = row_bcast15(gend[e]);
+                }
+                // gpK^T += dS V^T (dS after the sub-chunk, from registers) ; + gAhat -> sF
+#pragma unroll
+                for (int tt = 0; tt < MTC; ++tt) {
+#pragma unroll
+                    for (int kd = 0; kd < DP / 32; ++kd)
+                        EngBF16::mma(accPK[tt], acc_pair(accD[2 * kd], accD[2 * kd + 1]),
+                                     ld_pair(&sV[cur][0][0], LDX, tt * 16, 32 * kd, lane));
+                    *reinterpret_cast<f32x4 *>(&sF[tt * 16 + (lane & 15)][sb]) = accPK[tt] + accGA[tt];
+                }
+                if (wave >= NWS - MTC * MTC) {
+                    // Mp[tau][t] = pK_tau . W_t (t >= tau): rows t (tile ta), cols tau (tile tb)
+                    const int m = wave - (NWS - MTC * MTC), ta = m / MTC, tb = m % MTC;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    mma_ab<ST, LDS, LDS>(acc, &sW[0][0], ta * 16, &sPK[cur][0][0], tb * 16, lane);
+                    const int r0 = ta * 16 + g4, c0 = tb * 16 + (lane & 15);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (r0 + e < c0)
+                            acc[e] = 0.0f;
+                    st_vec4(&sMp[c0][r0], acc);
+                }
+                // St^T[d][s] += sum_t V[t][d] pK[t][s]
+#pragma unroll
+                for (int i = 0; i < NTD; ++i)
+                    EngBF16::mma(accS[i], ld_tr(&sV[cur][0][0], LDX, 0, i * 16, lane), fPK);
+            }
+            if (movkq && s + 1 < nsub)
+                hash_k(s + 1);
+            __syncthreads();
+        };
+        // unrolled by two, both halves unconditional inside the loop: each register set is named
+        // statically and the loop edge sees the same loads on every path
+        int s = 0;
+        for (; s + 1 < nsub; s += 2) {
+            body(s, mA);
+            body(s + 1, mB);
+        }
+        if (s < nsub)
+            body(s, mA);
+        wait_vmem_all();  // (the re-read rows past the end)
+        __syncthreads();
+        __syncthreads();
+    }
+}
+
 }  // namespace race
