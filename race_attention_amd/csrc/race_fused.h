@@ -556,13 +556,15 @@ void race_fused_fwd_readout(const ScanParams P)
 {
     using CF = FCfg<ST, DP, KB, NW>;
     constexpr int C = CF::C, NTH = CF::NTH, R = CF::R, MTC = CF::MTC;
-    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS;
+    // pK rows at a pitch of ST + 16 elements: its 16-byte MFMA operand reads (the triu product) hit
+    // every bank once per pass (two-way conflicts at ST + 8)
+    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDK = CF::LDS + 8;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
     __shared__ __align__(16) __bf16 sK[C][LDX];
     __shared__ __align__(16) __bf16 sQ[C][LDX];
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // v rows, double buffered
-    __shared__ __align__(16) __bf16 sPK[C][LDS];     // rows [t][s]
+    __shared__ __align__(16) __bf16 sPK[C][LDK];     // rows [t][s]
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
     __shared__ __align__(16) __bf16 sPm[C][LDC];
     // W (written in P2, read in P3) and the output staging (written in P4, read in the next
@@ -579,7 +581,7 @@ void race_fused_fwd_readout(const ScanParams P)
     constexpr int TPW_P0 = (2 * CF::NPT + NW - 1) / NW;
     FusedFrags<CF, DP, TPW_P0> fr;
     fr.load(P, c.l0, c.Lt, lane, wave);
-    zero_lds_bf16(&sPK[0][0], C * LDS, tid, NTH);
+    zero_lds_bf16(&sPK[0][0], C * LDK, tid, NTH);
     zero_lds_bf16(&sPQ[0][0], C * LDS, tid, NTH);
 
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;  // state tiles [ST x DP]
@@ -706,7 +708,7 @@ void race_fused_fwd_readout(const ScanParams P)
                     const int s = ts * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
                     if (g == 0) {
                         f32x4 a = *reinterpret_cast<const f32x4 *>(&sA0[cur][s]);
-                        EngBF16::mma(a, ld_tr(&sPK[0][0], LDS, 0, ts * 16, lane), fr.tri_of(tt));
+                        EngBF16::mma(a, ld_tr(&sPK[0][0], LDK, 0, ts * 16, lane), fr.tri_of(tt));
                         if (tt == MTC - 1 && (lane & 15) == 15)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
@@ -740,7 +742,7 @@ void race_fused_fwd_readout(const ScanParams P)
                 if (t < MTC * MTC) {
                     const int tu = t / MTC, tt = t % MTC;  // rows tau, cols t
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<ST, LDS, LDS>(acc, &sPK[0][0], tu * 16, &sW[0][0], tt * 16, lane);
+                    mma_ab<ST, LDK, LDS>(acc, &sPK[0][0], tu * 16, &sW[0][0], tt * 16, lane);
                     const int tau = tu * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -754,7 +756,7 @@ void race_fused_fwd_readout(const ScanParams P)
                 for (int i = 0; i < TPW_S; ++i) {
                     const int t = wave + i * NW;
                     if (t < CF::NTS * CF::NTD)
-                        EngBF16::mma(accS[i], ld_tr(&sPK[0][0], LDS, 0, (t / CF::NTD) * 16, lane),
+                        EngBF16::mma(accS[i], ld_tr(&sPK[0][0], LDK, 0, (t / CF::NTD) * 16, lane),
                                      ld_tr(&sV[cur][0][0], LDX, 0, (t % CF::NTD) * 16, lane));
                 }
             }

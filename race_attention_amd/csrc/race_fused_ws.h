@@ -41,6 +41,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     using CH = FCfg<ST, DP, KB, NWH>;  // row loads and staging: 256 threads per pair of row arrays
     constexpr int C = CF::C, R = CF::R, MTC = CF::MTC, NTD = CF::NTD;
     constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG;
+    // Mg rows at a pitch of C + 16 elements: its 16-byte MFMA operand reads hit every bank once per
+    // pass (two-way conflicts at C + 8)
+    constexpr int LDM = C + 16;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
     static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised totals: 128-bucket tiles, D = 64, K = 4");
@@ -58,7 +61,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     __shared__ __align__(16) __bf16 sPK[2][C][LDS];  // rows [t][s], by sub-chunk parity
     __shared__ __align__(16) __bf16 sPQ[2][C][LDS];
     __shared__ __align__(16) __bf16 sW[C][LDS];
-    __shared__ __align__(16) __bf16 sMg[C][LDC];     // Mg as [t][tau]
+    __shared__ __align__(16) __bf16 sMg[C][LDM];     // Mg as [t][tau]
     __shared__ __align__(16) float sGP[C][ST + 4];   // gpQ rows [t][s]
     __shared__ __align__(16) __bf16 sGU[C][LDG];     // projection gradients of q [t][j]
     __shared__ __align__(16) OT sO[C][LDO];          // dq staging
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
 #pragma unroll
             for (int tt = 0; tt < MTC; ++tt) {
                 const int sb = wave * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-                EngBF16::mma(accG[tt], fPK, ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
+                EngBF16::mma(accG[tt], fPK, ld_k(&sMg[0][0], LDM, tt * 16, 0, lane));
                 const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[cur][tok][sb]);
                 f32x4 gpq;
 #pragma unroll
@@ -457,7 +460,11 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     using CF = FCfg<ST, DP, KB, NWS>;
     using CH = FCfg<ST, DP, KB, NWH>;
     constexpr int C = CF::C, R = CF::R, MTC = CF::MTC, NTD = CF::NTD;
-    constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG, LDF = ST + 4;
+    constexpr int LDX = CF::LDX, LDS = CF::LDS, LDG = CF::LDG;
+    // row pitches of pK, Mg / Mp and the fp32 gpK rows. pK is read mostly as 16-byte MFMA operand
+    // rows (16 rows x 32 k per read): with a pitch of ST + 16 elements (an odd multiple of 32 bytes)
+    // those reads hit all 64 banks once per pass, with ST + 8 two-way (measured 1.7 % faster)
+    constexpr int LDK = ST + 16, LDM = C + 8, LDF = ST + 4;
     constexpr int LDO = DP + 8;
     static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised backward: 128-bucket tiles, D = 64, K = 4");
     static_assert(CF::NPT == NWH, "one projection tile of k and of q per helper wave");
@@ -471,12 +478,12 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     __shared__ __align__(16) __bf16 sQ[C][LDX];
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
     __shared__ __align__(16) __bf16 sGO[2][C][LDX];  // by sub-chunk parity
-    __shared__ __align__(16) __bf16 sPK[2][C][LDS];  // rows [t][s], by sub-chunk parity
+    __shared__ __align__(16) __bf16 sPK[2][C][LDK];  // rows [t][s], by sub-chunk parity
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
     __shared__ __align__(16) __bf16 sW[C][LDS];
     __shared__ __align__(16) __bf16 sdS[ST][LDX];    // dS rows [s][d] after the sub-chunk
-    __shared__ __align__(16) __bf16 sMg[C][LDC];     // Mg as [t][tau]
-    __shared__ __align__(16) __bf16 sMp[C][LDC];     // Mp as [tau][t]
+    __shared__ __align__(16) __bf16 sMg[C][LDM];     // Mg as [t][tau]
+    __shared__ __align__(16) __bf16 sMp[C][LDM];     // Mp as [tau][t]
     __shared__ __align__(16) float sF[C][LDF];       // gpK rows [t][s]
     __shared__ __align__(16) __bf16 sGU[C][LDG];     // projection gradients of k [t][j]
     __shared__ __align__(16) __bf16 sOk[C][LDO];     // dk staging
@@ -497,7 +504,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     const int hw = wave - NWS, hid = tid - NWS * 64;  // helper wave / thread index
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     auto nv_of = [&](int s) { return min(C, c.t_end - (c.t_begin + s * C)); };
-    zero_lds_bf16(&sPK[0][0][0], 2 * C * LDS, tid, NTH);
+    zero_lds_bf16(&sPK[0][0][0], 2 * C * LDK, tid, NTH);
     zero_lds_bf16(&sPQ[0][0], C * LDS, tid, NTH);
     zero_lds_bf16(&sGU[0][0], C * LDG, tid, NTH);
 
@@ -508,7 +515,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     // soft-hash of projection tile tw (token tile tw % MTC, tables 4 (tw / MTC) ..) of the rows in
     // sX for sub-chunk s -> probability rows of dst, with the planes fragments fp; keep_th: the tanh
     // of the projections into sThK[s & 1] for the backward
-    auto hash_fwd = [&](const bf16x8 (&fp)[DP / 32], const __bf16 *sX, __bf16 *dst, int tw, int s, bool keep_th) {
+    auto hash_fwd = [&](const bf16x8 (&fp)[DP / 32], const __bf16 *sX, __bf16 *dst, int ldd, int tw, int s, bool keep_th) {
         const int jt = tw / MTC, tt = tw % MTC;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * LDX + (lane >> 4) * 8;
@@ -521,7 +528,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         softhash_fwd_ct<KB>(acc, coef, ok, th, p);
         if (keep_th)
             *reinterpret_cast<f32x4 *>(&sThK[s & 1][tok][table * 4]) = f32x4{th[0], th[1], th[2], th[3]};
-        __bf16 *row = dst + tok * LDS + table * R;
+        __bf16 *row = dst + tok * ldd + table * R;
 #pragma unroll
         for (int h = 0; h < R / 8; ++h) {
             bf16x8 w;
@@ -599,7 +606,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         const int hjt = hw / MTC, htt = hw % MTC;
         f32x4 accV[TPH];
         AccRows<C, DP, NTHH> ar;  // (bf16 outputs: unused)
-        auto hash_q = [&](int s) { hash_fwd(fp, &sQ[0][0], &sPQ[0][0], hw, s, false); };
+        auto hash_q = [&](int s) { hash_fwd(fp, &sQ[0][0], &sPQ[0][0], LDS, hw, s, false); };
         // soft-hash backward of k for sub-chunk s (gpK rows in sF) -> sGU
         auto bwd_k = [&](int s) {
             const int tok = htt * 16 + (lane & 15), table = hjt * 4 + (lane >> 4);
@@ -630,7 +637,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
 #pragma unroll
                 for (int kk = 0; kk < ST; kk += 32)
                     EngBF16::mma(accV[i], ld_tr(&sdS[0][0], LDX, kk, td * 16, lane),
-                                 ld_k(&sPK[s & 1][0][0], LDS, tt * 16, kk, lane));
+                                 ld_k(&sPK[s & 1][0][0], LDK, tt * 16, kk, lane));
             }
         };
         // dv^T of sub-chunk s += go^T Mp^T -> sOv
@@ -639,7 +646,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
             for (int i = 0; i < TPH; ++i) {
                 const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
                 EngBF16::mma(accV[i], ld_tr(&sGO[s & 1][0][0], LDX, 0, td * 16, lane),
-                             ld_k(&sMp[0][0], LDC, tt * 16, 0, lane));
+                             ld_k(&sMp[0][0], LDM, tt * 16, 0, lane));
                 st_vec4(&sOv[tt * 16 + (lane & 15)][td * 16 + g4], accV[i]);
             }
         };
@@ -731,7 +738,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
 #pragma unroll
             for (int kb = 0; kb < DP / 32; ++kb)
                 fp[kb] = sProjK[wave][kb][lane];
-            hash_fwd(fp, &sK[0][0], &sPK[s & 1][0][0], wave, s, true);
+            hash_fwd(fp, &sK[0][0], &sPK[s & 1][0][0], LDK, wave, s, true);
         };
         f32x4 accI[MTC], accW[MTC], accG[MTC], accPK[MTC], accGA[MTC];
         MoveRegs mA, mB;
@@ -758,7 +765,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 load_rows(u, min(s + 3, nsub - 1));
             }
             {
-                const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, wave * 16, lane);
+                const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDK, 0, wave * 16, lane);
 #pragma unroll
                 for (int tt = 0; tt < MTC; ++tt) {
                     const int tok = tt * 16 + (lane & 15);
@@ -813,17 +820,17 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 load_rows(u, min(s + 3, nsub - 1));
             }
             {
-                const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, wave * 16, lane);
+                const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDK, 0, wave * 16, lane);
                 const bf16x8 fW = ld_tr(&sW[0][0], LDS, 0, wave * 16, lane);
 #pragma unroll
                 for (int tt = 0; tt < MTC; ++tt) {
                     // gW^T += pK^T Mg^T ; gA = -gW W / (A + eps) ; gpK^T = W^T Mg
-                    EngBF16::mma(accG[tt], fPK, ld_k(&sMg[0][0], LDC, tt * 16, 0, lane));
+                    EngBF16::mma(accG[tt], fPK, ld_k(&sMg[0][0], LDM, tt * 16, 0, lane));
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         accGA[tt][e] = -(accG[tt][e] * accI[tt][e]) * accW[tt][e];
                     accPK[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    EngBF16::mma(accPK[tt], fW, ld_tr(&sMg[0][0], LDC, 0, tt * 16, lane));
+                    EngBF16::mma(accPK[tt], fW, ld_tr(&sMg[0][0], LDM, 0, tt * 16, lane));
                 }
                 // gAhat_t = gAhat_start - sum_{tau < t} gA_tau: a token tile's 16 tokens lie along the
                 // 16 lanes of a DPP row, so fp32 row scans, with token tile 0's row total carried into
@@ -858,7 +865,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                     // Mp[tau][t] = pK_tau . W_t (t >= tau): rows t (tile ta), cols tau (tile tb)
                     const int m = wave - (NWS - MTC * MTC), ta = m / MTC, tb = m % MTC;
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<ST, LDS, LDS>(acc, &sW[0][0], ta * 16, &sPK[cur][0][0], tb * 16, lane);
+                    mma_ab<ST, LDS, LDK>(acc, &sW[0][0], ta * 16, &sPK[cur][0][0], tb * 16, lane);
                     const int r0 = ta * 16 + g4, c0 = tb * 16 + (lane & 15);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
