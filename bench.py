@@ -35,8 +35,8 @@ FP32_PEAK = 157.3e12   # dense fp32 MFMA flop/s
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--T", type=int, default=1 << 20)
     ap.add_argument("--B", type=int, default=1)
     ap.add_argument("--H", type=int, default=4)

@@ -265,8 +265,9 @@ RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int 
     }
 }
 
-// Tile rows into LDS, rows at and beyond nv as zeros.
-template <class CF>
+// Tile rows into LDS, rows at and beyond nv as zeros (ZERO) or as loaded (copies of row nv - 1:
+// finite values that every consumer multiplies by the zero probabilities of padding tokens).
+template <class CF, bool ZERO = true>
 RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int tid)
 {
     constexpr int CH = CF::CHUNKS / CF::C;
@@ -274,7 +275,7 @@ RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int
     for (int i = 0; i < CF::PF; ++i) {
         const int idx = tid + i * CF::NTH;
         if (idx < CF::CHUNKS) {
-            const bool ok = idx / CH < nv;
+            const bool ok = !ZERO || idx / CH < nv;
             const u32x4 x = {ok ? r[i][0] : 0u, ok ? r[i][1] : 0u, ok ? r[i][2] : 0u, ok ? r[i][3] : 0u};
             *reinterpret_cast<u32x4 *>(dst + (idx / CH) * CF::LDX + (idx % CH) * 8) = x;
         }
@@ -295,7 +296,8 @@ RACE_DEV float row_scan16(float v)
 // Value of lane 15 of each 16-lane DPP row, in every lane of that row (row_newbcast:15).
 RACE_DEV float row_bcast15(float v)
 {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x15F, 0xF, 0xF, false));
+    // every lane has a source lane: no old value to keep (and no zero move ahead of the DPP move)
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x15F, 0xF, 0xF, false));
 }
 
 // s_waitcnt vmcnt(0): every vector-memory operation of the wave has completed. Issued once
