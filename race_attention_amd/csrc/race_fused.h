@@ -265,9 +265,11 @@ RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int 
     }
 }
 
-// Tile rows into LDS, rows at and beyond nv as zeros (ZERO) or as loaded (copies of row nv - 1:
-// finite values that every consumer multiplies by the zero probabilities of padding tokens).
-template <class CF, bool ZERO = true>
+// Tile rows into LDS, rows at and beyond nv as loaded (copies of row nv - 1) or, with ZERO, as
+// zeros. The copies are finite, and every product the fused kernels form with a padding token's
+// row is multiplied by that token's zero probabilities (pK, pQ and so W are masked to zero by the
+// soft-hash), or lands in an output row that is not stored: no kernel needs the zeros.
+template <class CF, bool ZERO = false>
 RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int tid)
 {
     constexpr int CH = CF::CHUNKS / CF::C;

@@ -226,11 +226,11 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     auto stage_rows = [&](const MoveRegs &m, int s) {  // movers: registers into LDS (v, go by parity)
         const int nv = nv_of(s), pb = s & 1;
         if (movkq) {
-            tile_store_rows<CH, false>(&sK[0][0], m.a, nv, mid);
-            tile_store_rows<CH, false>(&sQ[0][0], m.b, nv, mid);
+            tile_store_rows<CH>(&sK[0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sQ[0][0], m.b, nv, mid);
         } else {
-            tile_store_rows<CH, false>(&sV[pb][0][0], m.a, nv, mid);
-            tile_store_rows<CH, false>(&sGO[pb][0][0], m.b, nv, mid);
+            tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
         }
     };
     // movers at the top of a sub-chunk: wait for the set holding the rows of the next sub-chunk,
@@ -623,11 +623,11 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     auto stage_rows = [&](const MoveRegs &m, int s) {
         const int nv = nv_of(s), pb = s & 1;
         if (movkq) {
-            tile_store_rows<CH, false>(&sK[0][0], m.a, nv, mid);
-            tile_store_rows<CH, false>(&sQ[0][0], m.b, nv, mid);
+            tile_store_rows<CH>(&sK[0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sQ[0][0], m.b, nv, mid);
         } else {
-            tile_store_rows<CH, false>(&sV[pb][0][0], m.a, nv, mid);
-            tile_store_rows<CH, false>(&sGO[pb][0][0], m.b, nv, mid);
+            tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
+            tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
         }
     };
 
