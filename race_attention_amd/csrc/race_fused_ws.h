@@ -498,7 +498,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
 //              soft-hash of q of s + 1
 // Arrays both roles touch in one phase are double buffered by sub-chunk parity (v and go rows,
 // pK, the tanh of the k projections); every other array is written and read in different phases.
-template <int ST, int DP, int KB>
+template <int ST, int DP, int KB, bool OUT_F32>
 __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P)
 {
     constexpr int NWS = ST / 16;  // state waves: one 16-bucket tile each
@@ -513,7 +513,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     // rows (16 rows x 32 k per read): with a pitch of ST + 16 elements (an odd multiple of 32 bytes)
     // those reads hit all 64 banks once per pass, with ST + 8 two-way (measured 1.7 % faster)
     constexpr int LDK = ST + 16, LDM = C + 8, LDF = ST + 4;
-    constexpr int LDO = DP + 8;
+    using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
+    constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
     static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised backward: 128-bucket tiles, D = 64, K = 4");
     static_assert(CF::NPT == NWH, "one projection tile of k and of q per helper wave");
     static_assert(CF::LKP == 32, "one MFMA k step for the dk product");
@@ -534,8 +535,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     __shared__ __align__(16) __bf16 sMp[C][LDM];     // Mp as [tau][t]
     __shared__ __align__(16) float sF[C][LDF];       // gpK rows [t][s]
     __shared__ __align__(16) __bf16 sGU[C][LDG];     // projection gradients of k [t][j]
-    __shared__ __align__(16) __bf16 sOk[C][LDO];     // dk staging
-    __shared__ __align__(16) __bf16 sOv[C][LDO];     // dv staging
+    __shared__ __align__(16) OT sOk[C][LDO];         // dk staging
+    __shared__ __align__(16) OT sOv[C][LDO];         // dv staging
     __shared__ __align__(16) bf16x8 sTri[MTC][64];   // lane-ordered triangle of the A scan
     // tanh of the k projections, from the soft-hash forward to its backward two phases later, by
     // sub-chunk parity: [parity][token][table*4 + bit]
@@ -653,7 +654,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         }
         const int hjt = hw / MTC, htt = hw % MTC;
         f32x4 accV[TPH];
-        AccRows<C, DP, NTHH> ar;  // (bf16 outputs: unused)
+        // (bucket tiles launched one after another) the earlier tiles' fp32 sums of the dk and dv
+        // rows, loaded a barrier phase before their stores
+        AccRows<C, DP, NTHH> arK, arV;
         auto hash_q = [&](int s) { hash_fwd(fp, &sQ[0][0], &sPQ[0][0], LDS, hw, s, false); };
         // soft-hash backward of k for sub-chunk s (gpK rows in sF) -> sGU
         auto bwd_k = [&](int s) {
@@ -695,7 +698,10 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
                 EngBF16::mma(accV[i], ld_tr(&sGO[s & 1][0][0], LDX, 0, td * 16, lane),
                              ld_k(&sMp[0][0], LDM, tt * 16, 0, lane));
-                st_vec4(&sOv[tt * 16 + (lane & 15)][td * 16 + g4], accV[i]);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sOv[tt * 16 + (lane & 15)][td * 16 + g4]) = accV[i];
+                else
+                    st_vec4(&sOv[tt * 16 + (lane & 15)][td * 16 + g4], accV[i]);
             }
         };
         // dk^T = P gproj^T -> sOk
@@ -705,14 +711,29 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
                 EngBF16::mma(acc, fb[i], *reinterpret_cast<const bf16x8 *>(&sGU[tt * 16 + (lane & 15)][(lane >> 4) * 8]));
-                st_vec4(&sOk[tt * 16 + (lane & 15)][td * 16 + g4], acc);
+                if constexpr (OUT_F32)
+                    *reinterpret_cast<f32x4 *>(&sOk[tt * 16 + (lane & 15)][td * 16 + g4]) = acc;
+                else
+                    st_vec4(&sOk[tt * 16 + (lane & 15)][td * 16 + g4], acc);
             }
         };
         auto store_k = [&](int s) {
-            store_out<__bf16, C, DP, LDO, NTHH>(P.dk, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sOk, ar, hid);
+            store_out<OT, C, DP, LDO, NTHH>(P.dk, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sOk, arK, hid);
         };
         auto store_v = [&](int s) {
-            store_out<__bf16, C, DP, LDO, NTHH>(P.dv, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sOv, ar, hid);
+            store_out<OT, C, DP, LDO, NTHH>(P.dv, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sOv, arV, hid);
+        };
+        auto acc_k = [&](int s) {
+            if constexpr (OUT_F32) {
+                if (P.dk.stage_f32)
+                    arK.load(P.dk, c.b, c.hk, c.t_begin + s * C, nv_of(s), hid);
+            }
+        };
+        auto acc_v = [&](int s) {
+            if constexpr (OUT_F32) {
+                if (P.dv.stage_f32)
+                    arV.load(P.dv, c.b, c.hk, c.t_begin + s * C, nv_of(s), hid);
+            }
         };
 
         // the same barrier sequence as the state waves: 2 before the loop, 2 per sub-chunk, 2 after
@@ -721,6 +742,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         __syncthreads();
         for (int s = 0; s < nsub; ++s) {
             // X0: dk rows of s - 2 out; dv of s - 1 -> sOv; soft-hash backward of k of s - 1
+            if (s >= 1)
+                acc_v(s - 1);
             if (s >= 2)
                 store_k(s - 2);
             if (s >= 1) {
@@ -730,6 +753,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
             __syncthreads();
             // X1: dv rows of s - 1 out; dk of s - 1; dv of s (dS part); soft-hash of s + 1
             if (s >= 1) {
+                acc_k(s - 1);
                 store_v(s - 1);
                 dk_mma();
             }
@@ -738,11 +762,13 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 hash_q(s + 1);
             __syncthreads();
         }
+        acc_v(nsub - 1);
         if (nsub >= 2)
             store_k(nsub - 2);
         dv_fin(nsub - 1);
         bwd_k(nsub - 1);
         __syncthreads();
+        acc_k(nsub - 1);
         store_v(nsub - 1);
         dk_mma();
         __syncthreads();
