@@ -95,6 +95,9 @@ struct FCfg {
     static constexpr int NTD = DP / 16;
     static constexpr int NPT = NJT * MTC;      // projection tiles per tensor
     static constexpr int LDX = DP + 8;         // bf16 rows of tokens
+    // k and q rows, read only as projection operands (16-byte MFMA reads): a pitch of DP + 16
+    // elements keeps those reads conflict-free (0.5 % per layer step over DP + 8)
+    static constexpr int LDQ = DP + 16;
     static constexpr int LDC = C + 8;          // bf16 rows of length C
     static constexpr int LDS = ST + 8;         // bf16 rows of length ST
     static constexpr int LDG = ((LKP + 31) / 32) * 32 + 8;  // rows of projection grads (whole MFMA k steps)
@@ -162,7 +165,7 @@ template <class CF, int DP, int NSLOT>
 RACE_DEV f32x4 proj_T(const FusedFrags<CF, DP, NSLOT> &fr, int i, const __bf16 *sX, int tt, int lane)
 {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDX + (lane >> 4) * 8;
+    const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDQ + (lane >> 4) * 8;
 #pragma unroll
     for (int kb = 0; kb < DP / 32; ++kb)
         EngBF16::mma(acc, fr.proj[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
@@ -269,7 +272,7 @@ RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int 
 // zeros. The copies are finite, and every product the fused kernels form with a padding token's
 // row is multiplied by that token's zero probabilities (pK, pQ and so W are masked to zero by the
 // soft-hash), or lands in an output row that is not stored: no kernel needs the zeros.
-template <class CF, bool ZERO = false>
+template <class CF, bool ZERO = false, int LD = CF::LDX>
 RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int tid)
 {
     constexpr int CH = CF::CHUNKS / CF::C;
@@ -279,7 +282,7 @@ RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int
         if (idx < CF::CHUNKS) {
             const bool ok = !ZERO || idx / CH < nv;
             const u32x4 x = {ok ? r[i][0] : 0u, ok ? r[i][1] : 0u, ok ? r[i][2] : 0u, ok ? r[i][3] : 0u};
-            *reinterpret_cast<u32x4 *>(dst + (idx / CH) * CF::LDX + (idx % CH) * 8) = x;
+            *reinterpret_cast<u32x4 *>(dst + (idx / CH) * LD + (idx % CH) * 8) = x;
         }
     }
 }
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
 {
     using CF = FCfg<ST, DP, KB, NW>;
     constexpr int C = CF::C, NTH = CF::NTH, R = CF::R;
-    __shared__ __align__(16) __bf16 sK[C][CF::LDX];
+    __shared__ __align__(16) __bf16 sK[C][CF::LDQ];
     __shared__ __align__(16) __bf16 sV[2][C][CF::LDX];  // by sub-chunk parity
     __shared__ __align__(16) __bf16 sPK[C][CF::LDS];  // rows [t][s]
 
@@ -466,7 +469,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     const int t_last = c.t_begin + (nsub - 1) * C;  // start of the last sub-chunk
     load_rows(pkB, pvB, c.t_begin);
     wait_vmem_all();
-    tile_store_rows<CF>(&sK[0][0], pkB, min(C, c.t_end - c.t_begin), tid);
+    tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pkB, min(C, c.t_end - c.t_begin), tid);
     tile_store_rows<CF>(&sV[0][0][0], pvB, min(C, c.t_end - c.t_begin), tid);
     load_rows(pkA, pvA, min(c.t_begin + C, t_last));
     __syncthreads();
@@ -521,7 +524,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
         // nothing reads): every prefetch set is consumed on every path, so the compiler's
         // memory-counter tracking needs no wait before the set is loaded again
         wait_vmem_older<2 * CF::PF>();
-        tile_store_rows<CF>(&sK[0][0], nk, min(C, c.t_end - t0 - C), tid);
+        tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], nk, min(C, c.t_end - t0 - C), tid);
         tile_store_rows<CF>(&sV[nxt][0][0], nvr, min(C, c.t_end - t0 - C), tid);
         __syncthreads();
     };
@@ -565,8 +568,8 @@ void race_fused_fwd_readout(const ScanParams P)
     constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDK = CF::LDS + 8;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
-    __shared__ __align__(16) __bf16 sK[C][LDX];
-    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sK[C][CF::LDQ];
+    __shared__ __align__(16) __bf16 sQ[C][CF::LDQ];
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // v rows, double buffered
     __shared__ __align__(16) __bf16 sPK[C][LDK];     // rows [t][s]
     __shared__ __align__(16) __bf16 sPQ[C][LDS];
@@ -629,8 +632,8 @@ void race_fused_fwd_readout(const ScanParams P)
         tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, nv0, tid);
         tile_load<CF>(pq, row_ptr(P.q, c.b, c.hk * G, c.t_begin), P.q.st, nv0, tid);
         tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, nv0, tid);
-        tile_store_rows<CF>(&sK[0][0], pk, nv0, tid);
-        tile_store_rows<CF>(&sQ[0][0], pq, nv0, tid);
+        tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pk, nv0, tid);
+        tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pq, nv0, tid);
         tile_store_rows<CF>(&sV[0][0][0], pv, nv0, tid);
     }
     wait_vmem_all();
@@ -656,7 +659,7 @@ void race_fused_fwd_readout(const ScanParams P)
             if (g > 0) {  // further query heads of the group: load q synchronously
                 u32x4 tq[CF::PF];
                 tile_load<CF>(tq, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
-                tile_store_rows<CF>(&sQ[0][0], tq, nv, tid);
+                tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], tq, nv, tid);
                 __syncthreads();
             }
             // ---- P1: soft-hash of k (first head only) and q; previous output rows to HBM
@@ -784,14 +787,14 @@ void race_fused_fwd_readout(const ScanParams P)
             if (g == G - 1) {
                 if (more) {
                     const int nv1 = min(C, c.t_end - t0 - C);
-                    tile_store_rows<CF>(&sK[0][0], pk, nv1, tid);
+                    tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pk, nv1, tid);
                     tile_store_rows<CF>(&sV[nxt][0][0], pv, nv1, tid);
                     if (G == 1)
-                        tile_store_rows<CF>(&sQ[0][0], pq, nv1, tid);
+                        tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pq, nv1, tid);
                     else {
                         u32x4 tq[CF::PF];
                         tile_load<CF>(tq, row_ptr(P.q, c.b, c.hk * G, t0 + C), P.q.st, nv1, tid);
-                        tile_store_rows<CF>(&sQ[0][0], tq, nv1, tid);
+                        tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], tq, nv1, tid);
                     }
                 }
             }
@@ -907,8 +910,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     constexpr int LDX = CF::LDX, LDC = CF::LDC, LDS = CF::LDS, LDG = CF::LDG;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
-    __shared__ __align__(16) __bf16 sK[C][LDX];
-    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sK[C][CF::LDQ];
+    __shared__ __align__(16) __bf16 sQ[C][CF::LDQ];
     __shared__ __align__(16) __bf16 sV[C][LDX];
     __shared__ __align__(16) __bf16 sGO[C][LDX];
     __shared__ __align__(16) __bf16 sPK[C][LDS];   // rows [t][s]
@@ -1057,10 +1060,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             //          | T4 of the previous step
             wait_vmem_all();
             if (g == 0) {
-                tile_store_rows<CF>(&sK[0][0], pf.k, nv, tid);
+                tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pf.k, nv, tid);
                 tile_store_rows<CF>(&sV[0][0], pf.v, nv, tid);
             }
-            tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
+            tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pf.q, nv, tid);
             tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
             // (tiles one launch after another) the earlier tiles' sum of the previous step's dq
             // rows, stored in P2; issued before the row prefetch so that waiting for it does not
@@ -1272,8 +1275,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     float(*sF)[LDF] = reinterpret_cast<float(*)[LDF]>(uF);
     __bf16(*sGAh)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uF);
     __bf16(*sGAl)[LDS] = reinterpret_cast<__bf16(*)[LDS]>(uF + SZ_PQ);
-    __shared__ __align__(16) __bf16 sK[C][LDX];
-    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sK[C][CF::LDQ];
+    __shared__ __align__(16) __bf16 sQ[C][CF::LDQ];
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
     // go rows; two buffers by step parity where the go^T Mp^T product of a step is deferred to
     // the next step's first phase (one wave per bucket tile)
@@ -1481,10 +1484,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             // ---- H0: rows into LDS (their loads were issued a step ago) | T5 of the previous sub-chunk
             wait_vmem_all();
             if (g == 0) {
-                tile_store_rows<CF>(&sK[0][0], pf.k, nv, tid);
+                tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pf.k, nv, tid);
                 tile_store_rows<CF>(&sV[cur][0][0], pf.v, nv, tid);
             }
-            tile_store_rows<CF>(&sQ[0][0], pf.q, nv, tid);
+            tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pf.q, nv, tid);
             tile_store_rows<CF>(&sGO[gb][0][0], pf.g, nv, tid);
             // (tiles one launch after another) the earlier tiles' sums of the previous sub-chunk's
             // dk and dv rows, stored in H3; issued before the row prefetch

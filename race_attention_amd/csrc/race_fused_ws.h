@@ -105,8 +105,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     static_assert(CF::LT == 8, "every (token, table) lane of a helper tile is a table of the bucket tile");
     constexpr int TPH_O = NTD * MTC / NWH;  // dq tiles per helper wave
 
-    __shared__ __align__(16) __bf16 sK[C][LDX];
-    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sK[C][CF::LDQ];
+    __shared__ __align__(16) __bf16 sQ[C][CF::LDQ];
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
     __shared__ __align__(16) __bf16 sGO[2][C][LDX];  // by sub-chunk parity
     __shared__ __align__(16) __bf16 sPK[2][C][LDS];  // rows [t][s], by sub-chunk parity
@@ -226,8 +226,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     auto stage_rows = [&](const MoveRegs &m, int s) {  // movers: registers into LDS (v, go by parity)
         const int nv = nv_of(s), pb = s & 1;
         if (movkq) {
-            tile_store_rows<CH>(&sK[0][0], m.a, nv, mid);
-            tile_store_rows<CH>(&sQ[0][0], m.b, nv, mid);
+            tile_store_rows<CH, false, CF::LDQ>(&sK[0][0], m.a, nv, mid);
+            tile_store_rows<CH, false, CF::LDQ>(&sQ[0][0], m.b, nv, mid);
         } else {
             tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
             tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     auto hash_fwd = [&](const __bf16 *sX, __bf16 *dst, int tw, int s, bool keep_th) {
         const int jt = tw / MTC, tt = tw % MTC;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * LDX + (lane >> 4) * 8;
+        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDQ + (lane >> 4) * 8;
 #pragma unroll
         for (int kb = 0; kb < DP / 32; ++kb)
             EngBF16::mma(acc, sProj[tw][kb][lane], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
@@ -523,8 +523,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     constexpr int TPH = NTD * MTC / NWH;  // dk and dv tiles per helper wave
     static_assert(TPH * NWH == NTD * MTC, "dk, dv tiles split evenly over the helper waves");
 
-    __shared__ __align__(16) __bf16 sK[C][LDX];
-    __shared__ __align__(16) __bf16 sQ[C][LDX];
+    __shared__ __align__(16) __bf16 sK[C][CF::LDQ];
+    __shared__ __align__(16) __bf16 sQ[C][CF::LDQ];
     __shared__ __align__(16) __bf16 sV[2][C][LDX];   // by sub-chunk parity
     __shared__ __align__(16) __bf16 sGO[2][C][LDX];  // by sub-chunk parity
     __shared__ __align__(16) __bf16 sPK[2][C][LDK];  // rows [t][s], by sub-chunk parity
@@ -567,7 +567,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     auto hash_fwd = [&](const bf16x8 (&fp)[DP / 32], const __bf16 *sX, __bf16 *dst, int ldd, int tw, int s, bool keep_th) {
         const int jt = tw / MTC, tt = tw % MTC;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * LDX + (lane >> 4) * 8;
+        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDQ + (lane >> 4) * 8;
 #pragma unroll
         for (int kb = 0; kb < DP / 32; ++kb)
             EngBF16::mma(acc, fp[kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
@@ -624,8 +624,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     auto stage_rows = [&](const MoveRegs &m, int s) {
         const int nv = nv_of(s), pb = s & 1;
         if (movkq) {
-            tile_store_rows<CH>(&sK[0][0], m.a, nv, mid);
-            tile_store_rows<CH>(&sQ[0][0], m.b, nv, mid);
+            tile_store_rows<CH, false, CF::LDQ>(&sK[0][0], m.a, nv, mid);
+            tile_store_rows<CH, false, CF::LDQ>(&sQ[0][0], m.b, nv, mid);
         } else {
             tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
             tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
