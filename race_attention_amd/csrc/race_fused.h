@@ -437,6 +437,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     const Ctx c = make_ctx(P, ST);
     const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
+    __builtin_assume(wave >= 0 && wave < NW);  // (threadIdx.x < NW * 64): per-wave tile counts that divide evenly need no guard
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
     constexpr int TPW_A = (CF::NTS + NW - 1) / NW;
     constexpr int TPW_P = (CF::NPT + NW - 1) / NW;
@@ -585,6 +586,7 @@ void race_fused_fwd_readout(const ScanParams P)
     const Ctx c = make_ctx(P, ST);
     const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
+    __builtin_assume(wave >= 0 && wave < NW);  // (threadIdx.x < NW * 64): per-wave tile counts that divide evenly need no guard
     constexpr int TPW_P0 = (2 * CF::NPT + NW - 1) / NW;
     FusedFrags<CF, DP, TPW_P0> fr;
     fr.load(P, c.l0, c.Lt, lane, wave);
@@ -928,6 +930,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
     const Ctx c = make_ctx(P, ST);
     const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
+    __builtin_assume(wave >= 0 && wave < NW);  // (threadIdx.x < NW * 64): per-wave tile counts that divide evenly need no guard
     constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;   // k then q projection tiles
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
     constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;
@@ -1297,6 +1300,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
     const Ctx c = make_ctx(P, ST);
     const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
     const int tid = c.tid, lane = c.lane, wave = c.wave;
+    __builtin_assume(wave >= 0 && wave < NW);  // (threadIdx.x < NW * 64): per-wave tile counts that divide evenly need no guard
     constexpr int TPW_P = (2 * CF::NPT + NW - 1) / NW;
     constexpr int TPW_S = (CF::NTS * CF::NTD + NW - 1) / NW;
     constexpr int TPW_A = (CF::NTS * MTC + NW - 1) / NW;
