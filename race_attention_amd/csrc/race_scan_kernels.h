@@ -119,6 +119,7 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
     __shared__ __align__(16) T sPKt[ST][LDC];
 
     const Ctx c = make_ctx(P, ST);
+    __builtin_assume(c.wave >= 0 && c.wave < NW);  // (threadIdx.x < NW * 64)
     PlaneFrags<E, CF> pf;
     if constexpr (CF::QKV)
         pf.load(P, c);
@@ -226,6 +227,7 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
     __shared__ float sA0[ST];
 
     const Ctx c = make_ctx(P, ST);
+    __builtin_assume(c.wave >= 0 && c.wave < NW);  // (threadIdx.x < NW * 64)
     PlaneFrags<E, CF> pf;
     if constexpr (CF::QKV)
         pf.load(P, c);
@@ -429,6 +431,7 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
     __shared__ float sA0[ST];
 
     const Ctx c = make_ctx(P, ST);
+    __builtin_assume(c.wave >= 0 && c.wave < NW);  // (threadIdx.x < NW * 64)
     PlaneFrags<E, CF> pf;
     if constexpr (CF::QKV) {
         pf.load(P, c);
@@ -744,6 +747,7 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
     T *sGU = reinterpret_cast<T *>(&sUq[0][0]);
 
     const Ctx c = make_ctx(P, ST);
+    __builtin_assume(c.wave >= 0 && c.wave < NW);  // (threadIdx.x < NW * 64)
     PlaneFrags<E, CF> pf;
     if constexpr (CF::QKV)
         pf.load(P, c);
