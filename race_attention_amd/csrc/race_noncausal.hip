@@ -223,6 +223,181 @@ __global__ __launch_bounds__(NC_NTH) void race_nc_backward(const NcParams P)
     }
 }
 
+// Backward on the matrix cores (fp32 v_mfma_f32_16x16x4_f32) for S <= 32 (every bucket in one
+// 32-row chunk, rows >= S zero), products formed transposed so that a lane's accumulator holds
+// four consecutive columns of one output row:
+//   gpQ^T = E go^T and gpK^T = gA + gB v^T  (M = bucket, N = token, K = d)
+//   gv^T  = gB^T pK^T                         (M = d, N = token, K = bucket)
+// Eight waves, each owning one 16-token tile of a 128-token step. Lane (n = lane % 16,
+// g = lane / 16) takes the d values 16 j + 4 g + e of k-step (j, e), so it loads its token's go and
+// v as 16-byte runs straight from HBM (no LDS staging) and reads the E / gB rows as 16-byte runs:
+// rows at a pitch of an odd multiple of 8 words make those reads conflict-free. gB is kept a
+// second time at a pitch of 16 x odd words for gv, whose A fragment reads row 4 kk + g at column
+// lane % 16 (banks 16 g + lane % 16).
+constexpr int NCM_W = 8, NCM_NTH = NCM_W * 64, NCM_TT = NCM_W * 16;
+
+template <int DP>
+__global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams P)
+{
+    constexpr int LDD = DP + 8, LDV = DP + 16;
+    __shared__ __align__(16) float sE[32][LDD];
+    __shared__ __align__(16) float sGB[32][LDD];
+    __shared__ __align__(16) float sGBv[32][LDV];
+    __shared__ float sGA[32];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, z = blockIdx.y;
+    const int n16 = lane & 15, g = lane >> 4;
+    // E, gB (and gA) of stream z: rows s < S, zero beyond
+    {
+        const int64_t slot = (int64_t)z * (P.NB + 1) + P.NB;
+        const float *B = P.totB + slot * P.S_pad * P.DPw;
+        const float *A = P.totA + slot * P.S_pad;
+        const float *GE = P.totGE + slot * P.S_pad * P.DPw;
+        for (int i = tid; i < 32 * DP; i += NCM_NTH) {
+            const int c = i / DP, d = i % DP;
+            float e = 0.0f, gb = 0.0f;
+            if (c < P.S && d < P.D) {
+                const float inv = 1.0f / (A[c] + P.eps);
+                e = B[(int64_t)c * P.DPw + d] * inv;
+                gb = GE[(int64_t)c * P.DPw + d] * inv;
+            }
+            sE[c][d] = e;
+            sGB[c][d] = gb;
+            sGBv[c][d] = gb;
+        }
+        __syncthreads();
+        // gA[s] = -(gE . E) / (A + eps) = -(gB . E): one wave per bucket row, lanes over d
+        for (int c = w; c < 32; c += NCM_W) {
+            float acc = 0.0f;
+            for (int d = lane; d < DP; d += 64)
+                acc += sGB[c][d] * sE[c][d];
+            for (int o = 32; o > 0; o >>= 1)
+                acc += __shfl_xor(acc, o);
+            if (lane == 0)
+                sGA[c] = -acc;
+        }
+        __syncthreads();
+    }
+    // gA of the lane's gpK columns 16 j + 4 g + e
+    float ga[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            ga[j][e] = sGA[16 * j + 4 * g + e];
+    constexpr int NJ = DP / 16;  // 16-wide d runs: k-steps 4 NJ over d, output tiles NJ over d
+    const bool vec_d = (P.D & 3) == 0, vec_s = (P.S & 3) == 0;
+    // a token row's d values 16 j + 4 g .. + 3, zero past D
+    auto row4 = [&](const float *row, int j, bool ok) {
+        const int d = 16 * j + 4 * g;
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        if (ok && d < P.D) {
+            if (vec_d) {
+                x = *reinterpret_cast<const f32x4 *>(row + d);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    x[e] = d + e < P.D ? row[d + e] : 0.0f;
+            }
+        }
+        return x;
+    };
+    // four consecutive columns c .. c + 3 of a [T][ncol] output row, those < ncol
+    auto put4 = [](float *row, int c, int ncol, bool vec, const f32x4 &x) {
+        if (vec && c + 4 <= ncol) {
+            *reinterpret_cast<f32x4 *>(row + c) = x;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (c + e < ncol)
+                    row[c + e] = x[e];
+        }
+    };
+    const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
+    const int ks = (P.S + 3) & ~3;
+    for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
+        const int t0 = st * NCM_TT + w * 16;
+        if (t0 >= P.T)
+            break;  // (uniform within the wave; no barrier inside the loop)
+        const int t = t0 + n16;
+        const bool ok = t < P.T;
+        const int64_t row = (int64_t)z * P.T + t;
+        // ---- gpQ^T[s][t] = E[s] . go_t
+        f32x4 aq[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        {
+            f32x4 x[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                x[j] = row4(P.gO + row * P.D, j, ok);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const f32x4 e0 = *reinterpret_cast<const f32x4 *>(&sE[n16][16 * j + 4 * g]);
+                const f32x4 e1 = *reinterpret_cast<const f32x4 *>(&sE[16 + n16][16 * j + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    EngF32::mma(aq[0], e0[e], x[j][e]);
+                    EngF32::mma(aq[1], e1[e], x[j][e]);
+                }
+            }
+        }
+        // ---- gpK^T[s][t] = gA[s] + gB[s] . v_t
+        f32x4 ak[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        {
+            f32x4 x[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                x[j] = row4(P.V + row * P.D, j, ok);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&sGB[n16][16 * j + 4 * g]);
+                const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&sGB[16 + n16][16 * j + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    EngF32::mma(ak[0], b0[e], x[j][e]);
+                    EngF32::mma(ak[1], b1[e], x[j][e]);
+                }
+            }
+        }
+        if (ok) {
+            float *q = P.gpQ + row * P.S, *k = P.gpK + row * P.S;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                f32x4 kk = ak[j];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    kk[e] += ga[j][e];
+                put4(q, 16 * j + 4 * g, P.S, vec_s, aq[j]);
+                put4(k, 16 * j + 4 * g, P.S, vec_s, kk);
+            }
+        }
+        // ---- gv^T[d][t] = sum_s gB[s][d] pK[t][s]  (k-step kk: bucket 4 kk + g)
+        f32x4 av[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            av[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        {
+            const float *pk = P.pK + row * P.S;
+            float pv[8];
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk)
+                pv[kk] = (ok && 4 * kk + g < P.S) ? pk[4 * kk + g] : 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                if (4 * kk < ks) {
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        EngF32::mma(av[j], sGBv[4 * kk + g][16 * j + n16], pv[kk]);
+                }
+            }
+        }
+        if (ok) {
+            float *gv = P.gV + row * P.D;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                put4(gv, 16 * j + 4 * g, P.D, vec_d, av[j]);
+        }
+    }
+}
+
 template <int DP>
 hipError_t launch_nc_dp(int bwd, const NcParams &P, int N, hipStream_t s)
 {
@@ -230,6 +405,17 @@ hipError_t launch_nc_dp(int bwd, const NcParams &P, int N, hipStream_t s)
     // 2048 workgroups (8 per CU)
     const int ntt = (P.T + NC_TT - 1) / NC_TT;
     NcParams Q = P;
+    {
+        if (bwd && P.S <= 32) {
+            // matrix-core backward: a workgroup walks up to 16 steps of 128 tokens, about 1024
+            // workgroups in the grid
+            const int nstep = (P.T + NCM_TT - 1) / NCM_TT;
+            Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)nstep * N / 1024));
+            const dim3 grid((unsigned)((nstep + Q.tpw - 1) / Q.tpw), (unsigned)N);
+            hipLaunchKernelGGL(race_nc_backward_mfma<DP>, grid, dim3(NCM_NTH), 0, s, Q);
+            return hipGetLastError();
+        }
+    }
     Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)ntt * N / 2048));
     const dim3 grid((unsigned)((ntt + Q.tpw - 1) / Q.tpw), (unsigned)N);
     if (bwd)

@@ -22,10 +22,12 @@ def _probs(N, T, S, D, seed):
     return pk, pq, v, go
 
 
-# the last two: enough 32-token tiles that each workgroup walks several (4 here, ragged last tile),
-# with every bucket in one chunk (S = 24) and over several chunks (S = 64)
+# S <= 32 with D <= 128 takes the matrix-core backward (ragged S and D: 30 x 100, 1 x 20, 32 x 64);
+# the last two: enough token tiles that each workgroup walks several (ragged last tile), with every
+# bucket in one chunk (S = 24) and over several chunks (S = 64)
 @pytest.mark.parametrize("N,T,S,D", [(1, 1, 8, 16), (2, 7, 24, 64), (3, 300, 128, 64), (1, 4096, 256, 128),
-                                     (2, 1000, 64, 100), (1, 513, 300, 256), (4, 2000, 16, 32),
+                                     (2, 1000, 64, 100), (2, 1000, 30, 100), (3, 517, 32, 64), (1, 77, 1, 20),
+                                     (1, 513, 300, 256), (2, 333, 24, 256), (4, 2000, 16, 32),
                                      (4, 70001, 24, 128), (4, 66017, 64, 32)])
 def test_noncausal_op(dev, N, T, S, D):
     from race_attention_amd.noncausal import RaceNonCausalFn
