@@ -7,8 +7,8 @@
 //   gpK[t][s] = gA[s] + v_t . gB[s],   gv_t = sum_s pK[t][s] gB[s]
 // The totals come from the causal machinery's per-block totals kernel and block scan
 // (slot NB of the scanned workspace holds the whole-sequence sum); the kernels here are
-// the per-token readout and backward, fp32 FMA on LDS tiles of NC_TT tokens x NC_SC
-// buckets.
+// the per-token readout and backward: on fp32 MFMA with the bucket tables resident in LDS
+// for S <= 32, else fp32 FMA on LDS tiles of NC_TT tokens x NC_SC buckets.
 #include <algorithm>
 
 #include "race_device.h"
@@ -236,6 +236,83 @@ __global__ __launch_bounds__(NC_NTH) void race_nc_backward(const NcParams P)
 // lane % 16 (banks 16 g + lane % 16).
 constexpr int NCM_W = 8, NCM_NTH = NCM_W * 64, NCM_TT = NCM_W * 16;
 
+// four consecutive columns c .. c + 3 of a [T][ncol] output row, those < ncol (one 16-byte store
+// when ncol is a multiple of 4)
+__device__ __forceinline__ void put4(float *row, int c, int ncol, bool vec, const f32x4 &x)
+{
+    if (vec && c + 4 <= ncol) {
+        *reinterpret_cast<f32x4 *>(row + c) = x;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (c + e < ncol)
+                row[c + e] = x[e];
+    }
+}
+
+// acc[j] (j < DP / 16) += X^T p^T for one 16-token tile: X is a [32][LD] bucket-by-d table in LDS
+// (rows >= S zero), p the lane's token row of S bucket probabilities; lane (n, g) holds
+// p[4 kk + g] for k-step kk and reads X[4 kk + g][16 j + n] (banks 16 g + n for LD = 16 x odd)
+template <int DP, int LD>
+__device__ __forceinline__ void bucket_contract(f32x4 (&acc)[DP / 16], const float (*X)[LD], const float *p, bool ok,
+                                                int S, int n16, int g)
+{
+    float pv[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+        pv[kk] = (ok && 4 * kk + g < S) ? p[4 * kk + g] : 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        if (4 * kk < S) {
+#pragma unroll
+            for (int j = 0; j < DP / 16; ++j)
+                EngF32::mma(acc[j], X[4 * kk + g][16 * j + n16], pv[kk]);
+        }
+    }
+}
+
+// Readout on the matrix cores for S <= 32: out^T = E^T pQ^T per 16-token tile (M = d, N = token,
+// K = bucket), E resident in LDS at a pitch of 16 x odd words; a lane's accumulator holds four
+// consecutive d of its token's output row, stored as one 16-byte run.
+template <int DP>
+__global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P)
+{
+    constexpr int LDV = DP + 16;
+    __shared__ __align__(16) float sEv[32][LDV];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, z = blockIdx.y;
+    const int n16 = lane & 15, g = lane >> 4;
+    {
+        const int64_t slot = (int64_t)z * (P.NB + 1) + P.NB;
+        const float *B = P.totB + slot * P.S_pad * P.DPw;
+        const float *A = P.totA + slot * P.S_pad;
+        for (int i = tid; i < 32 * DP; i += NCM_NTH) {
+            const int c = i / DP, d = i % DP;
+            sEv[c][d] = (c < P.S && d < P.D) ? B[(int64_t)c * P.DPw + d] / (A[c] + P.eps) : 0.0f;
+        }
+        __syncthreads();
+    }
+    const bool vec_d = (P.D & 3) == 0;
+    const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
+    for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
+        const int t0 = st * NCM_TT + w * 16;
+        if (t0 >= P.T)
+            break;  // (uniform within the wave; no barrier inside the loop)
+        const int t = t0 + n16;
+        const bool ok = t < P.T;
+        const int64_t row = (int64_t)z * P.T + t;
+        f32x4 acc[DP / 16];
+#pragma unroll
+        for (int j = 0; j < DP / 16; ++j)
+            acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        bucket_contract<DP, LDV>(acc, sEv, P.pQ + row * P.S, ok, P.S, n16, g);
+        if (ok) {
+#pragma unroll
+            for (int j = 0; j < DP / 16; ++j)
+                put4(P.out + row * P.D, 16 * j + 4 * g, P.D, vec_d, acc[j]);
+        }
+    }
+}
+
 template <int DP>
 __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams P)
 {
@@ -301,19 +378,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         }
         return x;
     };
-    // four consecutive columns c .. c + 3 of a [T][ncol] output row, those < ncol
-    auto put4 = [](float *row, int c, int ncol, bool vec, const f32x4 &x) {
-        if (vec && c + 4 <= ncol) {
-            *reinterpret_cast<f32x4 *>(row + c) = x;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (c + e < ncol)
-                    row[c + e] = x[e];
-        }
-    };
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
-    const int ks = (P.S + 3) & ~3;
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
         const int t0 = st * NCM_TT + w * 16;
         if (t0 >= P.T)
@@ -374,21 +439,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
             av[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        {
-            const float *pk = P.pK + row * P.S;
-            float pv[8];
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
-                pv[kk] = (ok && 4 * kk + g < P.S) ? pk[4 * kk + g] : 0.0f;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                if (4 * kk < ks) {
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j)
-                        EngF32::mma(av[j], sGBv[4 * kk + g][16 * j + n16], pv[kk]);
-                }
-            }
-        }
+        bucket_contract<DP, LDV>(av, sGBv, P.pK + row * P.S, ok, P.S, n16, g);
         if (ok) {
             float *gv = P.gV + row * P.D;
 #pragma unroll
@@ -405,16 +456,17 @@ hipError_t launch_nc_dp(int bwd, const NcParams &P, int N, hipStream_t s)
     // 2048 workgroups (8 per CU)
     const int ntt = (P.T + NC_TT - 1) / NC_TT;
     NcParams Q = P;
-    {
-        if (bwd && P.S <= 32) {
-            // matrix-core backward: a workgroup walks up to 16 steps of 128 tokens, about 1024
-            // workgroups in the grid
-            const int nstep = (P.T + NCM_TT - 1) / NCM_TT;
-            Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)nstep * N / 1024));
-            const dim3 grid((unsigned)((nstep + Q.tpw - 1) / Q.tpw), (unsigned)N);
+    if (P.S <= 32) {
+        // matrix-core kernels: a workgroup walks up to 16 steps of 128 tokens, about 1024
+        // workgroups in the grid
+        const int nstep = (P.T + NCM_TT - 1) / NCM_TT;
+        Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)nstep * N / 1024));
+        const dim3 grid((unsigned)((nstep + Q.tpw - 1) / Q.tpw), (unsigned)N);
+        if (bwd)
             hipLaunchKernelGGL(race_nc_backward_mfma<DP>, grid, dim3(NCM_NTH), 0, s, Q);
-            return hipGetLastError();
-        }
+        else
+            hipLaunchKernelGGL(race_nc_readout_mfma<DP>, grid, dim3(NCM_NTH), 0, s, Q);
+        return hipGetLastError();
     }
     Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)ntt * N / 2048));
     const dim3 grid((unsigned)((ntt + Q.tpw - 1) / Q.tpw), (unsigned)N);
