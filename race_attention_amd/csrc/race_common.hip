@@ -609,6 +609,337 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
     }
 }
 
+// ---------------------------------------------------------------------------- soft-hash on MFMA
+// Soft-hash for L*K <= 32 and K <= 4 on fp32 MFMA (v_mfma_f32_16x16x4_f32), one 16-token tile per
+// wave and no workgroup barrier after the planes are loaded. Lane (n = lane % 16, g = lane / 16)
+// loads its token's x at d = 16 jj + 4 g .. + 3 (one 16-byte or 8-byte run per jj, straight from
+// HBM), which is the K index of k-steps (jj, e) of the projection
+//   u^T[j][t] = sum_d planes^T[j][d] x[t][d]   (M = plane, N = token, K = d)
+// whose A fragment reads planes^T rows as 16-byte runs (pitch an odd multiple of 8 words:
+// conflict-free). The backward's
+//   dx^T[d][t] = sum_j planes[d][j] gproj[t][j]   (M = d, N = token, K = plane)
+// leaves four consecutive d of one token in a lane, stored as one run. u and gproj pass through
+// per-wave LDS rows between the MFMA layout and the (token, table) items.
+constexpr int SHM_W = 4;  // waves per workgroup
+
+struct ShmLayout {
+    int DX16, PT, PD, PU, njt;  // d rounded to 16, pitches (floats), plane tiles of 16
+    __host__ __device__ ShmLayout(int D, int LK)
+    {
+        DX16 = (D + 15) & ~15;
+        PT = DX16 + 8;  // odd multiple of 8
+        PD = (LK + 3) & ~3;
+        if (((PD / 4) & 1) == 0)
+            PD += 4;  // 4 x odd
+        njt = (LK + 15) / 16;
+        PU = njt == 1 ? 24 : 40;  // odd multiple of 8, >= 16 njt
+    }
+    // floats: planes^T [16 njt][PT], per-wave u [SHM_W][16][PU]; backward also planes [DX16][PD] and
+    // per-wave gproj [SHM_W][16][PD]
+    __host__ __device__ int floats(bool bwd) const
+    {
+        return 16 * njt * PT + SHM_W * 16 * PU + (bwd ? DX16 * PD + SHM_W * 16 * PD : 0);
+    }
+};
+
+bool softhash_mfma_ok(int D, int L, int K, int M, int bwd)
+{
+    return D <= 256 && L * K <= 32 && K <= 4 && (!bwd || M == 1);
+}
+
+// planes of one member into sPlT [16 njt][PT] (and sPl [DX16][PD]), zero beyond (LK, D)
+RACE_DEV void shm_load_planes(float *sPlT, float *sPl, const float *planes, const SoftHashParams &P,
+                              const ShmLayout &Y)
+{
+    for (int i = threadIdx.x; i < 16 * Y.njt * Y.DX16; i += SHM_W * 64) {
+        const int j = i / Y.DX16, d = i - j * Y.DX16;
+        float v = 0.0f;
+        if (d < P.D && j < P.LK) {
+            v = planes[d * P.LK + j];
+            if (P.round_planes)
+                v = (float)(__bf16)v;
+        }
+        sPlT[j * Y.PT + d] = v;
+        if (sPl && j < Y.PD)
+            sPl[d * Y.PD + j] = v;
+    }
+    if (sPl) {  // columns 16 njt .. PD (PD can exceed the plane tiles by 4)
+        for (int i = threadIdx.x; i < Y.DX16 * Y.PD; i += SHM_W * 64) {
+            const int d = i / Y.PD, j = i - d * Y.PD;
+            if (j >= 16 * Y.njt)
+                sPl[i] = 0.0f;
+        }
+    }
+}
+
+// 4 consecutive x elements d .. d + 3 of a token row (zero past D)
+template <class TX>
+RACE_DEV f32x4 shm_x4(const TX *row, int d, int D, bool vec)
+{
+    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (d >= D)
+        return v;
+    if (vec) {
+        typedef TX tx4 __attribute__((ext_vector_type(4)));
+        const tx4 w = *reinterpret_cast<const tx4 *>(row + d);
+        return f32x4{(float)w[0], (float)w[1], (float)w[2], (float)w[3]};
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        v[e] = d + e < D ? (float)row[d + e] : 0.0f;
+    return v;
+}
+
+// u = tanh(x . planes) / scale of this wave's 16 tokens into its sU rows [16][PU]
+template <class TX, int NJT>
+RACE_DEV void shm_project(float *sU, const float *sPlT, const SoftHashParams &P, const ShmLayout &Y, const TX *xrow,
+                          bool ok, bool vec, int n16, int g)
+{
+    f32x4 xv[16];
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj)
+        if (16 * jj < P.D)
+            xv[jj] = ok ? shm_x4<TX>(xrow, 16 * jj + 4 * g, P.D, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[NJT];
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt)
+        acc[jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+        if (16 * jj < P.D) {
+#pragma unroll
+            for (int jt = 0; jt < NJT; ++jt) {
+                const f32x4 pt = *reinterpret_cast<const f32x4 *>(sPlT + (16 * jt + n16) * Y.PT + 16 * jj + 4 * g);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    EngF32::mma(acc[jt], pt[e], xv[jj][e]);
+            }
+        }
+    }
+    // accumulator rows: planes 16 jt + 4 g + e of token n16
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt) {
+        f32x4 u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            u[e] = tanh_f(acc[jt][e]) * P.inv_scale;
+        *reinterpret_cast<f32x4 *>(sU + n16 * Y.PU + 16 * jt + 4 * g) = u;
+    }
+}
+
+template <class TX, int KB, int NJT>
+__global__ __launch_bounds__(SHM_W * 64) void race_softhash_fwd_mfma(SoftHashParams P)
+{
+    extern __shared__ float sm[];
+    const ShmLayout Y(P.D, P.LK);
+    float *sPlT = sm;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n16 = lane & 15, g = lane >> 4;
+    float *sU = sPlT + 16 * NJT * Y.PT + w * 16 * Y.PU;
+    const int bh = blockIdx.y, m = blockIdx.z;
+    const int b = bh / P.H, h = bh % P.H;
+    constexpr int R = 1 << KB;
+    const int S = P.L * R;
+    float *out = P.probs + ((int64_t)m * P.B * P.H + bh) * P.T * S;
+    const bool vec_out = (reinterpret_cast<uintptr_t>(P.probs) & 15) == 0;
+    const bool vec_x = sh_x_vec<TX>(P);
+    const TX *x = reinterpret_cast<const TX *>(P.x.p) + b * P.x.sb + h * P.x.sh;
+    shm_load_planes(sPlT, nullptr, P.planes + (int64_t)m * P.plane_stride, P, Y);
+    __syncthreads();
+    const int span = P.tpw * SH_TT;
+    const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
+    for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
+        const int t = t0 + n16;
+        shm_project<TX, NJT>(sU, sPlT, P, Y, x + (int64_t)t * P.x.st, t < tok1, vec_x, n16, g);
+        const int nv = min(16, tok1 - t0);
+        if constexpr (KB >= 2) {
+            if (vec_out) {
+                // R / 4 lanes per (token, table), each storing 4 consecutive corners: consecutive
+                // lanes write consecutive 16-byte runs. Corner c = 4q + c2 takes its KB - 2 high bits
+                // from q; products in the same order as corner_probs
+                constexpr int Q = R / 4;
+                for (int i = lane; i < nv * P.L * Q; i += 64) {
+                    const int it = i / Q, q = i - it * Q;
+                    const int r = it / P.L, l = it - r * P.L;
+                    float s0[KB], s1[KB];
+#pragma unroll
+                    for (int k = 0; k < KB; ++k)
+                        sigm_pair(sU[r * Y.PU + l * KB + k], s0[k], s1[k]);
+                    float pre = 1.0f;
+#pragma unroll
+                    for (int k = 0; k < KB - 2; ++k)
+                        pre *= ((q >> (KB - 3 - k)) & 1) ? s1[k] : s0[k];
+                    const float a0 = pre * s0[KB - 2], a1 = pre * s1[KB - 2];
+                    *reinterpret_cast<f32x4 *>(out + (int64_t)(t0 + r) * S + l * R + 4 * q) =
+                        f32x4{a0 * s0[KB - 1], a0 * s1[KB - 1], a1 * s0[KB - 1], a1 * s1[KB - 1]};
+                }
+                continue;
+            }
+        }
+        for (int i = lane; i < nv * P.L; i += 64) {
+            const int r = i / P.L, l = i - r * P.L;
+            float s0[KB], s1[KB], p[R];
+#pragma unroll
+            for (int k = 0; k < KB; ++k)
+                sigm_pair(sU[r * Y.PU + l * KB + k], s0[k], s1[k]);
+            corner_probs<KB>(s0, s1, p);
+            float *o = out + (int64_t)(t0 + r) * S + l * R;
+#pragma unroll
+            for (int c = 0; c < R; ++c)
+                o[c] = p[c];
+        }
+    }
+}
+
+template <class TX, int KB, int NJT>
+__global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashParams P)
+{
+    extern __shared__ float sm[];
+    const ShmLayout Y(P.D, P.LK);
+    float *sPlT = sm;
+    float *sPl = sPlT + 16 * NJT * Y.PT;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n16 = lane & 15, g = lane >> 4;
+    float *sU = sPl + Y.DX16 * Y.PD + w * 16 * Y.PU;
+    float *sGP = sPl + Y.DX16 * Y.PD + SHM_W * 16 * Y.PU + w * 16 * Y.PD;
+    const int bh = blockIdx.y;
+    const int b = bh / P.H, h = bh % P.H;
+    constexpr int R = 1 << KB;
+    const int S = P.L * R;
+    const bool vec_in = (reinterpret_cast<uintptr_t>(P.gprobs) & 15) == 0;
+    const bool vec_x = sh_x_vec<TX>(P);
+    const bool vec_dx = (P.D & 3) == 0 && (reinterpret_cast<uintptr_t>(P.dx.p) & (4 * sizeof(TX) - 1)) == 0 &&
+                        (P.dx.sb & 3) == 0 && (P.dx.sh & 3) == 0 && (P.dx.st & 3) == 0;
+    const TX *x = reinterpret_cast<const TX *>(P.x.p) + b * P.x.sb + h * P.x.sh;
+    TX *dx = reinterpret_cast<TX *>(const_cast<void *>(P.dx.p)) + b * P.dx.sb + h * P.dx.sh;
+    const float *gprobs = P.gprobs + (int64_t)bh * P.T * S;
+    for (int i = lane; i < 16 * Y.PD; i += 64)  // columns >= L*K stay zero
+        sGP[i] = 0.0f;
+    shm_load_planes(sPlT, sPl, P.planes, P, Y);
+    __syncthreads();
+    float gsu = 0.0f;  // sum of gu * u over this lane's (token, table) items
+    const int span = P.tpw * SH_TT;
+    const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
+    for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
+        const int t = t0 + n16;
+        shm_project<TX, NJT>(sU, sPlT, P, Y, x + (int64_t)t * P.x.st, t < tok1, vec_x, n16, g);
+        // (token, table) items: gu_k = d loss / d u_k, gproj = gu * (1 - tanh^2) / scale
+        for (int i = lane; i < 16 * P.L; i += 64) {
+            const int r = i / P.L, l = i - r * P.L;
+            float u[KB], s0[KB], s1[KB], gu[KB];
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                u[k] = sU[r * Y.PU + l * KB + k];
+                sigm_pair(u[k], s0[k], s1[k]);
+                gu[k] = 0.0f;
+            }
+            if (t0 + r < tok1) {
+                const float *gp = gprobs + (int64_t)(t0 + r) * S + l * R;
+                // gz_c = p_c (gp_c - sum p gp); gu_k = sum_c sign_k(c) gz_c with sign +1 where bit k
+                // of c is set: a butterfly from the least significant bit
+                float p[R], z[R], gr[R];
+                if (R % 4 == 0 && vec_in) {
+#pragma unroll
+                    for (int c = 0; c < R; c += 4) {
+                        const f32x4 v4 = *reinterpret_cast<const f32x4 *>(gp + c);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            gr[c + e] = v4[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < R; ++c)
+                        gr[c] = gp[c];
+                }
+                corner_probs<KB>(s0, s1, p);
+                float dot = 0.0f;
+#pragma unroll
+                for (int c = 0; c < R; ++c)
+                    dot += p[c] * gr[c];
+#pragma unroll
+                for (int c = 0; c < R; ++c)
+                    z[c] = p[c] * (gr[c] - dot);
+#pragma unroll
+                for (int lvl = 0; lvl < KB; ++lvl) {
+                    const int n = R >> (lvl + 1);
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < n; ++q) {
+                        acc += z[2 * q + 1] - z[2 * q];
+                        z[q] = z[2 * q] + z[2 * q + 1];
+                    }
+                    gu[KB - 1 - lvl] = acc;
+                }
+#pragma unroll
+                for (int k = 0; k < KB; ++k)
+                    gsu += gu[k] * u[k];
+            }
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                const float th = u[k] * P.scale;
+                sGP[r * Y.PD + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+            }
+        }
+        // dx^T tiles of 16 d: A = planes rows d (4-byte reads, pitch 4 x odd), B = gproj of token n16
+        const int nks = (P.LK + 3) / 4;
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+            if (16 * jj < P.D) {
+                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int kk = 0; kk < nks; ++kk)
+                    EngF32::mma(acc, sPl[(16 * jj + n16) * Y.PD + 4 * kk + g], sGP[n16 * Y.PD + 4 * kk + g]);
+                if (t < tok1) {
+                    TX *o = dx + (int64_t)t * P.dx.st;
+                    const int d = 16 * jj + 4 * g;
+                    if (vec_dx && d + 4 <= P.D) {
+                        typedef TX tx4 __attribute__((ext_vector_type(4)));
+                        *reinterpret_cast<tx4 *>(o + d) = tx4{(TX)acc[0], (TX)acc[1], (TX)acc[2], (TX)acc[3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (d + e < P.D)
+                                o[d + e] = (TX)acc[e];
+                    }
+                }
+            }
+        }
+    }
+    if (P.gscale) {
+        // workgroup sum of gu * u: d loss / d scale = -(1/scale) * (sum over all workgroups)
+        __shared__ float red[SHM_W];
+        for (int o = 32; o > 0; o >>= 1)
+            gsu += __shfl_xor(gsu, o);
+        if (lane == 0)
+            red[w] = gsu;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < SHM_W; ++i)
+                a += red[i];
+            P.gscale[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = a;
+        }
+    }
+}
+
+template <class TX, int KB>
+static const void *softhash_mfma_kernel(int bwd, int njt)
+{
+    if (bwd)
+        return njt == 1 ? (const void *)race_softhash_bwd_mfma<TX, KB, 1> : (const void *)race_softhash_bwd_mfma<TX, KB, 2>;
+    return njt == 1 ? (const void *)race_softhash_fwd_mfma<TX, KB, 1> : (const void *)race_softhash_fwd_mfma<TX, KB, 2>;
+}
+
+template <class TX>
+static const void *softhash_mfma_kernel_k(int K, int bwd, int njt)
+{
+    switch (K) {
+    case 1: return softhash_mfma_kernel<TX, 1>(bwd, njt);
+    case 2: return softhash_mfma_kernel<TX, 2>(bwd, njt);
+    case 3: return softhash_mfma_kernel<TX, 3>(bwd, njt);
+    case 4: return softhash_mfma_kernel<TX, 4>(bwd, njt);
+    default: return nullptr;
+    }
+}
+
 // kernel of bit count K (1..8) for one direction, dtype and head-dim class (D <= 64, 128, 256)
 template <class TX, int KB>
 static const void *softhash_kernel(int bwd, int D)
@@ -643,10 +974,10 @@ size_t softhash_smem(int D, int LK, bool bwd)
 
 int softhash_tiles_per_wg(int T, int B, int H)
 {
-    // a workgroup walks up to 8 consecutive tiles of one (b, h) (planes loaded once), as long as
+    // a workgroup walks up to 32 consecutive tiles of one (b, h) (planes loaded once), as long as
     // the grid keeps about 2048 workgroups (8 per CU)
     const int64_t tiles = (int64_t)((T + SH_TT - 1) / SH_TT) * B * H;
-    return (int)std::max<int64_t>(1, std::min<int64_t>(8, tiles / 2048));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(32, tiles / 2048));
 }
 
 int softhash_grid_x(int T, int B, int H)
@@ -657,12 +988,16 @@ int softhash_grid_x(int T, int B, int H)
 
 hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s)
 {
-    const void *fn = bf16 ? softhash_kernel_k<__bf16>(P.K, bwd, P.D) : softhash_kernel_k<float>(P.K, bwd, P.D);
+    const bool mf = softhash_mfma_ok(P.D, P.L, P.K, P.M, bwd);
+    const ShmLayout Y(P.D, P.LK);
+    const void *fn = mf ? (bf16 ? softhash_mfma_kernel_k<__bf16>(P.K, bwd, Y.njt)
+                                : softhash_mfma_kernel_k<float>(P.K, bwd, Y.njt))
+                        : (bf16 ? softhash_kernel_k<__bf16>(P.K, bwd, P.D) : softhash_kernel_k<float>(P.K, bwd, P.D));
     if (!fn)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)softhash_grid_x(P.T, P.B, P.H), (unsigned)(P.B * P.H),
                     (unsigned)(bwd ? 1 : (P.unshared ? P.M : 1)));
-    const size_t smem = softhash_smem(P.D, P.LK, bwd);
+    const size_t smem = mf ? sizeof(float) * Y.floats(bwd) : softhash_smem(P.D, P.LK, bwd);
     SoftHashParams args = P;
     args.tpw = softhash_tiles_per_wg(P.T, P.B, P.H);
     void *argv[] = {&args};
@@ -673,6 +1008,18 @@ hipError_t softhash_prepare(int D, int LK)
 {
     const int smem = (int)softhash_smem(D, LK, true);
     hipError_t e = hipSuccess;
+    const ShmLayout Y(D, LK);
+    const int smem_mf = (int)sizeof(float) * Y.floats(true);
+    if (D <= 256 && LK <= 32 && smem_mf > 64 * 1024) {
+        for (int K = 1; K <= 4 && e == hipSuccess; ++K)
+            for (int bwd = 0; bwd < 2 && e == hipSuccess; ++bwd) {
+                e = hipFuncSetAttribute(softhash_mfma_kernel_k<float>(K, bwd, Y.njt),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, smem_mf);
+                if (e == hipSuccess)
+                    e = hipFuncSetAttribute(softhash_mfma_kernel_k<__bf16>(K, bwd, Y.njt),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, smem_mf);
+            }
+    }
     if (smem > 64 * 1024) {
         for (int K = 1; K <= 8 && e == hipSuccess; ++K)
             for (int bwd = 0; bwd < 2 && e == hipSuccess; ++bwd) {

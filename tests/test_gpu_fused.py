@@ -163,13 +163,13 @@ def test_soft_hash_probs_fp32(dev):
         check("dK", Kd.grad, K64.grad, 1e-4)
 
 
-@pytest.mark.parametrize("B,H,T,L,Kb,M,share", [(4, 8, 4141, 4, 3, 2, False), (4, 8, 16389, 2, 2, 1, True)])
-def test_soft_hash_probs_multi_tile(dev, B, H, T, L, Kb, M, share):
-    """Enough 32-token tiles that each soft-hash workgroup walks several of them (2 and 8 per
+@pytest.mark.parametrize("B,H,T,D,L,Kb,M,share", [(4, 8, 4141, 64, 4, 3, 2, False), (4, 8, 16389, 64, 2, 2, 1, True),
+                                                   (1, 8, 262221, 16, 3, 3, 1, True)])
+def test_soft_hash_probs_multi_tile(dev, B, H, T, D, L, Kb, M, share):
+    """Enough 32-token tiles that each soft-hash workgroup walks several of them (2, 8 and 32 per
     workgroup here), with a ragged last tile and a last workgroup that holds fewer tiles."""
     from race_attention_amd import build_planes_protos, soft_hash_probs
-    D = 64
-    print(f"case B={B} H={H} T={T} L={L} K={Kb} M={M} share={share}", flush=True)
+    print(f"case B={B} H={H} T={T} D={D} L={L} K={Kb} M={M} share={share}", flush=True)
     planes_T, protos_T = build_planes_protos(D, Kb, L, M, device=dev, share_planes=share, seed=4)
     g = torch.Generator().manual_seed(T)
     Q, K, V = (torch.randn(B, H, T, D, generator=g) for _ in range(3))
