@@ -169,6 +169,21 @@ int race_nc_op_bwd_kept(const float *pK, const float *pQ, const float *V, const 
                         size_t workspace_bytes, const float *state, size_t state_bytes,
                         race_stream stream);
 
+/* The same non-causal pair with V, out, gO and gV as [B][H][T][D] views of any layout (fp32,
+ * contiguous last dim, token stride < 2^31) and the probabilities [B*H][T][S] contiguous, stream
+ * n = b * H + h. `state` may be null (no kept totals), else as race_nc_op_fwd_keep /
+ * race_nc_op_bwd_kept. No counterpart in the reference, whose BatchedACE moves its
+ * [M,B,T,H,d_k] values to [M*B*H, T, d_k] and back with torch permute/reshape copies
+ * (scaling/benchmark_time.py:116-128,164): for callers whose values keep that layout. */
+int race_nc_fwd_view(const float *pK, const float *pQ, race_tensor V, race_tensor out, int64_t B,
+                     int64_t H, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
+                     void *workspace, size_t workspace_bytes, float *state, size_t state_bytes,
+                     race_stream stream);
+int race_nc_bwd_view(const float *pK, const float *pQ, race_tensor V, race_tensor gO, float *gpK,
+                     float *gpQ, race_tensor gV, int64_t B, int64_t H, int64_t T, int64_t S,
+                     int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
+                     const float *state, size_t state_bytes, race_stream stream);
+
 /* ---------------------------------------------------------------- fused layer */
 typedef struct {
     int B, Hq, Hkv, T, D; /* q [B][Hq][T][D], k/v [B][Hkv][T][D]; query head h reads kv head h/(Hq/Hkv) */

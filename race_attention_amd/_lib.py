@@ -61,6 +61,10 @@ SIGNATURES = {
                                            ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_nc_op_bwd_kept": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                            ctypes.c_float, _i64, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
+    "race_nc_fwd_view": (ctypes.c_int, [_vp, _vp, Tensor4, Tensor4, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
+                                        _i64, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
+    "race_nc_bwd_view": (ctypes.c_int, [_vp, _vp, Tensor4, Tensor4, _vp, _vp, Tensor4, _i64, _i64, _i64, _i64, _i64,
+                                        ctypes.c_float, _i64, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
     "race_causal_dot_product": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp,
                                                ctypes.c_size_t, _vp]),
     "race_causal_dot_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

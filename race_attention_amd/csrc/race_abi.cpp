@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -400,6 +401,9 @@ static ScanParams op_params(const Geo &g, int64_t T, int64_t S, int64_t D, float
     P.eps = eps;
     P.scale = 1.0f;
     P.inv_scale = 1.0f;
+    P.v = View{nullptr, T * D, 0, D};  // contiguous [N][T][D] values / grads
+    P.go = P.v;
+    P.zH = 1;
     return P;
 }
 
@@ -616,19 +620,22 @@ size_t race_nc_op_workspace_bytes(int64_t N, int64_t T, int64_t S, int64_t D, in
     return nc_bytes(g, backward);
 }
 
-// whole-sequence totals of (w, x): per-block sums then the forward block scan (slot NB)
-static int nc_totals(const Geo &g, ScanParams P, const float *w, const float *x, float *wsB, float *wsA,
+// whole-sequence totals of (w, x): per-block sums then the forward block scan (slot NB); x rows
+// through the view xv of a [Z / zH][zH][T][D] layout
+static int nc_totals(const Geo &g, ScanParams P, const float *w, const View &xv, int zH, float *wsB, float *wsA,
                      hipStream_t s)
 {
     P.pK = w;
-    P.V = x;
+    P.V = static_cast<const float *>(xv.p);
+    P.v = xv;
+    P.zH = zH;
     P.wsB = wsB;
     P.wsA = wsA;
     RACE_TRY(run_scan_op(K_FWD_TOTALS, g, P, s));
     return hip_check(prof_block_scan(wsB, (int64_t)g.S_pad * g.DP, wsA, g.S_pad, (int)g.NB, (int)g.Z, 0, s), "block scan");
 }
 
-static NcParams nc_params(const Geo &g, int64_t T, int64_t S, int64_t D, float eps)
+static NcParams nc_params(const Geo &g, int64_t T, int64_t S, int64_t D, float eps, int zH)
 {
     NcParams Q;
     std::memset(&Q, 0, sizeof(Q));
@@ -639,78 +646,126 @@ static NcParams nc_params(const Geo &g, int64_t T, int64_t S, int64_t D, float e
     Q.S_pad = g.S_pad;
     Q.DPw = g.DP;
     Q.eps = eps;
+    Q.zH = zH;
     return Q;
 }
 
-static int nc_fwd_impl(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
-                       int64_t S, int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes,
-                       race_stream stream, float *state)
+static NcRows nc_rows(const View &v) { return NcRows{v.sb, v.sh, v.st}; }
+
+// every row of the views starts 16-byte aligned and D % 4 == 0: rows move as 16-byte runs
+static int nc_vec(int64_t D, std::initializer_list<const View *> vs)
 {
+    if (D & 3)
+        return 0;
+    for (const View *v : vs)
+        if ((reinterpret_cast<uintptr_t>(v->p) & 15) || (v->sb & 3) || (v->sh & 3) || (v->st & 3))
+            return 0;
+    return 1;
+}
+
+// the contiguous [N][T][D] layout of the race_nc_op_* entry points as a view (zH = 1)
+static View nc_flat(const float *p, int64_t T, int64_t D) { return View{p, T * D, 0, D}; }
+
+static int nc_view_check(const View &v, int64_t D, const char *name, const char *who)
+{
+    if (!v.p)
+        return fail(RACE_ERR_INVALID, "%s: null %s", who, name);
+    if (v.sb < 0 || v.sh < 0 || v.st < D || v.st >= ((int64_t)1 << 31))
+        return fail(RACE_ERR_INVALID, "%s: %s strides must be >= 0 with D <= token stride < 2^31", who, name);
+    return RACE_OK;
+}
+
+// streams n = b * H + h of the [B*H][T][S] probabilities; V / out rows through views
+static int nc_fwd_impl(const float *pK, const float *pQ, const View &V, const View &out, int64_t Bz, int64_t H,
+                       int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
+                       size_t workspace_bytes, race_stream stream, float *state, const char *who)
+{
+    if (Bz <= 0 || H <= 0 || Bz * H > INT32_MAX)
+        return fail(RACE_ERR_INVALID, "%s: B and H must be positive", who);
+    const int64_t N = Bz * H;
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
-    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, nc_bytes(g, 0), "race_nc_op_fwd"));
-    if (!out)
-        return fail(RACE_ERR_INVALID, "race_nc_op_fwd: null out");
+    RACE_TRY(op_check(pK, pQ, static_cast<const float *>(V.p), eps, workspace, workspace_bytes, nc_bytes(g, 0), who));
+    RACE_TRY(nc_view_check(V, D, "V", who));
+    RACE_TRY(nc_view_check(out, D, "out", who));
     Carver cv(workspace, workspace_bytes);
     float *wsB = cv.take(g.state_elems_B), *wsA = cv.take(g.state_elems_A);
     if (state)  // the totals are kept for the backward
         state_views(g, state, wsB, wsA);
     const hipStream_t s = hs(stream);
-    RACE_TRY(nc_totals(g, op_params(g, T, S, D, eps), pK, V, wsB, wsA, s));
-    NcParams Q = nc_params(g, T, S, D, eps);
+    RACE_TRY(nc_totals(g, op_params(g, T, S, D, eps), pK, V, (int)H, wsB, wsA, s));
+    NcParams Q = nc_params(g, T, S, D, eps, (int)H);
     Q.pQ = pQ;
-    Q.out = out;
+    Q.out = static_cast<float *>(const_cast<void *>(out.p));
+    Q.rO = nc_rows(out);
+    Q.vec = nc_vec(D, {&out});
     Q.totB = wsB;
     Q.totA = wsA;
     ProfScope ps(RACE_PROF_NC_FWD, s);
-    return hip_check(launch_noncausal(0, g.DP, Q, (int)N, s), "race_nc_op_fwd readout");
+    return hip_check(launch_noncausal(0, g.DP, Q, (int)N, s), "race_nc readout");
 }
 
-static int nc_bwd_impl(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
-                       float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
-                       void *workspace, size_t workspace_bytes, race_stream stream, const float *state)
+static int nc_bwd_impl(const float *pK, const float *pQ, const View &V, const View &gO, float *gpK, float *gpQ,
+                       const View &gV, int64_t Bz, int64_t H, int64_t T, int64_t S, int64_t D, float eps,
+                       int64_t block, void *workspace, size_t workspace_bytes, race_stream stream,
+                       const float *state, const char *who)
 {
+    if (Bz <= 0 || H <= 0 || Bz * H > INT32_MAX)
+        return fail(RACE_ERR_INVALID, "%s: B and H must be positive", who);
+    const int64_t N = Bz * H;
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
-    RACE_TRY(op_check(pK, pQ, V, eps, workspace, workspace_bytes, nc_bytes(g, 1), "race_nc_op_bwd"));
-    if (!gO || !gpK || !gpQ || !gV)
-        return fail(RACE_ERR_INVALID, "race_nc_op_bwd: null gradient pointer");
+    RACE_TRY(op_check(pK, pQ, static_cast<const float *>(V.p), eps, workspace, workspace_bytes, nc_bytes(g, 1), who));
+    if (!gpK || !gpQ)
+        return fail(RACE_ERR_INVALID, "%s: null gradient pointer", who);
+    RACE_TRY(nc_view_check(V, D, "V", who));
+    RACE_TRY(nc_view_check(gO, D, "gO", who));
+    RACE_TRY(nc_view_check(gV, D, "gV", who));
     Carver cv(workspace, workspace_bytes);
     float *wsB = cv.take(g.state_elems_B), *wsA = cv.take(g.state_elems_A);
     float *ws2B = cv.take(g.state_elems_B), *ws2A = cv.take(g.state_elems_A);
     const hipStream_t s = hs(stream);
     const ScanParams P = op_params(g, T, S, D, eps);
-    if (state)  // the forward's totals, kept by race_nc_op_fwd_keep
+    if (state)  // the forward's totals, kept by the forward
         state_views(g, state, wsB, wsA);
     else
-        RACE_TRY(nc_totals(g, P, pK, V, wsB, wsA, s));
-    RACE_TRY(nc_totals(g, P, pQ, gO, ws2B, ws2A, s));
-    NcParams Q = nc_params(g, T, S, D, eps);
+        RACE_TRY(nc_totals(g, P, pK, V, (int)H, wsB, wsA, s));
+    RACE_TRY(nc_totals(g, P, pQ, gO, (int)H, ws2B, ws2A, s));
+    NcParams Q = nc_params(g, T, S, D, eps, (int)H);
     Q.pK = pK;
-    Q.V = V;
-    Q.gO = gO;
+    Q.V = static_cast<const float *>(V.p);
+    Q.gO = static_cast<const float *>(gO.p);
     Q.gpK = gpK;
     Q.gpQ = gpQ;
-    Q.gV = gV;
+    Q.gV = static_cast<float *>(const_cast<void *>(gV.p));
+    Q.rV = nc_rows(V);
+    Q.rG = nc_rows(gO);
+    Q.rGV = nc_rows(gV);
+    Q.vec = nc_vec(D, {&V, &gO, &gV});
     Q.totB = wsB;
     Q.totA = wsA;
     Q.totGE = ws2B;
     ProfScope ps(RACE_PROF_NC_BWD, s);
-    return hip_check(launch_noncausal(1, g.DP, Q, (int)N, s), "race_nc_op_bwd backward");
+    return hip_check(launch_noncausal(1, g.DP, Q, (int)N, s), "race_nc backward");
 }
 
 int race_nc_op_fwd(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T, int64_t S,
                    int64_t D, float eps, int64_t block, void *workspace, size_t workspace_bytes, race_stream stream)
 {
-    return nc_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, nullptr);
+    if (!out)
+        return fail(RACE_ERR_INVALID, "race_nc_op_fwd: null out");
+    return nc_fwd_impl(pK, pQ, nc_flat(V, T, D), nc_flat(out, T, D), N, 1, T, S, D, eps, block, workspace,
+                       workspace_bytes, stream, nullptr, "race_nc_op_fwd");
 }
 
 int race_nc_op_bwd(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
                    float *gV, int64_t N, int64_t T, int64_t S, int64_t D, float eps, int64_t block,
                    void *workspace, size_t workspace_bytes, race_stream stream)
 {
-    return nc_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream,
-                       nullptr);
+    if (!gO || !gV)
+        return fail(RACE_ERR_INVALID, "race_nc_op_bwd: null gradient pointer");
+    return nc_bwd_impl(pK, pQ, nc_flat(V, T, D), nc_flat(gO, T, D), gpK, gpQ, nc_flat(gV, T, D), N, 1, T, S, D, eps,
+                       block, workspace, workspace_bytes, stream, nullptr, "race_nc_op_bwd");
 }
 
 int race_nc_op_fwd_keep(const float *pK, const float *pQ, const float *V, float *out, int64_t N, int64_t T,
@@ -718,7 +773,10 @@ int race_nc_op_fwd_keep(const float *pK, const float *pQ, const float *V, float 
                         float *state, size_t state_bytes, race_stream stream)
 {
     RACE_TRY(kept_state_check(state, state_bytes, N, T, S, D, block, "race_nc_op_fwd_keep"));
-    return nc_fwd_impl(pK, pQ, V, out, N, T, S, D, eps, block, workspace, workspace_bytes, stream, state);
+    if (!out)
+        return fail(RACE_ERR_INVALID, "race_nc_op_fwd_keep: null out");
+    return nc_fwd_impl(pK, pQ, nc_flat(V, T, D), nc_flat(out, T, D), N, 1, T, S, D, eps, block, workspace,
+                       workspace_bytes, stream, state, "race_nc_op_fwd_keep");
 }
 
 int race_nc_op_bwd_kept(const float *pK, const float *pQ, const float *V, const float *gO, float *gpK, float *gpQ,
@@ -727,8 +785,31 @@ int race_nc_op_bwd_kept(const float *pK, const float *pQ, const float *V, const 
                         race_stream stream)
 {
     RACE_TRY(kept_state_check(state, state_bytes, N, T, S, D, block, "race_nc_op_bwd_kept"));
-    return nc_bwd_impl(pK, pQ, V, gO, gpK, gpQ, gV, N, T, S, D, eps, block, workspace, workspace_bytes, stream,
-                       state);
+    if (!gO || !gV)
+        return fail(RACE_ERR_INVALID, "race_nc_op_bwd_kept: null gradient pointer");
+    return nc_bwd_impl(pK, pQ, nc_flat(V, T, D), nc_flat(gO, T, D), gpK, gpQ, nc_flat(gV, T, D), N, 1, T, S, D, eps,
+                       block, workspace, workspace_bytes, stream, state, "race_nc_op_bwd_kept");
+}
+
+int race_nc_fwd_view(const float *pK, const float *pQ, race_tensor V, race_tensor out, int64_t B, int64_t H,
+                     int64_t T, int64_t S, int64_t D, float eps, int64_t block, void *workspace,
+                     size_t workspace_bytes, float *state, size_t state_bytes, race_stream stream)
+{
+    if (state)
+        RACE_TRY(kept_state_check(state, state_bytes, B * H, T, S, D, block, "race_nc_fwd_view"));
+    return nc_fwd_impl(pK, pQ, to_view(V), to_view(out), B, H, T, S, D, eps, block, workspace, workspace_bytes,
+                       stream, state, "race_nc_fwd_view");
+}
+
+int race_nc_bwd_view(const float *pK, const float *pQ, race_tensor V, race_tensor gO, float *gpK, float *gpQ,
+                     race_tensor gV, int64_t B, int64_t H, int64_t T, int64_t S, int64_t D, float eps,
+                     int64_t block, void *workspace, size_t workspace_bytes, const float *state,
+                     size_t state_bytes, race_stream stream)
+{
+    if (state)
+        RACE_TRY(kept_state_check(state, state_bytes, B * H, T, S, D, block, "race_nc_bwd_view"));
+    return nc_bwd_impl(pK, pQ, to_view(V), to_view(gO), gpK, gpQ, to_view(gV), B, H, T, S, D, eps, block,
+                       workspace, workspace_bytes, stream, state, "race_nc_bwd_view");
 }
 
 // ============================================================================ fused layer

@@ -105,12 +105,11 @@ __global__ __launch_bounds__(NC_NTH) void race_nc_readout(const NcParams P)
                 }
             }
         }
-        float *out = P.out + ((int64_t)z * P.T + t0) * P.D;
 #pragma unroll
         for (int o = 0; o < NO; ++o) {
             const int r = tid / DP + o * (NC_NTH / DP), d = tid % DP;
             if (r < nv && d < P.D)
-                out[(int64_t)r * P.D + d] = acc[o];
+                P.out[nc_off(P.rO, P.zH, z, t0 + r) + d] = acc[o];
         }
     }
 }
@@ -135,14 +134,12 @@ __global__ __launch_bounds__(NC_NTH) void race_nc_backward(const NcParams P)
     for (int tt = blockIdx.x * P.tpw; tt < tt1; ++tt) {
         const int t0 = tt * NC_TT;
         const int nv = min(NC_TT, P.T - t0);
-        const float *go = P.gO + ((int64_t)z * P.T + t0) * P.D;
-        const float *v = P.V + ((int64_t)z * P.T + t0) * P.D;
         __syncthreads();  // the previous tile's readers of sG, sV and sPK are done
         for (int i = tid; i < NC_TT * DP; i += NC_NTH) {
             const int r = i / DP, d = i % DP;
             const bool ok = r < nv && d < P.D;
-            sG[r][d] = ok ? go[(int64_t)r * P.D + d] : 0.0f;
-            sV[r][d] = ok ? v[(int64_t)r * P.D + d] : 0.0f;
+            sG[r][d] = ok ? P.gO[nc_off(P.rG, P.zH, z, t0 + r) + d] : 0.0f;
+            sV[r][d] = ok ? P.V[nc_off(P.rV, P.zH, z, t0 + r) + d] : 0.0f;
         }
         constexpr int NO = NC_TT * DP / NC_NTH;     // gv outputs per thread
         constexpr int NS = NC_TT * NC_SC / NC_NTH;  // gpQ / gpK outputs per thread per chunk
@@ -213,12 +210,11 @@ __global__ __launch_bounds__(NC_NTH) void race_nc_backward(const NcParams P)
                 }
             }
         }
-        float *gV = P.gV + ((int64_t)z * P.T + t0) * P.D;
 #pragma unroll
         for (int o = 0; o < NO; ++o) {
             const int r = tid / DP + o * (NC_NTH / DP), d = tid % DP;
             if (r < nv && d < P.D)
-                gV[(int64_t)r * P.D + d] = gv[o];
+                P.gV[nc_off(P.rGV, P.zH, z, t0 + r) + d] = gv[o];
         }
     }
 }
@@ -291,7 +287,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
         }
         __syncthreads();
     }
-    const bool vec_d = (P.D & 3) == 0;
+    const bool vec_d = P.vec;
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
         const int t0 = st * NCM_TT + w * 16;
@@ -299,7 +295,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
             break;  // (uniform within the wave; no barrier inside the loop)
         const int t = t0 + n16;
         const bool ok = t < P.T;
-        const int64_t row = (int64_t)z * P.T + t;
+        const int64_t row = (int64_t)z * P.T + t;  // of the [N][T][S] probabilities
         f32x4 acc[DP / 16];
 #pragma unroll
         for (int j = 0; j < DP / 16; ++j)
@@ -308,7 +304,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
         if (ok) {
 #pragma unroll
             for (int j = 0; j < DP / 16; ++j)
-                put4(P.out + row * P.D, 16 * j + 4 * g, P.D, vec_d, acc[j]);
+                put4(P.out + nc_off(P.rO, P.zH, z, t), 16 * j + 4 * g, P.D, vec_d, acc[j]);
         }
     }
 }
@@ -362,7 +358,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         for (int e = 0; e < 4; ++e)
             ga[j][e] = sGA[16 * j + 4 * g + e];
     constexpr int NJ = DP / 16;  // 16-wide d runs: k-steps 4 NJ over d, output tiles NJ over d
-    const bool vec_d = (P.D & 3) == 0, vec_s = (P.S & 3) == 0;
+    const bool vec_d = P.vec, vec_s = (P.S & 3) == 0;
     // a token row's d values 16 j + 4 g .. + 3, zero past D
     auto row4 = [&](const float *row, int j, bool ok) {
         const int d = 16 * j + 4 * g;
@@ -385,14 +381,14 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             break;  // (uniform within the wave; no barrier inside the loop)
         const int t = t0 + n16;
         const bool ok = t < P.T;
-        const int64_t row = (int64_t)z * P.T + t;
+        const int64_t row = (int64_t)z * P.T + t;  // of the [N][T][S] probabilities
         // ---- gpQ^T[s][t] = E[s] . go_t
         f32x4 aq[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
         {
             f32x4 x[NJ];
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
-                x[j] = row4(P.gO + row * P.D, j, ok);
+                x[j] = row4(P.gO + nc_off(P.rG, P.zH, z, t), j, ok);
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const f32x4 e0 = *reinterpret_cast<const f32x4 *>(&sE[n16][16 * j + 4 * g]);
@@ -410,7 +406,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             f32x4 x[NJ];
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
-                x[j] = row4(P.V + row * P.D, j, ok);
+                x[j] = row4(P.V + nc_off(P.rV, P.zH, z, t), j, ok);
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&sGB[n16][16 * j + 4 * g]);
@@ -441,7 +437,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             av[j] = f32x4{0.f, 0.f, 0.f, 0.f};
         bucket_contract<DP, LDV>(av, sGBv, P.pK + row * P.S, ok, P.S, n16, g);
         if (ok) {
-            float *gv = P.gV + row * P.D;
+            float *gv = P.gV + nc_off(P.rGV, P.zH, z, t);
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
                 put4(gv, 16 * j + 4 * g, P.D, vec_d, av[j]);

@@ -42,8 +42,11 @@ struct ScanParams {
     View q, k, v, go;
     OutView out, dq, dk, dv;
     const float *planes;
-    // op mode (fp32): probabilities [N][T][S], values/grads [N][T][D]
+    // op mode (fp32): probabilities [N][T][S], values/grads rows of D floats. Stream z reads its
+    // V / gO rows as a [Z / zH][zH][T][D] view: row t of z at (z / zH) sb + (z % zH) sh + t st,
+    // strides in v / go (their p unused); contiguous [N][T][D] is zH = 1, sb = T D, st = D
     const float *pK, *pQ, *V, *gO;
+    int zH;
     float *gpK, *gpQ;
     // workspaces: block states [Z][NB+1][S_pad][DPw] and [Z][NB+1][S_pad]
     float *wsB, *wsA;    // forward: prefix (A, B) at each block start; slot NB = final

@@ -131,6 +131,12 @@ RACE_DEV void load_rows_bf16(__bf16 *dst, __bf16 *dstT, const View &vw, int b, i
     }
 }
 
+// op mode: first row of stream z in a V / gO view (ScanParams::zH; zH <= 1: stream stride sb)
+RACE_DEV const float *op_rows(const float *p, const View &v, int zH, int z)
+{
+    return zH <= 1 ? p + (int64_t)z * v.sb : p + (int64_t)(z / zH) * v.sb + (int64_t)(z % zH) * v.sh;
+}
+
 // Register-staged copy of one sub-chunk of an fp32 [N][T][ld] tensor (rows t0 .. t0 + C, columns
 // col0 .. col0 + W): fetch() issues this thread's loads, put() stores them to LDS [C][LD] and / or
 // transposed [W][LDT]. Loads go to clamped rows and columns (always inside the tensor) and are

@@ -139,10 +139,10 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
     // op mode: this sub-chunk's probabilities and values wait in registers, fetched one sub-chunk ahead
     SubChunkStage<C, ST, NTH> stP;
     SubChunkStage<C, DP, NTH> stV;
-    const float *srcP = P.pK + (int64_t)c.z * P.T * P.S, *srcV = P.V + (int64_t)c.z * P.T * P.D;
+    const float *srcP = P.pK + (int64_t)c.z * P.T * P.S, *srcV = op_rows(P.V, P.v, P.zH, c.z);
     if constexpr (!CF::QKV) {
         stP.fetch(srcP, P.S, c.s0, c.S_here, c.t_begin, P.T - 1, c.tid);
-        stV.fetch(srcV, P.D, 0, P.D, c.t_begin, P.T - 1, c.tid);
+        stV.fetch(srcV, (int)P.v.st, 0, P.D, c.t_begin, P.T - 1, c.tid);
     }
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
             stV.template put<T, LDC, LDC, false, true>(nullptr, &sVt[0][0], nv, P.D, c.tid);
             // next sub-chunk (past the block end: clamped rows, never stored)
             stP.fetch(srcP, P.S, c.s0, c.S_here, t0 + C, P.T - 1, c.tid);
-            stV.fetch(srcV, P.D, 0, P.D, t0 + C, P.T - 1, c.tid);
+            stV.fetch(srcV, (int)P.v.st, 0, P.D, t0 + C, P.T - 1, c.tid);
         }
         __syncthreads();
 #pragma unroll
@@ -265,11 +265,11 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
     SubChunkStage<C, ST, NTH> stK, stQ;
     SubChunkStage<C, DP, NTH> stV;
     const float *srcK = P.pK + (int64_t)c.z * P.T * P.S, *srcQ = P.pQ + (int64_t)c.z * P.T * P.S;
-    const float *srcV = P.V + (int64_t)c.z * P.T * P.D;
+    const float *srcV = op_rows(P.V, P.v, P.zH, c.z);
     if constexpr (!CF::QKV) {
         stK.fetch(srcK, P.S, c.s0, c.S_here, c.t_begin, P.T - 1, c.tid);
         stQ.fetch(srcQ, P.S, c.s0, c.S_here, c.t_begin, P.T - 1, c.tid);
-        stV.fetch(srcV, P.D, 0, P.D, c.t_begin, P.T - 1, c.tid);
+        stV.fetch(srcV, (int)P.v.st, 0, P.D, c.t_begin, P.T - 1, c.tid);
     }
     for (int sc = 0; sc < nsub; ++sc) {
         const int t0 = c.t_begin + sc * C;
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
             stV.template put<T, LDC, LDC, false, true>(nullptr, &sVt[0][0], nv, P.D, c.tid);
             stK.fetch(srcK, P.S, c.s0, c.S_here, t0 + C, P.T - 1, c.tid);
             stQ.fetch(srcQ, P.S, c.s0, c.S_here, t0 + C, P.T - 1, c.tid);
-            stV.fetch(srcV, P.D, 0, P.D, t0 + C, P.T - 1, c.tid);
+            stV.fetch(srcV, (int)P.v.st, 0, P.D, t0 + C, P.T - 1, c.tid);
         }
         __syncthreads();
 
@@ -479,12 +479,12 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
     SubChunkStage<C, ST, NTH> stK, stQ;
     SubChunkStage<C, DP, NTH> stV, stG;
     const float *srcK = P.pK + (int64_t)c.z * P.T * P.S, *srcQ = P.pQ + (int64_t)c.z * P.T * P.S;
-    const float *srcV = P.V + (int64_t)c.z * P.T * P.D, *srcG = P.gO + (int64_t)c.z * P.T * P.D;
+    const float *srcV = op_rows(P.V, P.v, P.zH, c.z), *srcG = op_rows(P.gO, P.go, P.zH, c.z);
     auto fetch_op = [&](int t) {
         stK.fetch(srcK, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
-        stV.fetch(srcV, P.D, 0, P.D, t, P.T - 1, c.tid);
+        stV.fetch(srcV, (int)P.v.st, 0, P.D, t, P.T - 1, c.tid);
         stQ.fetch(srcQ, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
-        stG.fetch(srcG, P.D, 0, P.D, t, P.T - 1, c.tid);
+        stG.fetch(srcG, (int)P.go.st, 0, P.D, t, P.T - 1, c.tid);
     };
     if constexpr (!CF::QKV)
         fetch_op(c.t_begin);
@@ -798,12 +798,12 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
     SubChunkStage<C, ST, NTH> stK, stQ;
     SubChunkStage<C, DP, NTH> stV, stG;
     const float *srcK = P.pK + (int64_t)c.z * P.T * P.S, *srcQ = P.pQ + (int64_t)c.z * P.T * P.S;
-    const float *srcV = P.V + (int64_t)c.z * P.T * P.D, *srcG = P.gO + (int64_t)c.z * P.T * P.D;
+    const float *srcV = op_rows(P.V, P.v, P.zH, c.z), *srcG = op_rows(P.gO, P.go, P.zH, c.z);
     auto fetch_op = [&](int t) {
         stK.fetch(srcK, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
-        stV.fetch(srcV, P.D, 0, P.D, t, P.T - 1, c.tid);
+        stV.fetch(srcV, (int)P.v.st, 0, P.D, t, P.T - 1, c.tid);
         stQ.fetch(srcQ, P.S, c.s0, c.S_here, t, P.T - 1, c.tid);
-        stG.fetch(srcG, P.D, 0, P.D, t, P.T - 1, c.tid);
+        stG.fetch(srcG, (int)P.go.st, 0, P.D, t, P.T - 1, c.tid);
     };
     if constexpr (!CF::QKV)
         fetch_op(c.t_begin);

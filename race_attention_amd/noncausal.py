@@ -7,7 +7,8 @@ temperature scale = exp(logit_temp).clamp(1e-2, 10) (benchmark_time.py:104,111).
 
 Here the summaries are the per-block totals of the causal scan machinery (one totals
 kernel and the block scan, whose last slot is the whole-sequence sum) and the readout
-and its backward are HIP kernels (race_nc_op_fwd / race_nc_op_bwd). The soft-hash runs
+and its backward are HIP kernels (race_nc_op_fwd / race_nc_op_bwd; race_nc_fwd_view /
+race_nc_bwd_view with the values in BatchedACE's [M,B,T,H,d_k] layout). The soft-hash runs
 in the HIP soft-hash kernels; with a learnable temperature its backward also returns
 d loss / d scale from per-workgroup partial sums (race_soft_hash_bwd_scale).
 """
@@ -18,7 +19,7 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import _lib
-from .race_causal_cuda import _op_inputs, op_state, state_arg
+from .race_causal_cuda import _op_inputs, op_state, state_arg, state_buffer
 from .race_common import _hash_shape
 
 
@@ -78,15 +79,79 @@ class RaceNonCausalFn(Function):
         return gpK, gpQ, gV.to(ctx.v_dtype), None
 
 
+def _bhtd(X5):
+    """[M,B,T,H,d] -> [M*B, H, T, d] view of the same storage, or None where its strides allow none."""
+    M, B, T, H, d = X5.shape
+    try:
+        return X5.permute(0, 1, 3, 2, 4).view(M * B, H, T, d)
+    except RuntimeError:
+        return None
+
+
+class RaceNonCausalViewFn(Function):
+    """out [M,B,T,H,d] fp32 = RaceNonCausalFn of probsK / probsQ [M*B*H, T, S] (streams ordered
+    (m, b, h)) and values Vhf [M,B,T,H,d]: values, output and their gradients stay in the
+    [M,B,T,H,d] layout (race_nc_fwd_view / race_nc_bwd_view), where the reference permutes them to
+    [N,T,d] and back (scaling/benchmark_time.py:116-128,164)."""
+
+    @staticmethod
+    def forward(ctx, probsK, probsQ, Vhf, eps):
+        _lib.require_device(probsK, probsQ, Vhf)
+        M, B, T, H, D = Vhf.shape
+        N, S = M * B * H, probsK.shape[-1]
+        if probsK.shape != (N, T, S) or probsQ.shape != probsK.shape:
+            raise ValueError(f"probsK/probsQ must be [{N},{T},S], got {tuple(probsK.shape)}, {tuple(probsQ.shape)}")
+        pK, pQ = probsK.contiguous().float(), probsQ.contiguous().float()
+        V = Vhf.float()
+        Vv = _bhtd(V)
+        if Vv is None:
+            Vv = V.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, D)
+        out = torch.empty(M, B, T, H, D, dtype=torch.float32, device=V.device)
+        lib = _lib.lib()
+        state = state_buffer(lib.race_op_state_bytes(N, T, S, D, 0), V.device, "race_op_state_bytes")
+        ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, 0, 0), V.device)
+        vv, Vv = _lib.view4(Vv)
+        ov, _ = _lib.view4(_bhtd(out))
+        _lib.check(lib.race_nc_fwd_view(_lib.ptr(pK), _lib.ptr(pQ), vv, ov, M * B, H, T, S, D, float(eps), 0,
+                                        _lib.ptr(ws), ws.numel(), *state_arg(state), _lib.stream_of(V)),
+                   "race_nc_fwd_view")
+        ctx.save_for_backward(pK, pQ, Vv, state)
+        ctx.shape = (M, B, T, H, D)
+        ctx.v_dtype = Vhf.dtype
+        ctx.eps = float(eps)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        pK, pQ, Vv, state = ctx.saved_tensors
+        M, B, T, H, D = ctx.shape
+        N, S = pK.shape[0], pK.shape[2]
+        g = grad_out.float()
+        gv_in = _bhtd(g)
+        if gv_in is None:
+            gv_in = g.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, D)
+        gpK, gpQ = torch.empty_like(pK), torch.empty_like(pQ)
+        gV = torch.empty(M, B, T, H, D, dtype=torch.float32, device=pK.device)
+        lib = _lib.lib()
+        ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, 0, 1), pK.device)
+        vv, _ = _lib.view4(Vv)
+        gov, gv_in = _lib.view4(gv_in)
+        gvv, _ = _lib.view4(_bhtd(gV))
+        _lib.check(lib.race_nc_bwd_view(_lib.ptr(pK), _lib.ptr(pQ), vv, gov, _lib.ptr(gpK), _lib.ptr(gpQ), gvv, M * B,
+                                        H, T, S, D, ctx.eps, 0, _lib.ptr(ws), ws.numel(), *state_arg(state),
+                                        _lib.stream_of(pK)), "race_nc_bwd_view")
+        return gpK, gpQ, gV.to(ctx.v_dtype), None
+
+
 class SoftHashTempFn(Function):
     """Soft-hash probabilities [Mp*B*H, T, L*2^K] of X [B,H,T,D] with a tensor scale;
     the backward returns d loss / d X and d loss / d scale."""
 
     @staticmethod
-    def forward(ctx, X, planes_T, L, Kbits, M, unshared, scale):
+    def forward(ctx, X, planes_T, L, Kbits, M, unshared, scale, scale_value=None):
         _lib.require_device(X, planes_T)
         B, H, T, D = X.shape
-        s = float(scale)
+        s = float(scale) if scale_value is None else float(scale_value)
         planes = planes_T.detach().float().contiguous()
         xv, Xc = _lib.view4(X)
         Mp = M if unshared else 1
@@ -116,7 +181,7 @@ class SoftHashTempFn(Function):
         _lib.check(lib.race_soft_hash_bwd_scale(sh, xv, _lib.dtype_code(Xc.dtype), _lib.ptr(planes), _lib.ptr(g),
                                                 dv, _lib.ptr(part), _lib.stream_of(Xc)), "race_soft_hash_bwd_scale")
         dscale = -part.double().sum() / s
-        return dX, None, None, None, None, None, dscale.to(torch.float32)
+        return dX, None, None, None, None, None, dscale.to(torch.float32), None
 
 
 class BatchedACE(nn.Module):
@@ -144,24 +209,24 @@ class BatchedACE(nn.Module):
         if M != self.M or dk != self.d_k:
             raise ValueError(f"expected [M={self.M},B,T,H,{self.d_k}] inputs, got {tuple(Khf.shape)}")
         scale = self.logit_temp.exp().clamp(1e-2, 10.0)
+        sv = float(scale)  # one host read of the temperature per call
         # streams ordered (M, B, H) as benchmark_time.py:121-131; one row of planes per m
         def bhtd(X):  # [M,B,T,H,dk] -> [M*B, H, T, dk] view
             return X.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, dk)
 
         if self.share_planes:
-            pK = SoftHashTempFn.apply(bhtd(Khf), self.planes_T, self.L, self.K, 1, False, scale)
-            pQ = SoftHashTempFn.apply(bhtd(Qhf), self.planes_T, self.L, self.K, 1, False, scale)
+            pK = SoftHashTempFn.apply(bhtd(Khf), self.planes_T, self.L, self.K, 1, False, scale, sv)
+            pQ = SoftHashTempFn.apply(bhtd(Qhf), self.planes_T, self.L, self.K, 1, False, scale, sv)
         else:
             # per-ensemble planes [M, dk, L*K]: member m hashes its own B*H rows
             Kx = Khf.permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
             Qx = Qhf.permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
-            pK = torch.cat([SoftHashTempFn.apply(Kx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale)
+            pK = torch.cat([SoftHashTempFn.apply(Kx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale, sv)
                             for m in range(M)], 0)
-            pQ = torch.cat([SoftHashTempFn.apply(Qx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale)
+            pQ = torch.cat([SoftHashTempFn.apply(Qx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale, sv)
                             for m in range(M)], 0)
-        V2 = Vhf.permute(0, 1, 3, 2, 4).reshape(M * B * H, T, dk)
-        out2 = RaceNonCausalFn.apply(pK, pQ, V2, eps)
-        return out2.view(M, B, H, T, dk).permute(0, 1, 3, 2, 4)
+        # values, output and gradients in the [M,B,T,H,dk] layout: no permute copies
+        return RaceNonCausalViewFn.apply(pK, pQ, Vhf, eps)
 
 
 def race_attention(Q, K, V, ace_module: BatchedACE, eps=1e-6):

@@ -103,6 +103,30 @@ def test_kept_state_must_be_aligned():
     assert rc == 1 and "256-byte aligned" in lib.race_last_error().decode()
 
 
+def test_nc_view_arguments_are_checked():
+    """race_nc_fwd_view / race_nc_bwd_view reject, on the host, bad stream counts, null views and
+    token strides below D, and check a given state's size as the kept entry points do."""
+    lib = _lib.load_library()
+    p = ctypes.c_void_p(256)
+    ok = _lib.Tensor4(256, 4 * 4096 * 64, 4096 * 64, 64)
+    ws = (ctypes.c_void_p(256), 1 << 30)
+    err = lambda: lib.race_last_error().decode()
+    assert lib.race_nc_fwd_view(p, p, ok, ok, 0, 4, 4096, 24, 64, 1e-6, 0, *ws, None, 0, None) == 1
+    assert "B and H must be positive" in err()
+    short = _lib.Tensor4(256, 0, 0, 32)
+    assert lib.race_nc_fwd_view(p, p, short, ok, 2, 4, 4096, 24, 64, 1e-6, 0, *ws, None, 0, None) == 1
+    assert "token stride" in err()
+    null = _lib.Tensor4(0, 0, 0, 64)
+    assert lib.race_nc_fwd_view(p, p, ok, null, 2, 4, 4096, 24, 64, 1e-6, 0, *ws, None, 0, None) == 1
+    assert "null out" in err()
+    assert lib.race_nc_bwd_view(p, p, ok, ok, p, p, null, 2, 4, 4096, 24, 64, 1e-6, 0, *ws, None, 0, None) == 1
+    assert "null gV" in err()
+    small = lib.race_op_state_bytes(8, 1024, 24, 64, 0)
+    assert lib.race_nc_bwd_view(p, p, ok, ok, p, p, ok, 2, 4, 4096, 24, 64, 1e-6, 0, *ws, ctypes.c_void_p(512),
+                                small, None) == 3
+    assert "state of" in err()
+
+
 KEPT = [("race_op_fwd_keep", 4), ("race_op_bwd_kept", 7), ("race_nc_op_fwd_keep", 4), ("race_nc_op_bwd_kept", 7),
         ("race_causal_dot_product_keep", 4), ("race_causal_dot_backward_kept", 7)]
 

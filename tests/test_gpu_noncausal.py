@@ -46,6 +46,42 @@ def test_noncausal_op(dev, N, T, S, D):
     check("gV", vx.grad, vr.grad, TOL)
 
 
+@pytest.mark.parametrize("S,D,pad", [(24, 128, 0), (30, 100, 1), (64, 64, 3)])
+def test_noncausal_view_layouts(dev, S, D, pad):
+    """race_nc_fwd_view / race_nc_bwd_view (RaceNonCausalViewFn): values and upstream gradient as
+    [M,B,T,H,D] slices of wider rows (odd pad: token and head strides not multiples of 4, rows
+    moved element-wise), output and gV written in [M,B,T,H,D], against the fp64 oracle on the
+    same streams in [N,T,D]; S <= 32 runs the matrix-core kernels, S = 64 the FMA ones."""
+    from race_attention_amd.noncausal import RaceNonCausalViewFn
+    M, B, T, H = 2, 2, 777, 3
+    N = M * B * H
+    print(f"nc view S={S} D={D} pad={pad}", flush=True)
+    g = torch.Generator().manual_seed(S + D + pad)
+    pk = torch.softmax(torch.randn(N, T, S, generator=g) * 2, -1)
+    pq = torch.softmax(torch.randn(N, T, S, generator=g) * 2, -1)
+    vfull = torch.randn(M, B, T, H, D + pad, generator=g)
+    gfull = torch.randn(M, B, T, H, D + pad, generator=g)
+    v5, go5 = vfull[..., :D], gfull[..., :D]
+    eps = 1e-6
+
+    def flat(x5):
+        return x5.permute(0, 1, 3, 2, 4).reshape(N, T, D)
+
+    pkr, pqr, vr = pk.double().requires_grad_(True), pq.double().requires_grad_(True), \
+        flat(v5).double().requires_grad_(True)
+    ref = orc.race_noncausal_ref(pkr, pqr, vr, eps)
+    ref.backward(flat(go5).double())
+    pkx, pqx = pk.to(dev).requires_grad_(True), pq.to(dev).requires_grad_(True)
+    vx = vfull.to(dev)[..., :D].detach().requires_grad_(True)
+    out = RaceNonCausalViewFn.apply(pkx, pqx, vx, eps)
+    assert out.shape == (M, B, T, H, D)
+    out.backward(gfull.to(dev)[..., :D])
+    check("out", flat(out), ref, TOL)
+    check("gpK", pkx.grad, pkr.grad, TOL)
+    check("gpQ", pqx.grad, pqr.grad, TOL)
+    check("gV", flat(vx.grad), vr.grad, TOL)
+
+
 def test_noncausal_block_invariance(dev):
     from race_attention_amd.noncausal import race_nc_fwd
     pk, pq, v, _ = _probs(2, 3000, 64, 64, seed=9)
