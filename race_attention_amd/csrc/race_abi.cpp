@@ -345,7 +345,8 @@ int race_soft_hash_bwd_partials(const race_hash_shape *sh)
 {
     if (!sh || sh->T <= 0 || sh->B <= 0 || sh->H <= 0)
         return 0;
-    return softhash_grid_x(sh->T, sh->B, sh->H) * sh->B * sh->H;
+    const bool mf = softhash_mfma_ok(sh->D, sh->L, sh->K, sh->M, 1);
+    return softhash_grid_x(sh->T, sh->B, sh->H, mf) * sh->B * sh->H;
 }
 
 int race_soft_hash_bwd_scale(const race_hash_shape *sh, race_tensor x, int x_dtype, const float *planes_T,

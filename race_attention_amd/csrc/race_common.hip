@@ -745,7 +745,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_fwd_mfma(SoftHashPar
     const TX *x = reinterpret_cast<const TX *>(P.x.p) + b * P.x.sb + h * P.x.sh;
     shm_load_planes(sPlT, nullptr, P.planes + (int64_t)m * P.plane_stride, P, Y);
     __syncthreads();
-    const int span = P.tpw * SH_TT;
+    const int span = P.tpw * SHM_W * 16;
     const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
     for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
         const int t = t0 + n16;
@@ -816,7 +816,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
     shm_load_planes(sPlT, sPl, P.planes, P, Y);
     __syncthreads();
     float gsu = 0.0f;  // sum of gu * u over this lane's (token, table) items
-    const int span = P.tpw * SH_TT;
+    const int span = P.tpw * SHM_W * 16;
     const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
     for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
         const int t = t0 + n16;
@@ -972,17 +972,22 @@ size_t softhash_smem(int D, int LK, bool bwd)
     return sizeof(float) * (DX * sh_pl(LK) + SH_TT * DX + (size_t)SH_TT * LK + (bwd ? (size_t)SH_TT * sh_pg(LK) : 0));
 }
 
-int softhash_tiles_per_wg(int T, int B, int H)
+// tokens per tile: SH_TT for the FMA kernels, one 16-token tile per wave for the matrix-core ones
+static int softhash_tile(bool mf) { return mf ? SHM_W * 16 : SH_TT; }
+
+int softhash_tiles_per_wg(int T, int B, int H, bool mf)
 {
     // a workgroup walks up to 32 consecutive tiles of one (b, h) (planes loaded once), as long as
     // the grid keeps about 2048 workgroups (8 per CU)
-    const int64_t tiles = (int64_t)((T + SH_TT - 1) / SH_TT) * B * H;
+    const int tile = softhash_tile(mf);
+    const int64_t tiles = (int64_t)((T + tile - 1) / tile) * B * H;
     return (int)std::max<int64_t>(1, std::min<int64_t>(32, tiles / 2048));
 }
 
-int softhash_grid_x(int T, int B, int H)
+int softhash_grid_x(int T, int B, int H, bool mf)
 {
-    const int ntt = (T + SH_TT - 1) / SH_TT, tpw = softhash_tiles_per_wg(T, B, H);
+    const int tile = softhash_tile(mf);
+    const int ntt = (T + tile - 1) / tile, tpw = softhash_tiles_per_wg(T, B, H, mf);
     return (ntt + tpw - 1) / tpw;
 }
 
@@ -995,11 +1000,11 @@ hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream
                         : (bf16 ? softhash_kernel_k<__bf16>(P.K, bwd, P.D) : softhash_kernel_k<float>(P.K, bwd, P.D));
     if (!fn)
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)softhash_grid_x(P.T, P.B, P.H), (unsigned)(P.B * P.H),
+    const dim3 grid((unsigned)softhash_grid_x(P.T, P.B, P.H, mf), (unsigned)(P.B * P.H),
                     (unsigned)(bwd ? 1 : (P.unshared ? P.M : 1)));
     const size_t smem = mf ? sizeof(float) * Y.floats(bwd) : softhash_smem(P.D, P.LK, bwd);
     SoftHashParams args = P;
-    args.tpw = softhash_tiles_per_wg(P.T, P.B, P.H);
+    args.tpw = softhash_tiles_per_wg(P.T, P.B, P.H, mf);
     void *argv[] = {&args};
     return hipLaunchKernel(fn, grid, dim3(256), argv, smem, s);
 }

@@ -21,12 +21,14 @@ struct SoftHashParams {
     int round_planes;     // 1: round planes to bf16 (bf16 inputs, as race_common.py:54)
     float scale, inv_scale;
     float *gscale;        // backward, optional: per-workgroup sums of gu * u (temperature grad)
-    int tpw;              // tiles per workgroup (set by launch_softhash)
+    int tpw;              // token tiles per workgroup (set by launch_softhash)
 };
 
 size_t softhash_smem(int D, int LK, bool bwd);
-int softhash_tiles_per_wg(int T, int B, int H);
-int softhash_grid_x(int T, int B, int H);  // workgroups along the tiles of one (b, h)
+// mf: the matrix-core kernels (softhash_mfma_ok) with their own token tile
+bool softhash_mfma_ok(int D, int L, int K, int M, int bwd);
+int softhash_tiles_per_wg(int T, int B, int H, bool mf);
+int softhash_grid_x(int T, int B, int H, bool mf);  // workgroups along the tiles of one (b, h)
 hipError_t softhash_prepare(int D, int LK);
 hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s);
 

@@ -164,10 +164,11 @@ def test_soft_hash_probs_fp32(dev):
 
 
 @pytest.mark.parametrize("B,H,T,D,L,Kb,M,share", [(4, 8, 4141, 64, 4, 3, 2, False), (4, 8, 16389, 64, 2, 2, 1, True),
-                                                   (1, 8, 262221, 16, 3, 3, 1, True)])
+                                                   (1, 8, 524365, 16, 3, 3, 1, True)])
 def test_soft_hash_probs_multi_tile(dev, B, H, T, D, L, Kb, M, share):
-    """Enough 32-token tiles that each soft-hash workgroup walks several of them (2, 8 and 32 per
-    workgroup here), with a ragged last tile and a last workgroup that holds fewer tiles."""
+    """Enough token tiles (32 tokens for the FMA kernels, 64 for the matrix-core ones) that each
+    soft-hash workgroup walks several of them (1 to 32 per workgroup here), with a ragged last tile
+    and a last workgroup that holds fewer tiles."""
     from race_attention_amd import build_planes_protos, soft_hash_probs
     print(f"case B={B} H={H} T={T} D={D} L={L} K={Kb} M={M} share={share}", flush=True)
     planes_T, protos_T = build_planes_protos(D, Kb, L, M, device=dev, share_planes=share, seed=4)
