@@ -714,8 +714,13 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
 // backward totals kernel added (see ga_accum), so the subtraction cancels exactly:
 //   dS_end(c)   = dS_start(c) - W_c^T go_c
 //   gAhat_end(c)= gAhat_start(c) - colsum(gA_c)
+// two 8-wave workgroups per CU where the 64 x 64 tile's LDS allows them (81.7 KB): 128 VGPRs
+template <int ST, int DP, int NW>
+constexpr int bwd_main_waves_per_eu() { return ST == 64 && DP == 64 && NW == 8 ? 4 : 1; }
+
 template <class E, int MODE, int ST, int DP, int C, int NW>
-__global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(bwd_main_waves_per_eu<ST, DP, NW>())))
+void race_bwd_main(const ScanParams P)
 {
     using CF = Cfg<E, MODE, ST, DP, C, NW>;
     using T = typename E::T;
@@ -735,8 +740,12 @@ __global__ __launch_bounds__(NW * 64) void race_bwd_main(const ScanParams P)
     __shared__ __align__(16) float sF[C][LDF];
     __shared__ __align__(16) T sW[C][LDS_];
     __shared__ __align__(16) T sWt[ST][LDC];
+    // sStS (the state at the sub-chunk start, read by gW = go St^T inside the query-head loop) and
+    // sdS (the suffix after the sub-chunk, written after that loop and read by gpK += V dS^T) are
+    // never live together: barriers separate the loop's last read from the dS store and the dS
+    // products from the next sub-chunk's St store
     __shared__ __align__(16) T sStS[ST][LDX];
-    __shared__ __align__(16) T sdS[ST][LDX];
+    T(*sdS)[LDX] = sStS;
     __shared__ __align__(16) T sdSt[DP][LDS_];
     __shared__ __align__(16) T sMg[C][LDC];
     __shared__ __align__(16) T sMv[C][LDC];
