@@ -407,8 +407,13 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
 }
 
 // ============================================================================ backward totals
+// op mode's fp32 64 x 64 tile: three 4-wave workgroups per CU (168 VGPRs) instead of two
+template <int MODE, int ST, int DP, int NW>
+constexpr int bwd_totals_waves_per_eu() { return MODE == 0 && ST == 64 && DP == 64 && NW == 4 ? 3 : 1; }
+
 template <class E, int MODE, int ST, int DP, int C, int NW>
-__global__ __launch_bounds__(NW * 64) void race_bwd_totals(const ScanParams P)
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(bwd_totals_waves_per_eu<MODE, ST, DP, NW>())))
+void race_bwd_totals(const ScanParams P)
 {
     using CF = Cfg<E, MODE, ST, DP, C, NW>;
     using T = typename E::T;
