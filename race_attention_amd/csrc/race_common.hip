@@ -622,11 +622,14 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
 // per-wave LDS rows between the MFMA layout and the (token, table) items.
 constexpr int SHM_W = 4;  // waves per workgroup
 
+// compiled head-dim class of the matrix-core soft-hash kernels
+__host__ __device__ inline int shm_dp(int D) { return D <= 64 ? 64 : D <= 128 ? 128 : 256; }
+
 struct ShmLayout {
-    int DX16, PT, PD, PU, njt;  // d rounded to 16, pitches (floats), plane tiles of 16
+    int DX16, PT, PD, PU, njt;  // d rounded to the head-dim class, pitches (floats), plane tiles of 16
     __host__ __device__ ShmLayout(int D, int LK)
     {
-        DX16 = (D + 15) & ~15;
+        DX16 = shm_dp(D);
         PT = DX16 + 8;  // odd multiple of 8
         PD = (LK + 3) & ~3;
         if (((PD / 4) & 1) == 0)
@@ -672,48 +675,48 @@ RACE_DEV void shm_load_planes(float *sPlT, float *sPl, const float *planes, cons
     }
 }
 
-// 4 consecutive x elements d .. d + 3 of a token row (zero past D)
-template <class TX>
-RACE_DEV f32x4 shm_x4(const TX *row, int d, int D, bool vec)
-{
-    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (d >= D)
-        return v;
-    if (vec) {
-        typedef TX tx4 __attribute__((ext_vector_type(4)));
-        const tx4 w = *reinterpret_cast<const tx4 *>(row + d);
-        return f32x4{(float)w[0], (float)w[1], (float)w[2], (float)w[3]};
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-        v[e] = d + e < D ? (float)row[d + e] : 0.0f;
-    return v;
-}
-
-// u = tanh(x . planes) / scale of this wave's 16 tokens into its sU rows [16][PU]
-template <class TX, int NJT>
+// u = tanh(x . planes) / scale of this wave's 16 tokens into its sU rows [16][PU]. x rows are
+// read from a clamped row and clamped columns (always inside the tensor), and elements past D or of
+// tokens past the tile (ok false) are selected to zero: no branch per 16-wide chunk
+template <class TX, int NJT, int DP>
 RACE_DEV void shm_project(float *sU, const float *sPlT, const SoftHashParams &P, const ShmLayout &Y, const TX *xrow,
                           bool ok, bool vec, int n16, int g)
 {
-    f32x4 xv[16];
+    constexpr int NJ = DP / 16;
+    f32x4 xv[NJ];
+    if (vec) {
+        typedef TX tx4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj)
-        if (16 * jj < P.D)
-            xv[jj] = ok ? shm_x4<TX>(xrow, 16 * jj + 4 * g, P.D, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int jj = 0; jj < NJ; ++jj) {
+            const int d = 16 * jj + 4 * g;
+            const tx4 w = *reinterpret_cast<const tx4 *>(xrow + min(d, P.D - 4));
+            const bool in = ok && d < P.D;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                xv[jj][e] = in ? (float)w[e] : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = 16 * jj + 4 * g + e;
+                const float v = (float)xrow[min(d, P.D - 1)];
+                xv[jj][e] = ok && d < P.D ? v : 0.0f;
+            }
+    }
     f32x4 acc[NJT];
 #pragma unroll
     for (int jt = 0; jt < NJT; ++jt)
         acc[jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-        if (16 * jj < P.D) {
+    for (int jj = 0; jj < NJ; ++jj) {
 #pragma unroll
-            for (int jt = 0; jt < NJT; ++jt) {
-                const f32x4 pt = *reinterpret_cast<const f32x4 *>(sPlT + (16 * jt + n16) * Y.PT + 16 * jj + 4 * g);
+        for (int jt = 0; jt < NJT; ++jt) {
+            const f32x4 pt = *reinterpret_cast<const f32x4 *>(sPlT + (16 * jt + n16) * Y.PT + 16 * jj + 4 * g);
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    EngF32::mma(acc[jt], pt[e], xv[jj][e]);
-            }
+            for (int e = 0; e < 4; ++e)
+                EngF32::mma(acc[jt], pt[e], xv[jj][e]);
         }
     }
     // accumulator rows: planes 16 jt + 4 g + e of token n16
@@ -727,7 +730,7 @@ RACE_DEV void shm_project(float *sU, const float *sPlT, const SoftHashParams &P,
     }
 }
 
-template <class TX, int KB, int NJT>
+template <class TX, int KB, int NJT, int DP>
 __global__ __launch_bounds__(SHM_W * 64) void race_softhash_fwd_mfma(SoftHashParams P)
 {
     extern __shared__ float sm[];
@@ -749,7 +752,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_fwd_mfma(SoftHashPar
     const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
     for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
         const int t = t0 + n16;
-        shm_project<TX, NJT>(sU, sPlT, P, Y, x + (int64_t)t * P.x.st, t < tok1, vec_x, n16, g);
+        shm_project<TX, NJT, DP>(sU, sPlT, P, Y, x + (int64_t)min(t, tok1 - 1) * P.x.st, t < tok1, vec_x, n16, g);
         const int nv = min(16, tok1 - t0);
         if constexpr (KB >= 2) {
             if (vec_out) {
@@ -790,7 +793,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_fwd_mfma(SoftHashPar
     }
 }
 
-template <class TX, int KB, int NJT>
+template <class TX, int KB, int NJT, int DP>
 __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashParams P)
 {
     extern __shared__ float sm[];
@@ -820,7 +823,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
     const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
     for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
         const int t = t0 + n16;
-        shm_project<TX, NJT>(sU, sPlT, P, Y, x + (int64_t)t * P.x.st, t < tok1, vec_x, n16, g);
+        shm_project<TX, NJT, DP>(sU, sPlT, P, Y, x + (int64_t)min(t, tok1 - 1) * P.x.st, t < tok1, vec_x, n16, g);
         // (token, table) items: gu_k = d loss / d u_k, gproj = gu * (1 - tanh^2) / scale
         for (int i = lane; i < 16 * P.L; i += 64) {
             const int r = i / P.L, l = i - r * P.L;
@@ -878,26 +881,25 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
                 sGP[r * Y.PD + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
             }
         }
-        // dx^T tiles of 16 d: A = planes rows d (4-byte reads, pitch 4 x odd), B = gproj of token n16
+        // dx^T tiles of 16 d: A = planes rows d (4-byte reads, pitch 4 x odd), B = gproj of token n16;
+        // k-steps over the planes (L*K <= 16 NJT, rounded to 4)
         const int nks = (P.LK + 3) / 4;
+        TX *o = dx + (int64_t)t * P.dx.st;
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-            if (16 * jj < P.D) {
-                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-                for (int kk = 0; kk < nks; ++kk)
-                    EngF32::mma(acc, sPl[(16 * jj + n16) * Y.PD + 4 * kk + g], sGP[n16 * Y.PD + 4 * kk + g]);
-                if (t < tok1) {
-                    TX *o = dx + (int64_t)t * P.dx.st;
-                    const int d = 16 * jj + 4 * g;
-                    if (vec_dx && d + 4 <= P.D) {
-                        typedef TX tx4 __attribute__((ext_vector_type(4)));
-                        *reinterpret_cast<tx4 *>(o + d) = tx4{(TX)acc[0], (TX)acc[1], (TX)acc[2], (TX)acc[3]};
-                    } else {
+        for (int jj = 0; jj < DP / 16; ++jj) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int kk = 0; kk < nks; ++kk)
+                EngF32::mma(acc, sPl[(16 * jj + n16) * Y.PD + 4 * kk + g], sGP[n16 * Y.PD + 4 * kk + g]);
+            const int d = 16 * jj + 4 * g;
+            if (t < tok1 && d < P.D) {
+                if (vec_dx) {
+                    typedef TX tx4 __attribute__((ext_vector_type(4)));
+                    *reinterpret_cast<tx4 *>(o + d) = tx4{(TX)acc[0], (TX)acc[1], (TX)acc[2], (TX)acc[3]};
+                } else {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (d + e < P.D)
-                                o[d + e] = (TX)acc[e];
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        if (d + e < P.D)
+                            o[d + e] = (TX)acc[e];
                 }
             }
         }
@@ -920,22 +922,31 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
     }
 }
 
-template <class TX, int KB>
-static const void *softhash_mfma_kernel(int bwd, int njt)
+template <class TX, int KB, int NJT>
+static const void *softhash_mfma_kernel(int bwd, int dp)
 {
     if (bwd)
-        return njt == 1 ? (const void *)race_softhash_bwd_mfma<TX, KB, 1> : (const void *)race_softhash_bwd_mfma<TX, KB, 2>;
-    return njt == 1 ? (const void *)race_softhash_fwd_mfma<TX, KB, 1> : (const void *)race_softhash_fwd_mfma<TX, KB, 2>;
+        return dp == 64 ? (const void *)race_softhash_bwd_mfma<TX, KB, NJT, 64>
+                        : dp == 128 ? (const void *)race_softhash_bwd_mfma<TX, KB, NJT, 128>
+                                    : (const void *)race_softhash_bwd_mfma<TX, KB, NJT, 256>;
+    return dp == 64 ? (const void *)race_softhash_fwd_mfma<TX, KB, NJT, 64>
+                    : dp == 128 ? (const void *)race_softhash_fwd_mfma<TX, KB, NJT, 128>
+                                : (const void *)race_softhash_fwd_mfma<TX, KB, NJT, 256>;
 }
 
+// kernel of bit count K (1..4), plane tiles njt (1, 2) and head-dim class dp (64, 128, 256)
 template <class TX>
-static const void *softhash_mfma_kernel_k(int K, int bwd, int njt)
+static const void *softhash_mfma_kernel_k(int K, int bwd, int njt, int dp)
 {
-    switch (K) {
-    case 1: return softhash_mfma_kernel<TX, 1>(bwd, njt);
-    case 2: return softhash_mfma_kernel<TX, 2>(bwd, njt);
-    case 3: return softhash_mfma_kernel<TX, 3>(bwd, njt);
-    case 4: return softhash_mfma_kernel<TX, 4>(bwd, njt);
+    switch (K * 2 + njt - 1) {
+    case 2: return softhash_mfma_kernel<TX, 1, 1>(bwd, dp);
+    case 3: return softhash_mfma_kernel<TX, 1, 2>(bwd, dp);
+    case 4: return softhash_mfma_kernel<TX, 2, 1>(bwd, dp);
+    case 5: return softhash_mfma_kernel<TX, 2, 2>(bwd, dp);
+    case 6: return softhash_mfma_kernel<TX, 3, 1>(bwd, dp);
+    case 7: return softhash_mfma_kernel<TX, 3, 2>(bwd, dp);
+    case 8: return softhash_mfma_kernel<TX, 4, 1>(bwd, dp);
+    case 9: return softhash_mfma_kernel<TX, 4, 2>(bwd, dp);
     default: return nullptr;
     }
 }
@@ -978,10 +989,11 @@ static int softhash_tile(bool mf) { return mf ? SHM_W * 16 : SH_TT; }
 int softhash_tiles_per_wg(int T, int B, int H, bool mf)
 {
     // a workgroup walks up to 32 consecutive tiles of one (b, h) (planes loaded once), as long as
-    // the grid keeps about 2048 workgroups (8 per CU)
+    // the grid keeps about 2048 workgroups (8 per CU; the FMA kernels) or 8192 (the matrix-core
+    // kernels, about 5 resident per CU: several rounds, so the last one's tail is short)
     const int tile = softhash_tile(mf);
     const int64_t tiles = (int64_t)((T + tile - 1) / tile) * B * H;
-    return (int)std::max<int64_t>(1, std::min<int64_t>(32, tiles / 2048));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(32, tiles / (mf ? 8192 : 2048)));
 }
 
 int softhash_grid_x(int T, int B, int H, bool mf)
@@ -995,8 +1007,8 @@ hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream
 {
     const bool mf = softhash_mfma_ok(P.D, P.L, P.K, P.M, bwd);
     const ShmLayout Y(P.D, P.LK);
-    const void *fn = mf ? (bf16 ? softhash_mfma_kernel_k<__bf16>(P.K, bwd, Y.njt)
-                                : softhash_mfma_kernel_k<float>(P.K, bwd, Y.njt))
+    const void *fn = mf ? (bf16 ? softhash_mfma_kernel_k<__bf16>(P.K, bwd, Y.njt, Y.DX16)
+                                : softhash_mfma_kernel_k<float>(P.K, bwd, Y.njt, Y.DX16))
                         : (bf16 ? softhash_kernel_k<__bf16>(P.K, bwd, P.D) : softhash_kernel_k<float>(P.K, bwd, P.D));
     if (!fn)
         return hipErrorInvalidValue;
@@ -1018,10 +1030,10 @@ hipError_t softhash_prepare(int D, int LK)
     if (D <= 256 && LK <= 32 && smem_mf > 64 * 1024) {
         for (int K = 1; K <= 4 && e == hipSuccess; ++K)
             for (int bwd = 0; bwd < 2 && e == hipSuccess; ++bwd) {
-                e = hipFuncSetAttribute(softhash_mfma_kernel_k<float>(K, bwd, Y.njt),
+                e = hipFuncSetAttribute(softhash_mfma_kernel_k<float>(K, bwd, Y.njt, Y.DX16),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, smem_mf);
                 if (e == hipSuccess)
-                    e = hipFuncSetAttribute(softhash_mfma_kernel_k<__bf16>(K, bwd, Y.njt),
+                    e = hipFuncSetAttribute(softhash_mfma_kernel_k<__bf16>(K, bwd, Y.njt, Y.DX16),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, smem_mf);
             }
     }
