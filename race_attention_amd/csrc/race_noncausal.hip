@@ -246,17 +246,22 @@ __device__ __forceinline__ void put4(float *row, int c, int ncol, bool vec, cons
     }
 }
 
-// acc[j] (j < DP / 16) += X^T p^T for one 16-token tile: X is a [32][LD] bucket-by-d table in LDS
-// (rows >= S zero), p the lane's token row of S bucket probabilities; lane (n, g) holds
-// p[4 kk + g] for k-step kk and reads X[4 kk + g][16 j + n] (banks 16 g + n for LD = 16 x odd)
-template <int DP, int LD>
-__device__ __forceinline__ void bucket_contract(f32x4 (&acc)[DP / 16], const float (*X)[LD], const float *p, bool ok,
-                                                int S, int n16, int g)
+// The lane's bucket probabilities p[4 kk + g] (k-step kk) of one token row, zero for buckets >= S
+// and when the token is outside the sequence (ok false)
+__device__ __forceinline__ void bucket_row(float (&pv)[8], const float *p, bool ok, int S, int g)
 {
-    float pv[8];
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
         pv[kk] = (ok && 4 * kk + g < S) ? p[4 * kk + g] : 0.0f;
+}
+
+// acc[j] (j < DP / 16) += X^T p^T for one 16-token tile: X is a [32][LD] bucket-by-d table in LDS
+// (rows >= S zero), pv the lane's bucket_row; lane (n, g) reads X[4 kk + g][16 j + n] (banks
+// 16 g + n for LD = 16 x odd)
+template <int DP, int LD>
+__device__ __forceinline__ void bucket_contract(f32x4 (&acc)[DP / 16], const float (*X)[LD], const float (&pv)[8],
+                                                int S, int n16, int g)
+{
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
         if (4 * kk < S) {
@@ -289,18 +294,31 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
     }
     const bool vec_d = P.vec;
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
+    // this step's pQ row waits in registers, loaded one step ahead
+    float pv[8];
+    {
+        const int t = blockIdx.x * P.tpw * NCM_TT + w * 16 + n16;
+        bucket_row(pv, P.pQ + ((int64_t)z * P.T + t) * P.S, t < P.T, P.S, g);
+    }
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
         const int t0 = st * NCM_TT + w * 16;
         if (t0 >= P.T)
             break;  // (uniform within the wave; no barrier inside the loop)
         const int t = t0 + n16;
         const bool ok = t < P.T;
-        const int64_t row = (int64_t)z * P.T + t;  // of the [N][T][S] probabilities
         f32x4 acc[DP / 16];
 #pragma unroll
         for (int j = 0; j < DP / 16; ++j)
             acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        bucket_contract<DP, LDV>(acc, sEv, P.pQ + row * P.S, ok, P.S, n16, g);
+        float pn[8];
+        {
+            const int tn = t + NCM_TT;  // the next step's token (loaded only inside the range)
+            bucket_row(pn, P.pQ + ((int64_t)z * P.T + tn) * P.S, st + 1 < st1 && tn < P.T, P.S, g);
+        }
+        bucket_contract<DP, LDV>(acc, sEv, pv, P.S, n16, g);
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            pv[kk] = pn[kk];
         if (ok) {
 #pragma unroll
             for (int j = 0; j < DP / 16; ++j)
@@ -435,7 +453,11 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
             av[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        bucket_contract<DP, LDV>(av, sGBv, P.pK + row * P.S, ok, P.S, n16, g);
+        {
+            float pv[8];
+            bucket_row(pv, P.pK + row * P.S, ok, P.S, g);
+            bucket_contract<DP, LDV>(av, sGBv, pv, P.S, n16, g);
+        }
         if (ok) {
             float *gv = P.gV + nc_off(P.rGV, P.zH, z, t);
 #pragma unroll
