@@ -279,7 +279,9 @@ template <int DP>
 __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P)
 {
     constexpr int LDV = DP + 16;
+    constexpr int HW = DP < 64 ? DP : 64, LDO = HW + 4;  // output staging: 64-column halves
     __shared__ __align__(16) float sEv[32][LDV];
+    __shared__ __align__(16) float sO[NCM_W][16][LDO];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, z = blockIdx.y;
     const int n16 = lane & 15, g = lane >> 4;
     {
@@ -319,10 +321,21 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
             pv[kk] = pn[kk];
-        if (ok) {
+        // through this wave's LDS rows, 64 columns at a time, so that each store instruction writes
+        // whole 256-byte runs of HW / 4 lanes per token row (in order within the wave: no barrier)
+        constexpr int LPR = HW / 4, RPI = 64 / LPR;  // lanes per row, rows per instruction
 #pragma unroll
-            for (int j = 0; j < DP / 16; ++j)
-                put4(P.out + nc_off(P.rO, P.zH, z, t), 16 * j + 4 * g, P.D, vec_d, acc[j]);
+        for (int h = 0; h < DP / HW; ++h) {
+#pragma unroll
+            for (int j = 0; j < HW / 16; ++j)
+                *reinterpret_cast<f32x4 *>(&sO[w][n16][16 * j + 4 * g]) = acc[h * (HW / 16) + j];
+#pragma unroll
+            for (int it = 0; it < 16 / RPI; ++it) {
+                const int r = it * RPI + lane / LPR, c = 4 * (lane % LPR);
+                const f32x4 x = *reinterpret_cast<const f32x4 *>(&sO[w][r][c]);
+                if (t0 + r < P.T)
+                    put4(P.out + nc_off(P.rO, P.zH, z, t0 + r), HW * h + c, P.D, vec_d, x);
+            }
         }
     }
 }
