@@ -340,6 +340,67 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
     }
 }
 
+// A wave's 16-token tile of a row view moved in row-contiguous runs: 32-column chunks, lane l
+// covering row it * 8 + l / 8 (it = 0, 1) at columns 32 c + 4 (l % 8), so a load or store
+// instruction touches 8 rows x 128 bytes; the chunk passes through per-wave LDS rows (pitch 4 x odd
+// words) to or from the MFMA layout, lane (n, g) holding columns 16 j + 4 g .. + 3 of row n.
+constexpr int NCS_LD = 32 + 4;
+
+template <int DP>
+struct RowTile {
+    f32x4 x[DP / 32][2];
+
+    __device__ void load(const float *base, const NcRows &rr, int zH, int z, int t0, int T, int D, bool vec, int lane)
+    {
+#pragma unroll
+        for (int c = 0; c < DP / 32; ++c)
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+                const int r = it * 8 + lane / 8, col = 32 * c + 4 * (lane % 8);
+                f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                if (t0 + r < T && col < D) {
+                    const float *p = base + nc_off(rr, zH, z, t0 + r) + col;
+                    if (vec) {
+                        v = *reinterpret_cast<const f32x4 *>(p);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            v[e] = col + e < D ? p[e] : 0.0f;
+                    }
+                }
+                x[c][it] = v;
+            }
+    }
+    // chunk c into the staging rows, then the MFMA-layout runs of columns 32 c + 16 jj + 4 g
+    __device__ void frags(float (*sX)[NCS_LD], int c, int lane, int n16, int g, f32x4 &f0, f32x4 &f1) const
+    {
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+            *reinterpret_cast<f32x4 *>(&sX[it * 8 + lane / 8][4 * (lane % 8)]) = x[c][it];
+        f0 = *reinterpret_cast<const f32x4 *>(&sX[n16][4 * g]);
+        f1 = *reinterpret_cast<const f32x4 *>(&sX[n16][16 + 4 * g]);
+    }
+};
+
+// MFMA-layout runs acc[j] (columns 16 j + 4 g .. + 3 of row n) stored as row-contiguous runs
+template <int DP>
+__device__ void store_rows(float (*sX)[NCS_LD], const f32x4 (&acc)[DP / 16], float *base, const NcRows &rr, int zH,
+                           int z, int t0, int T, int D, bool vec, int lane, int n16, int g)
+{
+#pragma unroll
+    for (int c = 0; c < DP / 32; ++c) {
+        *reinterpret_cast<f32x4 *>(&sX[n16][4 * g]) = acc[2 * c];
+        *reinterpret_cast<f32x4 *>(&sX[n16][16 + 4 * g]) = acc[2 * c + 1];
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int r = it * 8 + lane / 8, col = 4 * (lane % 8);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&sX[r][col]);
+            if (t0 + r < T)
+                put4(base + nc_off(rr, zH, z, t0 + r), 32 * c + col, D, vec, v);
+        }
+    }
+}
+
 template <int DP>
 __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams P)
 {
@@ -348,6 +409,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
     __shared__ __align__(16) float sGB[32][LDD];
     __shared__ __align__(16) float sGBv[32][LDV];
     __shared__ float sGA[32];
+    __shared__ __align__(16) float sXs[NCM_W][16][NCS_LD];  // per-wave row staging
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, z = blockIdx.y;
     const int n16 = lane & 15, g = lane >> 4;
     // E, gB (and gA) of stream z: rows s < S, zero beyond
@@ -390,21 +452,6 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             ga[j][e] = sGA[16 * j + 4 * g + e];
     constexpr int NJ = DP / 16;  // 16-wide d runs: k-steps 4 NJ over d, output tiles NJ over d
     const bool vec_d = P.vec, vec_s = (P.S & 3) == 0;
-    // a token row's d values 16 j + 4 g .. + 3, zero past D
-    auto row4 = [&](const float *row, int j, bool ok) {
-        const int d = 16 * j + 4 * g;
-        f32x4 x = {0.f, 0.f, 0.f, 0.f};
-        if (ok && d < P.D) {
-            if (vec_d) {
-                x = *reinterpret_cast<const f32x4 *>(row + d);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    x[e] = d + e < P.D ? row[d + e] : 0.0f;
-            }
-        }
-        return x;
-    };
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
         const int t0 = st * NCM_TT + w * 16;
@@ -413,41 +460,34 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         const int t = t0 + n16;
         const bool ok = t < P.T;
         const int64_t row = (int64_t)z * P.T + t;  // of the [N][T][S] probabilities
-        // ---- gpQ^T[s][t] = E[s] . go_t
+        float (*sX)[NCS_LD] = sXs[w];
+        // ---- gpQ^T[s][t] = E[s] . go_t ; gpK^T[s][t] = gA[s] + gB[s] . v_t
         f32x4 aq[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        {
-            f32x4 x[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-                x[j] = row4(P.gO + nc_off(P.rG, P.zH, z, t), j, ok);
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const f32x4 e0 = *reinterpret_cast<const f32x4 *>(&sE[n16][16 * j + 4 * g]);
-                const f32x4 e1 = *reinterpret_cast<const f32x4 *>(&sE[16 + n16][16 * j + 4 * g]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    EngF32::mma(aq[0], e0[e], x[j][e]);
-                    EngF32::mma(aq[1], e1[e], x[j][e]);
-                }
-            }
-        }
-        // ---- gpK^T[s][t] = gA[s] + gB[s] . v_t
         f32x4 ak[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        {
-            f32x4 x[NJ];
+        auto contract = [&](const RowTile<DP> &rt, const float (*X)[LDD], f32x4 (&a)[2]) {
 #pragma unroll
-            for (int j = 0; j < NJ; ++j)
-                x[j] = row4(P.V + nc_off(P.rV, P.zH, z, t), j, ok);
+            for (int c = 0; c < DP / 32; ++c) {
+                f32x4 f[2];
+                rt.frags(sX, c, lane, n16, g, f[0], f[1]);
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&sGB[n16][16 * j + 4 * g]);
-                const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&sGB[16 + n16][16 * j + 4 * g]);
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int j = 2 * c + jj;
+                    const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&X[n16][16 * j + 4 * g]);
+                    const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&X[16 + n16][16 * j + 4 * g]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    EngF32::mma(ak[0], b0[e], x[j][e]);
-                    EngF32::mma(ak[1], b1[e], x[j][e]);
+                    for (int e = 0; e < 4; ++e) {
+                        EngF32::mma(a[0], b0[e], f[jj][e]);
+                        EngF32::mma(a[1], b1[e], f[jj][e]);
+                    }
                 }
             }
+        };
+        {
+            RowTile<DP> rg, rv;
+            rg.load(P.gO, P.rG, P.zH, z, t0, P.T, P.D, vec_d, lane);
+            rv.load(P.V, P.rV, P.zH, z, t0, P.T, P.D, vec_d, lane);
+            contract(rg, sE, aq);
+            contract(rv, sGB, ak);
         }
         if (ok) {
             float *q = P.gpQ + row * P.S, *k = P.gpK + row * P.S;
@@ -471,12 +511,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             bucket_row(pv, P.pK + row * P.S, ok, P.S, g);
             bucket_contract<DP, LDV>(av, sGBv, pv, P.S, n16, g);
         }
-        if (ok) {
-            float *gv = P.gV + nc_off(P.rGV, P.zH, z, t);
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-                put4(gv, 16 * j + 4 * g, P.D, vec_d, av[j]);
-        }
+        store_rows<DP>(sX, av, P.gV, P.rGV, P.zH, z, t0, P.T, P.D, vec_d, lane, n16, g);
     }
 }
 
