@@ -638,10 +638,16 @@ struct ShmLayout {
         PU = njt == 1 ? 24 : 40;  // odd multiple of 8, >= 16 njt
     }
     // floats: planes^T [16 njt][PT], per-wave u [SHM_W][16][PU]; backward also planes [DX16][PD] and
-    // per-wave gproj [SHM_W][16][PD]
-    __host__ __device__ int floats(bool bwd) const
+    // per-wave gproj [SHM_W][16][PD]; then, for the 128 and 256 classes (whose x and dx rows move
+    // through it), per-wave row staging [SHM_W][16][SHS_LD] at stage_off
+    static constexpr int SHS_LD = 32 + 4;
+    __host__ __device__ int stage_off(bool bwd) const
     {
         return 16 * njt * PT + SHM_W * 16 * PU + (bwd ? DX16 * PD + SHM_W * 16 * PD : 0);
+    }
+    __host__ __device__ int floats(bool bwd) const
+    {
+        return stage_off(bwd) + (DX16 >= 128 ? SHM_W * 16 * SHS_LD : 0);
     }
 };
 
@@ -675,50 +681,99 @@ RACE_DEV void shm_load_planes(float *sPlT, float *sPl, const float *planes, cons
     }
 }
 
-// u = tanh(x . planes) / scale of this wave's 16 tokens into its sU rows [16][PU]. x rows are
-// read from a clamped row and clamped columns (always inside the tensor), and elements past D or of
-// tokens past the tile (ok false) are selected to zero: no branch per 16-wide chunk
+// u = tanh(x . planes) / scale of this wave's 16 tokens t0 .. t0 + 15 (those < tok1) into its sU
+// rows [16][PU]. x moves in row-contiguous runs: lane l loads row it * 8 + l / 8 (it = 0, 1) at
+// columns 32 c + 4 (l % 8) of each 32-column chunk c (8 rows x 4 elements per lane and row), the
+// chunk passes through the wave's staging rows sX [16][SHS_LD] (pitch 4 x odd words), and lane
+// (n, g) reads back columns 16 j + 4 g .. + 3 of row n, the K index of k-steps (j, e) of
+//   u^T[j][t] = sum_d planes^T[j][d] x[t][d]   (M = plane, N = token, K = d)
 template <class TX, int NJT, int DP>
-RACE_DEV void shm_project(float *sU, const float *sPlT, const SoftHashParams &P, const ShmLayout &Y, const TX *xrow,
-                          bool ok, bool vec, int n16, int g)
+RACE_DEV void shm_project(float *sU, float *sX, const float *sPlT, const SoftHashParams &P, const ShmLayout &Y,
+                          const TX *x, int t0, int tok1, bool vec, int lane, int n16, int g)
 {
-    constexpr int NJ = DP / 16;
-    f32x4 xv[NJ];
-    if (vec) {
-        typedef TX tx4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-        for (int jj = 0; jj < NJ; ++jj) {
-            const int d = 16 * jj + 4 * g;
-            const tx4 w = *reinterpret_cast<const tx4 *>(xrow + min(d, P.D - 4));
-            const bool in = ok && d < P.D;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                xv[jj][e] = in ? (float)w[e] : 0.0f;
-        }
-    } else {
-#pragma unroll
-        for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int d = 16 * jj + 4 * g + e;
-                const float v = (float)xrow[min(d, P.D - 1)];
-                xv[jj][e] = ok && d < P.D ? v : 0.0f;
-            }
-    }
+    constexpr int NJ = DP / 16, LD = ShmLayout::SHS_LD;
     f32x4 acc[NJT];
 #pragma unroll
     for (int jt = 0; jt < NJT; ++jt)
         acc[jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (DP < 128) {
+        // 64-column rows: lane (n, g) loads its own row's columns 16 j + 4 g .. + 3 straight into the
+        // fragments (clamped addresses, masked lanes selected to zero; measured faster than staging)
+        const int t = min(t0 + n16, tok1 - 1);
+        const bool ok = t0 + n16 < tok1;
+        const TX *xrow = x + (int64_t)t * P.x.st;
+        f32x4 xv[NJ];
+        if (vec) {
+            typedef TX tx4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int jj = 0; jj < NJ; ++jj) {
+            for (int j = 0; j < NJ; ++j) {
+                const int d = 16 * j + 4 * g;
+                const tx4 w = *reinterpret_cast<const tx4 *>(xrow + min(d, P.D - 4));
 #pragma unroll
-        for (int jt = 0; jt < NJT; ++jt) {
-            const f32x4 pt = *reinterpret_cast<const f32x4 *>(sPlT + (16 * jt + n16) * Y.PT + 16 * jj + 4 * g);
+                for (int e = 0; e < 4; ++e)
+                    xv[j][e] = ok && d < P.D ? (float)w[e] : 0.0f;
+            }
+        } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                EngF32::mma(acc[jt], pt[e], xv[jj][e]);
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int d = 16 * j + 4 * g + e;
+                    const float v = (float)xrow[min(d, P.D - 1)];
+                    xv[j][e] = ok && d < P.D ? v : 0.0f;
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int jt = 0; jt < NJT; ++jt) {
+                const f32x4 pt = *reinterpret_cast<const f32x4 *>(sPlT + (16 * jt + n16) * Y.PT + 16 * j + 4 * g);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    EngF32::mma(acc[jt], pt[e], xv[j][e]);
+            }
+    } else {
+        f32x4 xr[DP / 32][2];
+#pragma unroll
+        for (int c = 0; c < DP / 32; ++c)
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+                const int r = it * 8 + lane / 8, col = 32 * c + 4 * (lane % 8);
+                f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (t0 + r < tok1 && col < P.D) {
+                    const TX *p = x + (int64_t)(t0 + r) * P.x.st + col;
+                    if (vec) {
+                        typedef TX tx4 __attribute__((ext_vector_type(4)));
+                        const tx4 w = *reinterpret_cast<const tx4 *>(p);
+                        v = f32x4{(float)w[0], (float)w[1], (float)w[2], (float)w[3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            v[e] = col + e < P.D ? (float)p[e] : 0.0f;
+                    }
+                }
+                xr[c][it] = v;
+            }
+#pragma unroll
+        for (int c = 0; c < DP / 32; ++c) {
+#pragma unroll
+            for (int it = 0; it < 2; ++it)
+                *reinterpret_cast<f32x4 *>(sX + (it * 8 + lane / 8) * LD + 4 * (lane % 8)) = xr[c][it];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const f32x4 xv = *reinterpret_cast<const f32x4 *>(sX + n16 * LD + 16 * jj + 4 * g);
+                const int j = 2 * c + jj;
+#pragma unroll
+                for (int jt = 0; jt < NJT; ++jt) {
+                    const f32x4 pt = *reinterpret_cast<const f32x4 *>(sPlT + (16 * jt + n16) * Y.PT + 16 * j + 4 * g);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        EngF32::mma(acc[jt], pt[e], xv[e]);
+                }
+            }
         }
     }
+    static_assert(NJ == 2 * (DP / 32), "32-column chunks of two 16-wide k runs");
     // accumulator rows: planes 16 jt + 4 g + e of token n16
 #pragma unroll
     for (int jt = 0; jt < NJT; ++jt) {
@@ -738,6 +793,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_fwd_mfma(SoftHashPar
     float *sPlT = sm;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n16 = lane & 15, g = lane >> 4;
     float *sU = sPlT + 16 * NJT * Y.PT + w * 16 * Y.PU;
+    float *sX = sm + Y.stage_off(false) + w * 16 * ShmLayout::SHS_LD;
     const int bh = blockIdx.y, m = blockIdx.z;
     const int b = bh / P.H, h = bh % P.H;
     constexpr int R = 1 << KB;
@@ -751,8 +807,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_fwd_mfma(SoftHashPar
     const int span = P.tpw * SHM_W * 16;
     const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
     for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
-        const int t = t0 + n16;
-        shm_project<TX, NJT, DP>(sU, sPlT, P, Y, x + (int64_t)min(t, tok1 - 1) * P.x.st, t < tok1, vec_x, n16, g);
+        shm_project<TX, NJT, DP>(sU, sX, sPlT, P, Y, x, t0, tok1, vec_x, lane, n16, g);
         const int nv = min(16, tok1 - t0);
         if constexpr (KB >= 2) {
             if (vec_out) {
@@ -803,6 +858,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n16 = lane & 15, g = lane >> 4;
     float *sU = sPl + Y.DX16 * Y.PD + w * 16 * Y.PU;
     float *sGP = sPl + Y.DX16 * Y.PD + SHM_W * 16 * Y.PU + w * 16 * Y.PD;
+    float *sX = sm + Y.stage_off(true) + w * 16 * ShmLayout::SHS_LD;
     const int bh = blockIdx.y;
     const int b = bh / P.H, h = bh % P.H;
     constexpr int R = 1 << KB;
@@ -822,8 +878,7 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
     const int span = P.tpw * SHM_W * 16;
     const int tok0 = blockIdx.x * span, tok1 = min(P.T, tok0 + span);
     for (int t0 = tok0 + 16 * w; t0 < tok1; t0 += 16 * SHM_W) {
-        const int t = t0 + n16;
-        shm_project<TX, NJT, DP>(sU, sPlT, P, Y, x + (int64_t)min(t, tok1 - 1) * P.x.st, t < tok1, vec_x, n16, g);
+        shm_project<TX, NJT, DP>(sU, sX, sPlT, P, Y, x, t0, tok1, vec_x, lane, n16, g);
         // (token, table) items: gu_k = d loss / d u_k, gproj = gu * (1 - tanh^2) / scale
         for (int i = lane; i < 16 * P.L; i += 64) {
             const int r = i / P.L, l = i - r * P.L;
@@ -882,24 +937,59 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
             }
         }
         // dx^T tiles of 16 d: A = planes rows d (4-byte reads, pitch 4 x odd), B = gproj of token n16;
-        // k-steps over the planes (L*K <= 16 NJT, rounded to 4)
+        // k-steps over the planes (L*K <= 16 NJT, rounded to 4). Two tiles (32 columns) at a time pass
+        // through the staging rows and leave as row-contiguous runs (8 rows per store instruction)
         const int nks = (P.LK + 3) / 4;
-        TX *o = dx + (int64_t)t * P.dx.st;
+        constexpr int LD = ShmLayout::SHS_LD;
+        if constexpr (DP < 128) {
+            // 64-column rows: each lane stores its own row's four columns per tile (measured faster)
+            const int t = t0 + n16;
+            TX *o = dx + (int64_t)t * P.dx.st;
 #pragma unroll
-        for (int jj = 0; jj < DP / 16; ++jj) {
-            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-            for (int kk = 0; kk < nks; ++kk)
-                EngF32::mma(acc, sPl[(16 * jj + n16) * Y.PD + 4 * kk + g], sGP[n16 * Y.PD + 4 * kk + g]);
-            const int d = 16 * jj + 4 * g;
-            if (t < tok1 && d < P.D) {
-                if (vec_dx) {
-                    typedef TX tx4 __attribute__((ext_vector_type(4)));
-                    *reinterpret_cast<tx4 *>(o + d) = tx4{(TX)acc[0], (TX)acc[1], (TX)acc[2], (TX)acc[3]};
-                } else {
+            for (int j = 0; j < DP / 16; ++j) {
+                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int kk = 0; kk < nks; ++kk)
+                    EngF32::mma(acc, sPl[(16 * j + n16) * Y.PD + 4 * kk + g], sGP[n16 * Y.PD + 4 * kk + g]);
+                const int d = 16 * j + 4 * g;
+                if (t < tok1 && d < P.D) {
+                    if (vec_dx) {
+                        typedef TX tx4 __attribute__((ext_vector_type(4)));
+                        *reinterpret_cast<tx4 *>(o + d) = tx4{(TX)acc[0], (TX)acc[1], (TX)acc[2], (TX)acc[3]};
+                    } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (d + e < P.D)
-                            o[d + e] = (TX)acc[e];
+                        for (int e = 0; e < 4; ++e)
+                            if (d + e < P.D)
+                                o[d + e] = (TX)acc[e];
+                    }
+                }
+            }
+            continue;
+        }
+#pragma unroll
+        for (int c = 0; c < DP / 32; ++c) {
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int j = 2 * c + jj;
+                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int kk = 0; kk < nks; ++kk)
+                    EngF32::mma(acc, sPl[(16 * j + n16) * Y.PD + 4 * kk + g], sGP[n16 * Y.PD + 4 * kk + g]);
+                *reinterpret_cast<f32x4 *>(sX + n16 * LD + 16 * jj + 4 * g) = acc;
+            }
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+                const int r = it * 8 + lane / 8, cl = 4 * (lane % 8), d = 32 * c + cl;
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(sX + r * LD + cl);
+                if (t0 + r < tok1 && d < P.D) {
+                    TX *o = dx + (int64_t)(t0 + r) * P.dx.st + d;
+                    if (vec_dx) {
+                        typedef TX tx4 __attribute__((ext_vector_type(4)));
+                        *reinterpret_cast<tx4 *>(o) = tx4{(TX)v[0], (TX)v[1], (TX)v[2], (TX)v[3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (d + e < P.D)
+                                o[e] = (TX)v[e];
+                    }
                 }
             }
         }
