@@ -272,6 +272,51 @@ __device__ __forceinline__ void bucket_contract(f32x4 (&acc)[DP / 16], const flo
     }
 }
 
+// A wave's 16-token tile of [T][S] probabilities (S <= 32, S % 4 == 0): rows t0 .. t0 + 15 of one
+// stream are one contiguous block of 16 S floats, moved as 16-byte runs by consecutive lanes (two
+// instructions) instead of 16 rows x 16 bytes per instruction; staged into per-wave LDS rows [16][ld]
+// so that each lane reads its bucket_row from there. Floats past the valid rows read as zero.
+struct ProbTile {
+    f32x4 x[2];
+
+    __device__ void load(const float *blk, int nfl, int lane)
+    {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int o = 4 * lane + 256 * it;
+            x[it] = o < nfl ? *reinterpret_cast<const f32x4 *>(blk + o) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    __device__ void row(float (&pv)[8], float *sP, int ld, int S, int lane, int n16, int g) const
+    {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int o = 4 * lane + 256 * it;
+            if (o < 16 * S)
+                *reinterpret_cast<f32x4 *>(sP + (o / S) * ld + o % S) = x[it];
+        }
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            pv[kk] = 4 * kk + g < S ? sP[n16 * ld + 4 * kk + g] : 0.0f;
+    }
+};
+
+// the inverse for one [16][ld] tile of MFMA-layout runs a[j] (columns 16 j + 4 g .. + 3 of row n,
+// j < 2): staged, then stored as the contiguous block of the tile's nv rows of S floats
+__device__ __forceinline__ void store_prob_tile(float *blk, const f32x4 (&a)[2], float *sP, int ld, int S, int nv,
+                                                int lane, int n16, int g)
+{
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        *reinterpret_cast<f32x4 *>(sP + n16 * ld + 16 * j + 4 * g) = a[j];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int o = 4 * lane + 256 * it;
+        if (o < nv * S)
+            *reinterpret_cast<f32x4 *>(blk + o) = *reinterpret_cast<const f32x4 *>(sP + (o / S) * ld + o % S);
+    }
+}
+
 // Readout on the matrix cores for S <= 32: out^T = E^T pQ^T per 16-token tile (M = d, N = token,
 // K = bucket), E resident in LDS at a pitch of 16 x odd words; a lane's accumulator holds four
 // consecutive d of its token's output row, stored as one 16-byte run.
@@ -295,32 +340,43 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
         __syncthreads();
     }
     const bool vec_d = P.vec;
+    // pQ tiles as contiguous blocks (S % 4 == 0, 16-byte aligned), else each lane's row directly
+    const bool blk_p = (P.S & 3) == 0 && (reinterpret_cast<uintptr_t>(P.pQ) & 15) == 0;
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
-    // this step's pQ row waits in registers, loaded one step ahead
+    const float *pQz = P.pQ + (int64_t)z * P.T * P.S;
+    // this step's pQ waits in registers, loaded one step ahead
+    ProbTile pt;
     float pv[8];
     {
-        const int t = blockIdx.x * P.tpw * NCM_TT + w * 16 + n16;
-        bucket_row(pv, P.pQ + ((int64_t)z * P.T + t) * P.S, t < P.T, P.S, g);
+        const int t0 = blockIdx.x * P.tpw * NCM_TT + w * 16, t = t0 + n16;
+        if (blk_p)
+            pt.load(pQz + (int64_t)t0 * P.S, max(0, min(16, P.T - t0)) * P.S, lane);
+        else
+            bucket_row(pv, pQz + (int64_t)t * P.S, t < P.T, P.S, g);
     }
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
         const int t0 = st * NCM_TT + w * 16;
         if (t0 >= P.T)
             break;  // (uniform within the wave; no barrier inside the loop)
-        const int t = t0 + n16;
-        const bool ok = t < P.T;
         f32x4 acc[DP / 16];
 #pragma unroll
         for (int j = 0; j < DP / 16; ++j)
             acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int tn0 = t0 + NCM_TT;  // the next step's tile (loaded only inside the range)
+        const bool nxt = st + 1 < st1 && tn0 < P.T;
         float pn[8];
-        {
-            const int tn = t + NCM_TT;  // the next step's token (loaded only inside the range)
-            bucket_row(pn, P.pQ + ((int64_t)z * P.T + tn) * P.S, st + 1 < st1 && tn < P.T, P.S, g);
+        if (blk_p) {
+            pt.row(pv, &sO[w][0][0], LDO, P.S, lane, n16, g);
+            pt.load(pQz + (int64_t)tn0 * P.S, nxt ? min(16, P.T - tn0) * P.S : 0, lane);
+        } else {
+            bucket_row(pn, pQz + (int64_t)(tn0 + n16) * P.S, nxt && tn0 + n16 < P.T, P.S, g);
         }
         bucket_contract<DP, LDV>(acc, sEv, pv, P.S, n16, g);
+        if (!blk_p) {
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            pv[kk] = pn[kk];
+            for (int kk = 0; kk < 8; ++kk)
+                pv[kk] = pn[kk];
+        }
         // through this wave's LDS rows, 64 columns at a time, so that each store instruction writes
         // whole 256-byte runs of HW / 4 lanes per token row (in order within the wave: no barrier)
         constexpr int LPR = HW / 4, RPI = 64 / LPR;  // lanes per row, rows per instruction
@@ -452,6 +508,9 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             ga[j][e] = sGA[16 * j + 4 * g + e];
     constexpr int NJ = DP / 16;  // 16-wide d runs: k-steps 4 NJ over d, output tiles NJ over d
     const bool vec_d = P.vec, vec_s = (P.S & 3) == 0;
+    // probability tiles as contiguous blocks (S % 4 == 0, every pointer 16-byte aligned)
+    const bool blk_p = vec_s && ((reinterpret_cast<uintptr_t>(P.pK) | reinterpret_cast<uintptr_t>(P.gpQ) |
+                                  reinterpret_cast<uintptr_t>(P.gpK)) & 15) == 0;
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
         const int t0 = st * NCM_TT + w * 16;
@@ -489,16 +548,23 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             contract(rg, sE, aq);
             contract(rv, sGB, ak);
         }
-        if (ok) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ak[j][e] += ga[j][e];
+        if (blk_p) {
+            // contiguous blocks of the tile's rows (S % 4 == 0, 16-byte aligned) through sX
+            const int64_t b0 = ((int64_t)z * P.T + t0) * P.S;
+            const int nv = min(16, P.T - t0);
+            store_prob_tile(P.gpQ + b0, aq, &sX[0][0], NCS_LD, P.S, nv, lane, n16, g);
+            store_prob_tile(P.gpK + b0, ak, &sX[0][0], NCS_LD, P.S, nv, lane, n16, g);
+        } else if (ok) {
             float *q = P.gpQ + row * P.S, *k = P.gpK + row * P.S;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                f32x4 kk = ak[j];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    kk[e] += ga[j][e];
                 put4(q, 16 * j + 4 * g, P.S, vec_s, aq[j]);
-                put4(k, 16 * j + 4 * g, P.S, vec_s, kk);
+                put4(k, 16 * j + 4 * g, P.S, vec_s, ak[j]);
             }
         }
         // ---- gv^T[d][t] = sum_s gB[s][d] pK[t][s]  (k-step kk: bucket 4 kk + g)
@@ -508,7 +574,13 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             av[j] = f32x4{0.f, 0.f, 0.f, 0.f};
         {
             float pv[8];
-            bucket_row(pv, P.pK + row * P.S, ok, P.S, g);
+            if (blk_p) {
+                ProbTile pt;
+                pt.load(P.pK + ((int64_t)z * P.T + t0) * P.S, min(16, P.T - t0) * P.S, lane);
+                pt.row(pv, &sX[0][0], NCS_LD, P.S, lane, n16, g);
+            } else {
+                bucket_row(pv, P.pK + row * P.S, ok, P.S, g);
+            }
             bucket_contract<DP, LDV>(av, sGBv, pv, P.S, n16, g);
         }
         store_rows<DP>(sX, av, P.gV, P.rGV, P.zH, z, t0, P.T, P.D, vec_d, lane, n16, g);
