@@ -1108,7 +1108,7 @@ hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream
     SoftHashParams args = P;
     args.tpw = softhash_tiles_per_wg(P.T, P.B, P.H, mf);
     void *argv[] = {&args};
-    return hipLaunchKernel(fn, grid, dim3(256), argv, smem, s);
+    return hipLaunchKernel(fn, grid, dim3(mf ? SHM_W * 64 : 256), argv, smem, s);
 }
 
 hipError_t softhash_prepare(int D, int LK)
