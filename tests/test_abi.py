@@ -196,3 +196,22 @@ def test_qkv_bwd_static_refuses_oversize_on_the_host():
     for shape in ((1, 4, 4, 1 << 20, 64, 8, 4), (8, 32, 8, 8192, 64, 8, 4)):
         s2 = _lib.QKVShape(*shape, 8.0, 1e-6, 0)
         assert 0 < lib.race_qkv_scratch_bytes(s2, 1) <= lib.race_static_scratch_bytes()
+
+
+def test_nc_view_layouts_need_no_copy():
+    """BatchedACE's [M,B,T,H,d] values reach race_nc_*_view as [M*B, H, T, d] views of the same
+    storage (no permute copy); where the strides allow no such view (an expanded ensemble axis) the
+    helper says so and the caller copies."""
+    import torch
+    from race_attention_amd.noncausal import _bhtd
+    x = torch.randn(2, 3, 5, 4, 8)
+    v = _bhtd(x)
+    assert v.shape == (6, 4, 5, 8) and v.data_ptr() == x.data_ptr() and v.stride(3) == 1
+    assert torch.equal(v, x.permute(0, 1, 3, 2, 4).reshape(6, 4, 5, 8))
+    # the [B,H,T,D] wrapper's M = 1 pack (race_attention): a view of the caller's tensor
+    q = torch.randn(3, 4, 5, 8)
+    p1 = q.permute(0, 2, 1, 3).unsqueeze(0).expand(1, -1, -1, -1, -1)
+    assert _bhtd(p1).data_ptr() == q.data_ptr()
+    # M = 2 copies of one tensor (stride 0 on M): no view
+    p2 = q.permute(0, 2, 1, 3).unsqueeze(0).expand(2, -1, -1, -1, -1)
+    assert _bhtd(p2) is None
