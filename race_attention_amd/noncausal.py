@@ -151,7 +151,7 @@ class SoftHashTempFn(Function):
     def forward(ctx, X, planes_T, L, Kbits, M, unshared, scale, scale_value=None):
         _lib.require_device(X, planes_T)
         B, H, T, D = X.shape
-        s = float(scale) if scale_value is None else float(scale_value)
+        s = float(scale.detach() if torch.is_tensor(scale) else scale) if scale_value is None else float(scale_value)
         planes = planes_T.detach().float().contiguous()
         xv, Xc = _lib.view4(X)
         Mp = M if unshared else 1
@@ -209,7 +209,7 @@ class BatchedACE(nn.Module):
         if M != self.M or dk != self.d_k:
             raise ValueError(f"expected [M={self.M},B,T,H,{self.d_k}] inputs, got {tuple(Khf.shape)}")
         scale = self.logit_temp.exp().clamp(1e-2, 10.0)
-        sv = float(scale)  # one host read of the temperature per call
+        sv = float(scale.detach())  # one host read of the temperature per call
         # streams ordered (M, B, H) as benchmark_time.py:121-131; one row of planes per m
         def bhtd(X):  # [M,B,T,H,dk] -> [M*B, H, T, dk] view
             return X.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, dk)

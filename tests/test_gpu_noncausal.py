@@ -82,6 +82,34 @@ def test_noncausal_view_layouts(dev, S, D, pad):
     check("gV", flat(vx.grad), vr.grad, TOL)
 
 
+def test_noncausal_unaligned_buffers(dev):
+    """Contiguous probabilities, values and upstream gradient that start 4 bytes past a 16-byte
+    boundary: the matrix-core kernels take their element-wise paths (no 16-byte runs) and agree with
+    the fp64 oracle as the aligned case does."""
+    from race_attention_amd.noncausal import RaceNonCausalFn
+    N, T, S, D = 2, 1000, 24, 128
+    pk, pq, v, go = _probs(N, T, S, D, seed=5)
+
+    def odd(x):  # same values, data pointer 4 bytes past 16-byte alignment
+        buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=dev)
+        y = buf[1:].view(x.shape)
+        y.copy_(x.to(dev))
+        assert y.is_contiguous() and y.data_ptr() % 16 == 4
+        return y
+
+    eps = 1e-6
+    pkr, pqr, vr = (x.double().requires_grad_(True) for x in (pk, pq, v))
+    ref = orc.race_noncausal_ref(pkr, pqr, vr, eps)
+    ref.backward(go.double())
+    pkx, pqx, vx = (odd(x).requires_grad_(True) for x in (pk, pq, v))
+    out = RaceNonCausalFn.apply(pkx, pqx, vx, eps)
+    out.backward(odd(go))
+    check("out", out, ref, TOL)
+    check("gpK", pkx.grad, pkr.grad, TOL)
+    check("gpQ", pqx.grad, pqr.grad, TOL)
+    check("gV", vx.grad, vr.grad, TOL)
+
+
 @pytest.mark.parametrize("S", [64, 24])
 def test_noncausal_block_invariance(dev, S):
     """The totals over any block split agree to fp32 rounding (S = 24: one bucket tile, with the
