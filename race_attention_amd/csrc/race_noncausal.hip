@@ -248,22 +248,23 @@ __device__ __forceinline__ void put4(float *row, int c, int ncol, bool vec, cons
 
 // The lane's bucket probabilities p[4 kk + g] (k-step kk) of one token row, zero for buckets >= S
 // and when the token is outside the sequence (ok false)
-__device__ __forceinline__ void bucket_row(float (&pv)[8], const float *p, bool ok, int S, int g)
+template <int NK>
+__device__ __forceinline__ void bucket_row(float (&pv)[NK], const float *p, bool ok, int S, int g)
 {
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
+    for (int kk = 0; kk < NK; ++kk)
         pv[kk] = (ok && 4 * kk + g < S) ? p[4 * kk + g] : 0.0f;
 }
 
-// acc[j] (j < DP / 16) += X^T p^T for one 16-token tile: X is a [32][LD] bucket-by-d table in LDS
+// acc[j] (j < DP / 16) += X^T p^T for one 16-token tile: X is a [4 NK][LD] bucket-by-d table in LDS
 // (rows >= S zero), pv the lane's bucket_row; lane (n, g) reads X[4 kk + g][16 j + n] (banks
 // 16 g + n for LD = 16 x odd)
-template <int DP, int LD>
-__device__ __forceinline__ void bucket_contract(f32x4 (&acc)[DP / 16], const float (*X)[LD], const float (&pv)[8],
+template <int DP, int LD, int NK>
+__device__ __forceinline__ void bucket_contract(f32x4 (&acc)[DP / 16], const float (*X)[LD], const float (&pv)[NK],
                                                 int S, int n16, int g)
 {
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int kk = 0; kk < NK; ++kk) {
         if (4 * kk < S) {
 #pragma unroll
             for (int j = 0; j < DP / 16; ++j)
@@ -272,31 +273,33 @@ __device__ __forceinline__ void bucket_contract(f32x4 (&acc)[DP / 16], const flo
     }
 }
 
-// A wave's 16-token tile of [T][S] probabilities (S <= 32, S % 4 == 0): rows t0 .. t0 + 15 of one
-// stream are one contiguous block of 16 S floats, moved as 16-byte runs by consecutive lanes (two
+// A wave's 16-token tile of [T][S] probabilities (S <= 4 NK, S % 4 == 0): rows t0 .. t0 + 15 of one
+// stream are one contiguous block of 16 S floats, moved as 16-byte runs by consecutive lanes (NK / 4
 // instructions) instead of 16 rows x 16 bytes per instruction; staged into per-wave LDS rows [16][ld]
-// so that each lane reads its bucket_row from there. Floats past the valid rows read as zero.
+// (ld >= S) so that each lane reads its bucket_row from there. Floats past the valid rows read as zero.
+template <int NK>
 struct ProbTile {
-    f32x4 x[2];
+    static constexpr int NI = NK / 4;
+    f32x4 x[NI];
 
     __device__ void load(const float *blk, int nfl, int lane)
     {
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
+        for (int it = 0; it < NI; ++it) {
             const int o = 4 * lane + 256 * it;
             x[it] = o < nfl ? *reinterpret_cast<const f32x4 *>(blk + o) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
-    __device__ void row(float (&pv)[8], float *sP, int ld, int S, int lane, int n16, int g) const
+    __device__ void row(float (&pv)[NK], float *sP, int ld, int S, int lane, int n16, int g) const
     {
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
+        for (int it = 0; it < NI; ++it) {
             const int o = 4 * lane + 256 * it;
             if (o < 16 * S)
                 *reinterpret_cast<f32x4 *>(sP + (o / S) * ld + o % S) = x[it];
         }
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
+        for (int kk = 0; kk < NK; ++kk)
             pv[kk] = 4 * kk + g < S ? sP[n16 * ld + 4 * kk + g] : 0.0f;
     }
 };
@@ -317,15 +320,15 @@ __device__ __forceinline__ void store_prob_tile(float *blk, const f32x4 (&a)[2],
     }
 }
 
-// Readout on the matrix cores for S <= 32: out^T = E^T pQ^T per 16-token tile (M = d, N = token,
-// K = bucket), E resident in LDS at a pitch of 16 x odd words; a lane's accumulator holds four
-// consecutive d of its token's output row, stored as one 16-byte run.
-template <int DP>
+// Readout on the matrix cores for S <= SP (32 or 64): out^T = E^T pQ^T per 16-token tile (M = d,
+// N = token, K = bucket), E resident in LDS at a pitch of 16 x odd words; a lane's accumulator holds
+// four consecutive d of its token's output row.
+template <int DP, int SP>
 __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P)
 {
-    constexpr int LDV = DP + 16;
+    constexpr int LDV = DP + 16, NK = SP / 4;
     constexpr int HW = DP < 64 ? DP : 64, LDO = HW + 4;  // output staging: 64-column halves
-    __shared__ __align__(16) float sEv[32][LDV];
+    __shared__ __align__(16) float sEv[SP][LDV];
     __shared__ __align__(16) float sO[NCM_W][16][LDO];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, z = blockIdx.y;
     const int n16 = lane & 15, g = lane >> 4;
@@ -333,7 +336,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
         const int64_t slot = (int64_t)z * (P.NB + 1) + P.NB;
         const float *B = P.totB + slot * P.S_pad * P.DPw;
         const float *A = P.totA + slot * P.S_pad;
-        for (int i = tid; i < 32 * DP; i += NCM_NTH) {
+        for (int i = tid; i < SP * DP; i += NCM_NTH) {
             const int c = i / DP, d = i % DP;
             sEv[c][d] = (c < P.S && d < P.D) ? B[(int64_t)c * P.DPw + d] / (A[c] + P.eps) : 0.0f;
         }
@@ -341,12 +344,12 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
     }
     const bool vec_d = P.vec;
     // pQ tiles as contiguous blocks (S % 4 == 0, 16-byte aligned), else each lane's row directly
-    const bool blk_p = (P.S & 3) == 0 && (reinterpret_cast<uintptr_t>(P.pQ) & 15) == 0;
+    const bool blk_p = (P.S & 3) == 0 && P.S <= HW && (reinterpret_cast<uintptr_t>(P.pQ) & 15) == 0;
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
     const float *pQz = P.pQ + (int64_t)z * P.T * P.S;
     // this step's pQ waits in registers, loaded one step ahead
-    ProbTile pt;
-    float pv[8];
+    ProbTile<NK> pt;
+    float pv[NK];
     {
         const int t0 = blockIdx.x * P.tpw * NCM_TT + w * 16, t = t0 + n16;
         if (blk_p)
@@ -364,17 +367,17 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_readout_mfma(const NcParams P
             acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
         const int tn0 = t0 + NCM_TT;  // the next step's tile (loaded only inside the range)
         const bool nxt = st + 1 < st1 && tn0 < P.T;
-        float pn[8];
+        float pn[NK];
         if (blk_p) {
             pt.row(pv, &sO[w][0][0], LDO, P.S, lane, n16, g);
             pt.load(pQz + (int64_t)tn0 * P.S, nxt ? min(16, P.T - tn0) * P.S : 0, lane);
         } else {
             bucket_row(pn, pQz + (int64_t)(tn0 + n16) * P.S, nxt && tn0 + n16 < P.T, P.S, g);
         }
-        bucket_contract<DP, LDV>(acc, sEv, pv, P.S, n16, g);
+        bucket_contract<DP, LDV, NK>(acc, sEv, pv, P.S, n16, g);
         if (!blk_p) {
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
+            for (int kk = 0; kk < NK; ++kk)
                 pv[kk] = pn[kk];
         }
         // through this wave's LDS rows, 64 columns at a time, so that each store instruction writes
@@ -457,14 +460,14 @@ __device__ void store_rows(float (*sX)[NCS_LD], const f32x4 (&acc)[DP / 16], flo
     }
 }
 
-template <int DP>
+template <int DP, int SP>
 __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams P)
 {
-    constexpr int LDD = DP + 8, LDV = DP + 16;
-    __shared__ __align__(16) float sE[32][LDD];
-    __shared__ __align__(16) float sGB[32][LDD];
-    __shared__ __align__(16) float sGBv[32][LDV];
-    __shared__ float sGA[32];
+    constexpr int LDD = DP + 8, LDV = DP + 16, NK = SP / 4, NT = SP / 16;  // bucket k-steps and tiles
+    __shared__ __align__(16) float sE[SP][LDD];
+    __shared__ __align__(16) float sGB[SP][LDD];
+    __shared__ __align__(16) float sGBv[SP][LDV];
+    __shared__ float sGA[SP];
     __shared__ __align__(16) float sXs[NCM_W][16][NCS_LD];  // per-wave row staging
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, z = blockIdx.y;
     const int n16 = lane & 15, g = lane >> 4;
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         const float *B = P.totB + slot * P.S_pad * P.DPw;
         const float *A = P.totA + slot * P.S_pad;
         const float *GE = P.totGE + slot * P.S_pad * P.DPw;
-        for (int i = tid; i < 32 * DP; i += NCM_NTH) {
+        for (int i = tid; i < SP * DP; i += NCM_NTH) {
             const int c = i / DP, d = i % DP;
             float e = 0.0f, gb = 0.0f;
             if (c < P.S && d < P.D) {
@@ -488,7 +491,7 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         }
         __syncthreads();
         // gA[s] = -(gE . E) / (A + eps) = -(gB . E): one wave per bucket row, lanes over d
-        for (int c = w; c < 32; c += NCM_W) {
+        for (int c = w; c < SP; c += NCM_W) {
             float acc = 0.0f;
             for (int d = lane; d < DP; d += 64)
                 acc += sGB[c][d] * sE[c][d];
@@ -500,16 +503,16 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         __syncthreads();
     }
     // gA of the lane's gpK columns 16 j + 4 g + e
-    float ga[2][4];
+    float ga[NT][4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             ga[j][e] = sGA[16 * j + 4 * g + e];
     constexpr int NJ = DP / 16;  // 16-wide d runs: k-steps 4 NJ over d, output tiles NJ over d
     const bool vec_d = P.vec, vec_s = (P.S & 3) == 0;
     // probability tiles as contiguous blocks (S % 4 == 0, every pointer 16-byte aligned)
-    const bool blk_p = vec_s && ((reinterpret_cast<uintptr_t>(P.pK) | reinterpret_cast<uintptr_t>(P.gpQ) |
+    const bool blk_p = SP == 32 && vec_s && ((reinterpret_cast<uintptr_t>(P.pK) | reinterpret_cast<uintptr_t>(P.gpQ) |
                                   reinterpret_cast<uintptr_t>(P.gpK)) & 15) == 0;
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
@@ -521,9 +524,11 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         const int64_t row = (int64_t)z * P.T + t;  // of the [N][T][S] probabilities
         float (*sX)[NCS_LD] = sXs[w];
         // ---- gpQ^T[s][t] = E[s] . go_t ; gpK^T[s][t] = gA[s] + gB[s] . v_t
-        f32x4 aq[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        f32x4 ak[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        auto contract = [&](const RowTile<DP> &rt, const float (*X)[LDD], f32x4 (&a)[2]) {
+        f32x4 aq[NT], ak[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+            aq[j] = ak[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto contract = [&](const RowTile<DP> &rt, const float (*X)[LDD], f32x4 (&a)[NT]) {
 #pragma unroll
             for (int c = 0; c < DP / 32; ++c) {
                 f32x4 f[2];
@@ -531,12 +536,12 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj) {
                     const int j = 2 * c + jj;
-                    const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&X[n16][16 * j + 4 * g]);
-                    const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&X[16 + n16][16 * j + 4 * g]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        EngF32::mma(a[0], b0[e], f[jj][e]);
-                        EngF32::mma(a[1], b1[e], f[jj][e]);
+                    for (int st = 0; st < NT; ++st) {
+                        const f32x4 b = *reinterpret_cast<const f32x4 *>(&X[16 * st + n16][16 * j + 4 * g]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            EngF32::mma(a[st], b[e], f[jj][e]);
                     }
                 }
             }
@@ -549,20 +554,23 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
             contract(rv, sGB, ak);
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 ak[j][e] += ga[j][e];
-        if (blk_p) {
+        if constexpr (SP == 32) {
+          if (blk_p) {
             // contiguous blocks of the tile's rows (S % 4 == 0, 16-byte aligned) through sX
             const int64_t b0 = ((int64_t)z * P.T + t0) * P.S;
             const int nv = min(16, P.T - t0);
             store_prob_tile(P.gpQ + b0, aq, &sX[0][0], NCS_LD, P.S, nv, lane, n16, g);
             store_prob_tile(P.gpK + b0, ak, &sX[0][0], NCS_LD, P.S, nv, lane, n16, g);
-        } else if (ok) {
+          }
+        }
+        if (!blk_p && ok) {
             float *q = P.gpQ + row * P.S, *k = P.gpK + row * P.S;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < NT; ++j) {
                 put4(q, 16 * j + 4 * g, P.S, vec_s, aq[j]);
                 put4(k, 16 * j + 4 * g, P.S, vec_s, ak[j]);
             }
@@ -573,15 +581,15 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         for (int j = 0; j < NJ; ++j)
             av[j] = f32x4{0.f, 0.f, 0.f, 0.f};
         {
-            float pv[8];
+            float pv[NK];
             if (blk_p) {
-                ProbTile pt;
+                ProbTile<NK> pt;
                 pt.load(P.pK + ((int64_t)z * P.T + t0) * P.S, min(16, P.T - t0) * P.S, lane);
                 pt.row(pv, &sX[0][0], NCS_LD, P.S, lane, n16, g);
             } else {
                 bucket_row(pv, P.pK + row * P.S, ok, P.S, g);
             }
-            bucket_contract<DP, LDV>(av, sGBv, pv, P.S, n16, g);
+            bucket_contract<DP, LDV, NK>(av, sGBv, pv, P.S, n16, g);
         }
         store_rows<DP>(sX, av, P.gV, P.rGV, P.zH, z, t0, P.T, P.D, vec_d, lane, n16, g);
     }
@@ -594,16 +602,23 @@ hipError_t launch_nc_dp(int bwd, const NcParams &P, int N, hipStream_t s)
     // 2048 workgroups (8 per CU)
     const int ntt = (P.T + NC_TT - 1) / NC_TT;
     NcParams Q = P;
-    if (P.S <= 32) {
-        // matrix-core kernels: a workgroup walks up to 16 steps of 128 tokens, about 1024
-        // workgroups in the grid
+    if (P.S <= 32 || (P.S <= 64 && DP <= 128)) {
+        // matrix-core kernels (buckets padded to 32, or to 64 up to D = 128 for their LDS): a
+        // workgroup walks up to 16 steps of 128 tokens, about 1024 workgroups in the grid
         const int nstep = (P.T + NCM_TT - 1) / NCM_TT;
         Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)nstep * N / 1024));
         const dim3 grid((unsigned)((nstep + Q.tpw - 1) / Q.tpw), (unsigned)N);
-        if (bwd)
-            hipLaunchKernelGGL(race_nc_backward_mfma<DP>, grid, dim3(NCM_NTH), 0, s, Q);
-        else
-            hipLaunchKernelGGL(race_nc_readout_mfma<DP>, grid, dim3(NCM_NTH), 0, s, Q);
+        if (P.S <= 32) {
+            if (bwd)
+                hipLaunchKernelGGL((race_nc_backward_mfma<DP, 32>), grid, dim3(NCM_NTH), 0, s, Q);
+            else
+                hipLaunchKernelGGL((race_nc_readout_mfma<DP, 32>), grid, dim3(NCM_NTH), 0, s, Q);
+        } else if constexpr (DP <= 128) {
+            if (bwd)
+                hipLaunchKernelGGL((race_nc_backward_mfma<DP, 64>), grid, dim3(NCM_NTH), 0, s, Q);
+            else
+                hipLaunchKernelGGL((race_nc_readout_mfma<DP, 64>), grid, dim3(NCM_NTH), 0, s, Q);
+        }
         return hipGetLastError();
     }
     Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)ntt * N / 2048));
