@@ -8,7 +8,8 @@
 // The totals come from the causal machinery's per-block totals kernel and block scan
 // (slot NB of the scanned workspace holds the whole-sequence sum); the kernels here are
 // the per-token readout and backward: on fp32 MFMA with the bucket tables resident in LDS
-// for S <= 32, else fp32 FMA on LDS tiles of NC_TT tokens x NC_SC buckets.
+// for S <= 32 (and for S <= 64 up to D = 128), else fp32 FMA on LDS tiles of NC_TT tokens x NC_SC
+// buckets.
 #include <algorithm>
 
 #include "race_device.h"
