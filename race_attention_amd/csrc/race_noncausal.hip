@@ -8,8 +8,8 @@
 // The totals come from the causal machinery's per-block totals kernel and block scan
 // (slot NB of the scanned workspace holds the whole-sequence sum); the kernels here are
 // the per-token readout and backward: on fp32 MFMA with the bucket tables resident in LDS
-// for S <= 32 (and for S <= 64 up to D = 128), else fp32 FMA on LDS tiles of NC_TT tokens x NC_SC
-// buckets.
+// for S <= 32 (S <= 64 up to D = 128, S <= 128 up to D = 64), else fp32 FMA on LDS tiles of NC_TT
+// tokens x NC_SC buckets.
 #include <algorithm>
 
 #include "race_device.h"
@@ -603,9 +603,9 @@ hipError_t launch_nc_dp(int bwd, const NcParams &P, int N, hipStream_t s)
     // 2048 workgroups (8 per CU)
     const int ntt = (P.T + NC_TT - 1) / NC_TT;
     NcParams Q = P;
-    if (P.S <= 32 || (P.S <= 64 && DP <= 128)) {
-        // matrix-core kernels (buckets padded to 32, or to 64 up to D = 128 for their LDS): a
-        // workgroup walks up to 16 steps of 128 tokens, about 1024 workgroups in the grid
+    if (P.S <= 32 || (P.S <= 64 && DP <= 128) || (P.S <= 128 && DP <= 64)) {
+        // matrix-core kernels (buckets padded to 32, to 64 up to D = 128 or to 128 up to D = 64, for
+        // their LDS): a workgroup walks up to 16 steps of 128 tokens, about 1024 workgroups in the grid
         const int nstep = (P.T + NCM_TT - 1) / NCM_TT;
         Q.tpw = (int)std::max<int64_t>(1, std::min<int64_t>(16, (int64_t)nstep * N / 1024));
         const dim3 grid((unsigned)((nstep + Q.tpw - 1) / Q.tpw), (unsigned)N);
@@ -614,11 +614,18 @@ hipError_t launch_nc_dp(int bwd, const NcParams &P, int N, hipStream_t s)
                 hipLaunchKernelGGL((race_nc_backward_mfma<DP, 32>), grid, dim3(NCM_NTH), 0, s, Q);
             else
                 hipLaunchKernelGGL((race_nc_readout_mfma<DP, 32>), grid, dim3(NCM_NTH), 0, s, Q);
-        } else if constexpr (DP <= 128) {
+        } else if (P.S <= 64) {
+            if constexpr (DP <= 128) {
+                if (bwd)
+                    hipLaunchKernelGGL((race_nc_backward_mfma<DP, 64>), grid, dim3(NCM_NTH), 0, s, Q);
+                else
+                    hipLaunchKernelGGL((race_nc_readout_mfma<DP, 64>), grid, dim3(NCM_NTH), 0, s, Q);
+            }
+        } else if constexpr (DP <= 64) {
             if (bwd)
-                hipLaunchKernelGGL((race_nc_backward_mfma<DP, 64>), grid, dim3(NCM_NTH), 0, s, Q);
+                hipLaunchKernelGGL((race_nc_backward_mfma<DP, 128>), grid, dim3(NCM_NTH), 0, s, Q);
             else
-                hipLaunchKernelGGL((race_nc_readout_mfma<DP, 64>), grid, dim3(NCM_NTH), 0, s, Q);
+                hipLaunchKernelGGL((race_nc_readout_mfma<DP, 128>), grid, dim3(NCM_NTH), 0, s, Q);
         }
         return hipGetLastError();
     }
