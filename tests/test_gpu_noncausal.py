@@ -22,11 +22,13 @@ def _probs(N, T, S, D, seed):
     return pk, pq, v, go
 
 
-# S <= 32 with D <= 128 takes the matrix-core backward (ragged S and D: 30 x 100, 1 x 20, 32 x 64);
+# S <= 32 (any D), S <= 64 (D <= 128) and S <= 128 (D <= 64) take the matrix-core kernels (ragged S
+# and D: 30 x 100, 1 x 20, 32 x 64, 40 x 120, 100 x 50);
 # the last two: enough token tiles that each workgroup walks several (ragged last tile), with every
 # bucket in one chunk (S = 24) and over several chunks (S = 64)
 @pytest.mark.parametrize("N,T,S,D", [(1, 1, 8, 16), (2, 7, 24, 64), (3, 300, 128, 64), (1, 4096, 256, 128),
                                      (2, 1000, 64, 100), (2, 1000, 30, 100), (3, 517, 32, 64), (1, 77, 1, 20),
+                                     (2, 555, 40, 120), (2, 777, 100, 50),
                                      (1, 513, 300, 256), (2, 333, 24, 256), (4, 2000, 16, 32),
                                      (4, 70001, 24, 128), (4, 66017, 64, 32)])
 def test_noncausal_op(dev, N, T, S, D):
