@@ -81,6 +81,21 @@ int race_soft_hash_bwd_scale(const race_hash_shape *sh, race_tensor x, int x_dty
                              const float *planes_T, const float *gprobs, race_tensor dx,
                              float *gscale_partials, race_stream stream);
 
+/* race_soft_hash_fwd / race_soft_hash_bwd_scale with the scale read on the device from
+ * scale_dev (one fp32 > 0; sh->scale is ignored), for the learnable temperature of the
+ * non-causal BatchedACE (scaling/benchmark_time.py:104,111: scale =
+ * exp(logit_temp).clamp(1e-2, 10), a device tensor that the reference's torch autograd never
+ * reads back to the host). The backward also reduces its partials on the device:
+ * dscale[0] = -(sum of the race_soft_hash_bwd_partials(sh) partials) / scale_dev[0], summed in
+ * fp64 in a fixed order. Neither call synchronises, so both can be captured in a HIP graph. */
+int race_soft_hash_fwd_dscale(const race_hash_shape *sh, race_tensor x, int x_dtype,
+                              const float *planes_T, const float *scale_dev, float *probs,
+                              race_stream stream);
+int race_soft_hash_bwd_dscale(const race_hash_shape *sh, race_tensor x, int x_dtype,
+                              const float *planes_T, const float *scale_dev,
+                              const float *gprobs, race_tensor dx, float *gscale_partials,
+                              float *dscale, race_stream stream);
+
 /* ---------------------------------------------------------------- op-level scan */
 /* pK, pQ [N][T][S], V / out / gO / gV [N][T][D], gpK / gpQ [N][T][S]; fp32,
  * contiguous. `block` = tokens per workgroup (0: automatic; results do not depend

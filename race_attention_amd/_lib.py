@@ -52,6 +52,10 @@ SIGNATURES = {
     "race_soft_hash_bwd_partials": (ctypes.c_int, [ctypes.POINTER(HashShape)]),
     "race_soft_hash_bwd_scale": (ctypes.c_int, [ctypes.POINTER(HashShape), Tensor4, ctypes.c_int, _vp, _vp,
                                                 Tensor4, _vp, _vp]),
+    "race_soft_hash_fwd_dscale": (ctypes.c_int, [ctypes.POINTER(HashShape), Tensor4, ctypes.c_int, _vp, _vp, _vp,
+                                                 _vp]),
+    "race_soft_hash_bwd_dscale": (ctypes.c_int, [ctypes.POINTER(HashShape), Tensor4, ctypes.c_int, _vp, _vp, _vp,
+                                                 Tensor4, _vp, _vp, _vp]),
     "race_nc_op_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, ctypes.c_int]),
     "race_nc_op_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _vp,
                                       ctypes.c_size_t, _vp]),

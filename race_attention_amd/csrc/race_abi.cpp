@@ -189,8 +189,10 @@ int check_view(const race_tensor &t, const char *name, bool bf16_vec)
         if (((uintptr_t)t.data & 15) || (t.stride_b & 7) || (t.stride_h & 7) || (t.stride_t & 7))
             return fail(RACE_ERR_INVALID,
                         "%s: bf16 rows must be 16-byte aligned (pointer %% 16 == 0, strides %% 8 == 0)", name);
-        if (t.stride_t >= ((int64_t)1 << 26))
-            return fail(RACE_ERR_UNSUPPORTED, "%s: token stride %lld too large", name, (long long)t.stride_t);
+        // the row movers form in-sub-chunk row offsets with 24-bit multiplies (row < 32)
+        if (t.stride_t >= ((int64_t)1 << 24))
+            return fail(RACE_ERR_UNSUPPORTED, "%s: token stride %lld too large (at most 2^24 - 1 elements)", name,
+                        (long long)t.stride_t);
     }
     return RACE_OK;
 }
@@ -361,6 +363,48 @@ int race_soft_hash_bwd_scale(const race_hash_shape *sh, race_tensor x, int x_dty
     P.dx = to_view(dx);
     P.gscale = gscale_partials;
     return hip_check(prof_softhash(P, x_dtype == RACE_BF16, 1, hs(stream)), "race_soft_hash_bwd_scale");
+}
+
+// The same two calls with the scale read on the device (BatchedACE's learnable temperature,
+// scaling/benchmark_time.py:104,111, which the reference keeps as a device tensor): sh->scale is
+// not used. scale_dev must point to one fp32 > 0 that stays unchanged until the kernels have run.
+int race_soft_hash_fwd_dscale(const race_hash_shape *sh, race_tensor x, int x_dtype, const float *planes_T,
+                              const float *scale_dev, float *probs, race_stream stream)
+{
+    if (!scale_dev)
+        return fail(RACE_ERR_INVALID, "race_soft_hash_fwd_dscale: null scale");
+    race_hash_shape s1 = sh ? *sh : race_hash_shape{};
+    s1.scale = 1.0f;  // checked on the device side by its producer (a clamp), not here
+    SoftHashParams P;
+    RACE_TRY(hash_common(sh ? &s1 : nullptr, x, x_dtype, planes_T, P));
+    if (!probs)
+        return fail(RACE_ERR_INVALID, "race_soft_hash_fwd_dscale: null probs");
+    P.probs = probs;
+    P.scale_dev = scale_dev;
+    return hip_check(prof_softhash(P, x_dtype == RACE_BF16, 0, hs(stream)), "race_soft_hash_fwd_dscale");
+}
+
+int race_soft_hash_bwd_dscale(const race_hash_shape *sh, race_tensor x, int x_dtype, const float *planes_T,
+                              const float *scale_dev, const float *gprobs, race_tensor dx, float *gscale_partials,
+                              float *dscale, race_stream stream)
+{
+    if (!scale_dev)
+        return fail(RACE_ERR_INVALID, "race_soft_hash_bwd_dscale: null scale");
+    race_hash_shape s1 = sh ? *sh : race_hash_shape{};
+    s1.scale = 1.0f;
+    SoftHashParams P;
+    RACE_TRY(hash_common(sh ? &s1 : nullptr, x, x_dtype, planes_T, P));
+    if (!gprobs || !gscale_partials || !dscale)
+        return fail(RACE_ERR_INVALID, "race_soft_hash_bwd_dscale: null gprobs, partials or dscale");
+    RACE_TRY(check_view(dx, "race_soft_hash_bwd_dscale: dx", false));
+    P.gprobs = gprobs;
+    P.dx = to_view(dx);
+    P.gscale = gscale_partials;
+    P.scale_dev = scale_dev;
+    hipStream_t st = hs(stream);
+    RACE_TRY(hip_check(prof_softhash(P, x_dtype == RACE_BF16, 1, st), "race_soft_hash_bwd_dscale"));
+    return hip_check(launch_scale_grad(gscale_partials, race_soft_hash_bwd_partials(&s1), scale_dev, dscale, st),
+                     "race_soft_hash_bwd_dscale: scale gradient");
 }
 
 // ============================================================================ op-level scan
@@ -667,12 +711,36 @@ static int nc_vec(int64_t D, std::initializer_list<const View *> vs)
 // the contiguous [N][T][D] layout of the race_nc_op_* entry points as a view (zH = 1)
 static View nc_flat(const float *p, int64_t T, int64_t D) { return View{p, T * D, 0, D}; }
 
-static int nc_view_check(const View &v, int64_t D, const char *name, const char *who)
+// A [Bz][H][T][D] view of the view entry points. Inputs may share rows between streams (a zero
+// stream or head stride reads one row set for all of them); an output must give every
+// (stream, head, token) row its own D elements, or concurrent workgroups would write the same
+// memory: sorted by stride, each dimension of extent > 1 must step past everything the smaller
+// ones span.
+static int nc_view_check(const View &v, int64_t Bz, int64_t H, int64_t T, int64_t D, bool output, const char *name,
+                         const char *who)
 {
     if (!v.p)
         return fail(RACE_ERR_INVALID, "%s: null %s", who, name);
     if (v.sb < 0 || v.sh < 0 || v.st < D || v.st >= ((int64_t)1 << 31))
         return fail(RACE_ERR_INVALID, "%s: %s strides must be >= 0 with D <= token stride < 2^31", who, name);
+    if (output) {
+        int64_t st[3] = {v.sb, v.sh, v.st}, n[3] = {Bz, H, T};
+        for (int i = 0; i < 3; ++i)  // sort the three dimensions by stride
+            for (int j = i + 1; j < 3; ++j)
+                if (st[j] < st[i]) {
+                    std::swap(st[i], st[j]);
+                    std::swap(n[i], n[j]);
+                }
+        int64_t span = D;  // elements covered by the dimensions taken so far
+        for (int i = 0; i < 3; ++i) {
+            if (n[i] <= 1)
+                continue;
+            if (st[i] < span)
+                return fail(RACE_ERR_INVALID, "%s: output %s has overlapping rows (strides %lld, %lld, %lld)", who,
+                            name, (long long)v.sb, (long long)v.sh, (long long)v.st);
+            span = st[i] * (n[i] - 1) + span;
+        }
+    }
     return RACE_OK;
 }
 
@@ -687,8 +755,8 @@ static int nc_fwd_impl(const float *pK, const float *pQ, const View &V, const Vi
     Geo g;
     RACE_TRY(op_geometry(N, T, S, D, block, g));
     RACE_TRY(op_check(pK, pQ, static_cast<const float *>(V.p), eps, workspace, workspace_bytes, nc_bytes(g, 0), who));
-    RACE_TRY(nc_view_check(V, D, "V", who));
-    RACE_TRY(nc_view_check(out, D, "out", who));
+    RACE_TRY(nc_view_check(V, Bz, H, T, D, false, "V", who));
+    RACE_TRY(nc_view_check(out, Bz, H, T, D, true, "out", who));
     Carver cv(workspace, workspace_bytes);
     float *wsB = cv.take(g.state_elems_B), *wsA = cv.take(g.state_elems_A);
     if (state)  // the totals are kept for the backward
@@ -719,9 +787,9 @@ static int nc_bwd_impl(const float *pK, const float *pQ, const View &V, const Vi
     RACE_TRY(op_check(pK, pQ, static_cast<const float *>(V.p), eps, workspace, workspace_bytes, nc_bytes(g, 1), who));
     if (!gpK || !gpQ)
         return fail(RACE_ERR_INVALID, "%s: null gradient pointer", who);
-    RACE_TRY(nc_view_check(V, D, "V", who));
-    RACE_TRY(nc_view_check(gO, D, "gO", who));
-    RACE_TRY(nc_view_check(gV, D, "gV", who));
+    RACE_TRY(nc_view_check(V, Bz, H, T, D, false, "V", who));
+    RACE_TRY(nc_view_check(gO, Bz, H, T, D, false, "gO", who));
+    RACE_TRY(nc_view_check(gV, Bz, H, T, D, true, "gV", who));
     Carver cv(workspace, workspace_bytes);
     float *wsB = cv.take(g.state_elems_B), *wsA = cv.take(g.state_elems_A);
     float *ws2B = cv.take(g.state_elems_B), *ws2A = cv.take(g.state_elems_A);

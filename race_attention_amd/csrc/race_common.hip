@@ -299,6 +299,11 @@ RACE_DEV void sh_load_planes(float *sPl, const float *planes, const SoftHashPara
     }
 }
 
+// The logits divisor: the device scalar when one is given (a learnable temperature that stays in
+// device memory, so its caller never reads it back to the host), else the launch argument.
+RACE_DEV float sh_scale(const SoftHashParams &P) { return P.scale_dev ? *P.scale_dev : P.scale; }
+RACE_DEV float sh_inv_scale(const SoftHashParams &P) { return P.scale_dev ? 1.0f / *P.scale_dev : P.inv_scale; }
+
 // x rows of one tile into sX. vec: D % 4 == 0, and every row starts at a multiple of 4 elements
 // of a buffer aligned to 4 elements, so a row is read as runs of 4 elements (16 or 8 bytes)
 template <class TX>
@@ -357,7 +362,7 @@ RACE_DEV void sh_project(const float *sX, const float *sPl, float *sU, const Sof
         }
 #pragma unroll
         for (int q = 0; q < SH_RB; ++q)
-            sU[(rg * SH_RB + q) * LK + j] = tanh_f(acc[q]) * P.inv_scale;
+            sU[(rg * SH_RB + q) * LK + j] = tanh_f(acc[q]) * sh_inv_scale(P);
     }
 }
 
@@ -550,8 +555,8 @@ __global__ __launch_bounds__(256) void race_softhash_bwd(SoftHashParams P)
                 }
 #pragma unroll
                 for (int k = 0; k < KB; ++k) {
-                    const float th = u[k] * P.scale;
-                    sGP[r * PG + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+                    const float th = u[k] * sh_scale(P);
+                    sGP[r * PG + l * KB + k] = gu[k] * sh_inv_scale(P) * (1.0f - th * th);
                 }
             }
             __syncthreads();
@@ -780,7 +785,7 @@ RACE_DEV void shm_project(float *sU, float *sX, const float *sPlT, const SoftHas
         f32x4 u;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            u[e] = tanh_f(acc[jt][e]) * P.inv_scale;
+            u[e] = tanh_f(acc[jt][e]) * sh_inv_scale(P);
         *reinterpret_cast<f32x4 *>(sU + n16 * Y.PU + 16 * jt + 4 * g) = u;
     }
 }
@@ -932,8 +937,8 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
             }
 #pragma unroll
             for (int k = 0; k < KB; ++k) {
-                const float th = u[k] * P.scale;
-                sGP[r * Y.PD + l * KB + k] = gu[k] * P.inv_scale * (1.0f - th * th);
+                const float th = u[k] * sh_scale(P);
+                sGP[r * Y.PD + l * KB + k] = gu[k] * sh_inv_scale(P) * (1.0f - th * th);
             }
         }
         // dx^T tiles of 16 d: A = planes rows d (4-byte reads, pitch 4 x odd), B = gproj of token n16;
@@ -1010,6 +1015,29 @@ __global__ __launch_bounds__(SHM_W * 64) void race_softhash_bwd_mfma(SoftHashPar
             P.gscale[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = a;
         }
     }
+}
+
+// d loss / d scale = -(sum of the soft-hash backward's per-workgroup partials) / scale, summed in
+// fp64 by one workgroup in a fixed order (deterministic, and no host round trip for the scale).
+__global__ __launch_bounds__(256) void race_scale_grad(const float *part, int n, const float *scale, float *out)
+{
+    __shared__ double red[4];
+    double a = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256)
+        a += (double)part[i];
+    for (int o = 32; o > 0; o >>= 1)
+        a += __shfl_xor(a, o);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = a;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        out[0] = (float)(-(red[0] + red[1] + red[2] + red[3]) / (double)scale[0]);
+}
+
+hipError_t launch_scale_grad(const float *part, int n, const float *scale, float *out, hipStream_t s)
+{
+    hipLaunchKernelGGL(race_scale_grad, dim3(1), dim3(256), 0, s, part, n, scale, out);
+    return hipGetLastError();
 }
 
 template <class TX, int KB, int NJT>

@@ -511,10 +511,12 @@ __global__ __launch_bounds__(NCM_NTH) void race_nc_backward_mfma(const NcParams 
         for (int e = 0; e < 4; ++e)
             ga[j][e] = sGA[16 * j + 4 * g + e];
     constexpr int NJ = DP / 16;  // 16-wide d runs: k-steps 4 NJ over d, output tiles NJ over d
-    const bool vec_d = P.vec, vec_s = (P.S & 3) == 0;
-    // probability tiles as contiguous blocks (S % 4 == 0, every pointer 16-byte aligned)
-    const bool blk_p = SP == 32 && vec_s && ((reinterpret_cast<uintptr_t>(P.pK) | reinterpret_cast<uintptr_t>(P.gpQ) |
-                                  reinterpret_cast<uintptr_t>(P.gpK)) & 15) == 0;
+    // 16-byte gpQ / gpK stores: S % 4 == 0 and both outputs 16-byte aligned (every row then is)
+    const bool vec_d = P.vec,
+               vec_s = (P.S & 3) == 0 &&
+                       ((reinterpret_cast<uintptr_t>(P.gpQ) | reinterpret_cast<uintptr_t>(P.gpK)) & 15) == 0;
+    // probability tiles as contiguous blocks (vec_s, and pK 16-byte aligned as well)
+    const bool blk_p = SP == 32 && vec_s && (reinterpret_cast<uintptr_t>(P.pK) & 15) == 0;
     const int nstep = (P.T + NCM_TT - 1) / NCM_TT, st1 = min(nstep, ((int)blockIdx.x + 1) * P.tpw);
     for (int st = blockIdx.x * P.tpw; st < st1; ++st) {
         const int t0 = st * NCM_TT + w * 16;

@@ -20,6 +20,7 @@ struct SoftHashParams {
     int unshared;         // 1: planes differ per ensemble member
     int round_planes;     // 1: round planes to bf16 (bf16 inputs, as race_common.py:54)
     float scale, inv_scale;
+    const float *scale_dev;  // optional: the scale as one fp32 in device memory (overrides scale)
     float *gscale;        // backward, optional: per-workgroup sums of gu * u (temperature grad)
     int tpw;              // token tiles per workgroup (set by launch_softhash)
 };
@@ -31,5 +32,7 @@ int softhash_tiles_per_wg(int T, int B, int H, bool mf);
 int softhash_grid_x(int T, int B, int H, bool mf);  // workgroups along the tiles of one (b, h)
 hipError_t softhash_prepare(int D, int LK);
 hipError_t launch_softhash(const SoftHashParams &P, int bf16, int bwd, hipStream_t s);
+// out[0] = -(sum of part[0 .. n)) / scale[0]: the temperature gradient from the backward's partials
+hipError_t launch_scale_grad(const float *part, int n, const float *scale, float *out, hipStream_t s);
 
 }  // namespace race

@@ -10,7 +10,8 @@ kernel and the block scan, whose last slot is the whole-sequence sum) and the re
 and its backward are HIP kernels (race_nc_op_fwd / race_nc_op_bwd; race_nc_fwd_view /
 race_nc_bwd_view with the values in BatchedACE's [M,B,T,H,d_k] layout). The soft-hash runs
 in the HIP soft-hash kernels; with a learnable temperature its backward also returns
-d loss / d scale from per-workgroup partial sums (race_soft_hash_bwd_scale).
+d loss / d scale, reduced on the device from per-workgroup partial sums with the scale
+read from device memory (race_soft_hash_fwd_dscale / race_soft_hash_bwd_dscale).
 """
 import itertools
 
@@ -88,6 +89,20 @@ def _bhtd(X5):
         return None
 
 
+def _bhtd_rows(X5):
+    """[M*B, H, T, d] rows of X5 for the view entry points, which take one distinct row per
+    (stream, token) with a token stride of at least d: a view of X5 where its strides give that,
+    else a copy (an expanded tensor, e.g. the upstream gradient of out.sum(dim=2), has stride 0)."""
+    M, B, T, H, d = X5.shape
+    v = _bhtd(X5)
+    if v is not None:
+        z, h, t, _ = v.shape
+        sz, sh, st, _ = v.stride()
+        if st >= d and (h == 1 or sh > 0) and (z == 1 or sz > 0):
+            return v
+    return X5.permute(0, 1, 3, 2, 4).contiguous().view(M * B, H, T, d)
+
+
 class RaceNonCausalViewFn(Function):
     """out [M,B,T,H,d] fp32 = RaceNonCausalFn of probsK / probsQ [M*B*H, T, S] (streams ordered
     (m, b, h)) and values Vhf [M,B,T,H,d]: values, output and their gradients stay in the
@@ -102,18 +117,15 @@ class RaceNonCausalViewFn(Function):
         if probsK.shape != (N, T, S) or probsQ.shape != probsK.shape:
             raise ValueError(f"probsK/probsQ must be [{N},{T},S], got {tuple(probsK.shape)}, {tuple(probsQ.shape)}")
         pK, pQ = probsK.contiguous().float(), probsQ.contiguous().float()
-        V = Vhf.float()
-        Vv = _bhtd(V)
-        if Vv is None:
-            Vv = V.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, D)
-        out = torch.empty(M, B, T, H, D, dtype=torch.float32, device=V.device)
+        Vv = _bhtd_rows(Vhf.float())
+        out = torch.empty(M, B, T, H, D, dtype=torch.float32, device=Vv.device)
         lib = _lib.lib()
-        state = state_buffer(lib.race_op_state_bytes(N, T, S, D, 0), V.device, "race_op_state_bytes")
-        ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, 0, 0), V.device)
+        state = state_buffer(lib.race_op_state_bytes(N, T, S, D, 0), Vv.device, "race_op_state_bytes")
+        ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, 0, 0), Vv.device)
         vv, Vv = _lib.view4(Vv)
         ov, _ = _lib.view4(_bhtd(out))
         _lib.check(lib.race_nc_fwd_view(_lib.ptr(pK), _lib.ptr(pQ), vv, ov, M * B, H, T, S, D, float(eps), 0,
-                                        _lib.ptr(ws), ws.numel(), *state_arg(state), _lib.stream_of(V)),
+                                        _lib.ptr(ws), ws.numel(), *state_arg(state), _lib.stream_of(Vv)),
                    "race_nc_fwd_view")
         ctx.save_for_backward(pK, pQ, Vv, state)
         ctx.shape = (M, B, T, H, D)
@@ -126,10 +138,7 @@ class RaceNonCausalViewFn(Function):
         pK, pQ, Vv, state = ctx.saved_tensors
         M, B, T, H, D = ctx.shape
         N, S = pK.shape[0], pK.shape[2]
-        g = grad_out.float()
-        gv_in = _bhtd(g)
-        if gv_in is None:
-            gv_in = g.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, D)
+        gv_in = _bhtd_rows(grad_out.float())
         gpK, gpQ = torch.empty_like(pK), torch.empty_like(pQ)
         gV = torch.empty(M, B, T, H, D, dtype=torch.float32, device=pK.device)
         lib = _lib.lib()
@@ -144,29 +153,37 @@ class RaceNonCausalViewFn(Function):
 
 
 class SoftHashTempFn(Function):
-    """Soft-hash probabilities [Mp*B*H, T, L*2^K] of X [B,H,T,D] with a tensor scale;
-    the backward returns d loss / d X and d loss / d scale."""
+    """Soft-hash probabilities [Mp*B*H, T, L*2^K] of X [B,H,T,D] with a learnable scale held in
+    device memory (a 0-d fp32 tensor, as the reference's exp(logit_temp).clamp(1e-2, 10),
+    scaling/benchmark_time.py:104,111): the kernels read it there, and the backward returns
+    d loss / d X and d loss / d scale, reduced on the device. Nothing is read back to the host,
+    so a forward+backward runs asynchronously and can be captured in a HIP graph."""
 
     @staticmethod
-    def forward(ctx, X, planes_T, L, Kbits, M, unshared, scale, scale_value=None):
+    def forward(ctx, X, planes_T, L, Kbits, M, unshared, scale):
         _lib.require_device(X, planes_T)
         B, H, T, D = X.shape
-        s = float(scale.detach() if torch.is_tensor(scale) else scale) if scale_value is None else float(scale_value)
+        if not torch.is_tensor(scale):
+            scale = torch.tensor(float(scale), device=X.device)
+        _lib.require_device(scale)
+        sc = scale.detach().to(torch.float32).reshape(1).contiguous()
         planes = planes_T.detach().float().contiguous()
         xv, Xc = _lib.view4(X)
         Mp = M if unshared else 1
         probs = torch.empty(Mp * B * H, T, L << Kbits, dtype=torch.float32, device=X.device)
-        sh = _hash_shape(X, L, Kbits, M, unshared, s)
-        _lib.check(_lib.lib().race_soft_hash_fwd(sh, xv, _lib.dtype_code(X.dtype), _lib.ptr(planes),
-                                                 _lib.ptr(probs), _lib.stream_of(X)), "race_soft_hash_fwd")
-        ctx.save_for_backward(Xc, planes)
-        ctx.cfg = (L, Kbits, M, unshared, s)
+        sh = _hash_shape(X, L, Kbits, M, unshared, 1.0)  # the scale comes from sc
+        _lib.check(_lib.lib().race_soft_hash_fwd_dscale(sh, xv, _lib.dtype_code(X.dtype), _lib.ptr(planes),
+                                                        _lib.ptr(sc), _lib.ptr(probs), _lib.stream_of(X)),
+                   "race_soft_hash_fwd_dscale")
+        ctx.save_for_backward(Xc, planes, sc)
+        ctx.cfg = (L, Kbits, M, unshared)
+        ctx.scale_shape = scale.shape
         return probs
 
     @staticmethod
     def backward(ctx, gprobs):
-        Xc, planes = ctx.saved_tensors
-        L, Kbits, M, unshared, s = ctx.cfg
+        Xc, planes, sc = ctx.saved_tensors
+        L, Kbits, M, unshared = ctx.cfg
         B, H, T, D = Xc.shape
         Mp = M if unshared else 1
         g = gprobs.float().contiguous().view(Mp, B * H, T, -1)
@@ -175,13 +192,14 @@ class SoftHashTempFn(Function):
         dX = torch.empty_like(Xc)
         xv, _ = _lib.view4(Xc)
         dv, _ = _lib.view4(dX)
-        sh = _hash_shape(Xc, L, Kbits, Mp, unshared, s)
+        sh = _hash_shape(Xc, L, Kbits, Mp, unshared, 1.0)
         lib = _lib.lib()
         part = torch.empty(lib.race_soft_hash_bwd_partials(sh), dtype=torch.float32, device=Xc.device)
-        _lib.check(lib.race_soft_hash_bwd_scale(sh, xv, _lib.dtype_code(Xc.dtype), _lib.ptr(planes), _lib.ptr(g),
-                                                dv, _lib.ptr(part), _lib.stream_of(Xc)), "race_soft_hash_bwd_scale")
-        dscale = -part.double().sum() / s
-        return dX, None, None, None, None, None, dscale.to(torch.float32), None
+        dscale = torch.empty(1, dtype=torch.float32, device=Xc.device)
+        _lib.check(lib.race_soft_hash_bwd_dscale(sh, xv, _lib.dtype_code(Xc.dtype), _lib.ptr(planes), _lib.ptr(sc),
+                                                 _lib.ptr(g), dv, _lib.ptr(part), _lib.ptr(dscale),
+                                                 _lib.stream_of(Xc)), "race_soft_hash_bwd_dscale")
+        return dX, None, None, None, None, None, dscale.view(ctx.scale_shape)
 
 
 class BatchedACE(nn.Module):
@@ -208,22 +226,21 @@ class BatchedACE(nn.Module):
         M, B, T, H, dk = Khf.shape
         if M != self.M or dk != self.d_k:
             raise ValueError(f"expected [M={self.M},B,T,H,{self.d_k}] inputs, got {tuple(Khf.shape)}")
-        scale = self.logit_temp.exp().clamp(1e-2, 10.0)
-        sv = float(scale.detach())  # one host read of the temperature per call
+        scale = self.logit_temp.exp().clamp(1e-2, 10.0)  # stays on the device (no host read)
         # streams ordered (M, B, H) as benchmark_time.py:121-131; one row of planes per m
         def bhtd(X):  # [M,B,T,H,dk] -> [M*B, H, T, dk] view
             return X.permute(0, 1, 3, 2, 4).reshape(M * B, H, T, dk)
 
         if self.share_planes:
-            pK = SoftHashTempFn.apply(bhtd(Khf), self.planes_T, self.L, self.K, 1, False, scale, sv)
-            pQ = SoftHashTempFn.apply(bhtd(Qhf), self.planes_T, self.L, self.K, 1, False, scale, sv)
+            pK = SoftHashTempFn.apply(bhtd(Khf), self.planes_T, self.L, self.K, 1, False, scale)
+            pQ = SoftHashTempFn.apply(bhtd(Qhf), self.planes_T, self.L, self.K, 1, False, scale)
         else:
             # per-ensemble planes [M, dk, L*K]: member m hashes its own B*H rows
             Kx = Khf.permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
             Qx = Qhf.permute(0, 1, 3, 2, 4).reshape(M, B * H, T, dk)
-            pK = torch.cat([SoftHashTempFn.apply(Kx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale, sv)
+            pK = torch.cat([SoftHashTempFn.apply(Kx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale)
                             for m in range(M)], 0)
-            pQ = torch.cat([SoftHashTempFn.apply(Qx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale, sv)
+            pQ = torch.cat([SoftHashTempFn.apply(Qx[m:m + 1], self.planes_T[m], self.L, self.K, 1, False, scale)
                             for m in range(M)], 0)
         # values, output and gradients in the [M,B,T,H,dk] layout: no permute copies
         return RaceNonCausalViewFn.apply(pK, pQ, Vhf, eps)

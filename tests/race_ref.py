@@ -150,6 +150,38 @@ def oracle_prefix_state(k_rows, v_rows, planes_T, L, Kb, scale, chunk=1 << 20):
     return A, Bst
 
 
+def oracle_segment_windows(q, k, v, go, planes_T, L, Kb, scale, eps, b, h, t0, t1, wins, wlen):
+    """fp64 reference of one (b, h) stream with one query head per kv head (q, k, v, go
+    [B,H,T,D], any dtype, values taken exactly) on token windows inside the segment [t0, t1):
+    the bucket state of tokens [0, t0) comes from oracle_prefix_state, then the streaming C oracle
+    (oracle_c.race_windows) runs over [t0, t1) from it. out and dq need only the prefix, so they
+    are exact for any t1; dk and dv need the suffix sums of every later token, so they are exact
+    only when t1 = T (with go None only out is returned). `wins` are absolute window starts.
+    Returns out, dq, dk, dv [nwin, wlen, D] fp64."""
+    wins = sorted(int(w) for w in wins)
+    assert all(t0 <= w and w + wlen <= t1 for w in wins), (t0, t1, wins)
+    A0, B0 = oracle_prefix_state(k[b, h, :t0], v[b, h, :t0], planes_T, L, Kb, scale)
+    ks = k[b, h, t0:t1].detach().to("cpu", F64)
+    qs = q[b, h, t0:t1].detach().to("cpu", F64)
+    vs = v[b, h, t0:t1].detach().to("cpu", F64)
+    pK = _stream_probs(ks, planes_T, L, Kb, scale)
+    pQ = _stream_probs(qs, planes_T, L, Kb, scale)
+    rel = [w - t0 for w in wins]
+    gos = None if go is None else go[b, h, t0:t1].detach().to("cpu", F64)
+    res = oracle_c.race_windows(pK, pQ, vs, gos, eps, rel, wlen, A0, B0)
+    del pK, pQ
+    if go is None:
+        return res
+    out_w, gpk_w, gpq_w, gv_w = res
+    idx = torch.cat([torch.arange(w, w + wlen) for w in rel])
+    nw, S = len(wins), gpq_w.shape[-1]
+    qw = qs[idx].clone().requires_grad_(True)
+    _stream_probs(qw, planes_T, L, Kb, scale).backward(gpq_w.reshape(-1, S))
+    kw = ks[idx].clone().requires_grad_(True)
+    _stream_probs(kw, planes_T, L, Kb, scale).backward(gpk_w.reshape(-1, S))
+    return out_w, qw.grad.view(nw, wlen, -1), kw.grad.view(nw, wlen, -1), gv_w
+
+
 def qkv_blocks(T, Z, L, Kb, D=64, C=32, target=768):
     """The fused kernels' automatic block size and count (tokens per workgroup, as
     race_abi.cpp's qkv_geometry / resolve_block choose them) for Z = B*Hkv kv streams."""

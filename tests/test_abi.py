@@ -79,6 +79,11 @@ def test_misaligned_bf16_rows_rejected():
     rc = lib.race_qkv_fwd(sh, bad, good, good, ctypes.c_void_p(16), good, 1, ctypes.c_void_p(16), 1 << 30,
                           None, 0, None)
     assert rc == 1 and "aligned" in lib.race_last_error().decode()
+    # a token stride beyond the row movers' 24-bit offset multiply is refused, not wrapped
+    wide = _lib.Tensor4(16, 0, 0, 1 << 24)
+    rc = lib.race_qkv_fwd(sh, good, wide, good, ctypes.c_void_p(16), good, 1, ctypes.c_void_p(16), 1 << 30,
+                          None, 0, None)
+    assert rc == 2 and "token stride" in lib.race_last_error().decode()
 
 
 def test_cpu_tensors_rejected_without_fallback():
@@ -215,3 +220,33 @@ def test_nc_view_layouts_need_no_copy():
     # M = 2 copies of one tensor (stride 0 on M): no view
     p2 = q.permute(0, 2, 1, 3).unsqueeze(0).expand(2, -1, -1, -1, -1)
     assert _bhtd(p2) is None
+    # the upstream gradient of out.sum(dim=2) is expanded along T (token stride 0): _bhtd gives a
+    # view with stride 0, _bhtd_rows copies it to distinct rows with the same values
+    from race_attention_amd.noncausal import _bhtd_rows
+    g = torch.randn(2, 3, 1, 4, 8).expand(2, 3, 5, 4, 8)
+    assert _bhtd(g).stride(2) == 0
+    r = _bhtd_rows(g)
+    assert r.stride(2) >= 8 and r.stride(1) > 0 and torch.equal(r, g.permute(0, 1, 3, 2, 4).reshape(6, 4, 5, 8))
+    assert _bhtd_rows(x).data_ptr() == x.data_ptr()  # distinct rows already: no copy
+
+
+@pytest.mark.parametrize("out_strides", [
+    (3 * 100 * 64, 0, 64),       # every head writes the same rows
+    (0, 100 * 64, 64),           # every stream writes the same rows
+    (3 * 100 * 64, 64, 64),      # head and token strides both D: token t of head h is token t+1 of h-1
+])
+def test_noncausal_view_rejects_overlapping_outputs(out_strides):
+    """race_nc_fwd_view / race_nc_bwd_view refuse an output view (out, gV) whose rows of different
+    (stream, head, token) overlap: concurrent workgroups would race on them. Inputs may share rows
+    (here one row set read by every stream). The refusal is the host-side argument check, made
+    before any launch."""
+    lib = _lib.load_library()
+    Bz, H, T, S, D = 2, 3, 100, 24, 64
+    shared_in = _lib.Tensor4(256, 0, 0, 64)
+    bad = _lib.Tensor4(256, *out_strides)
+    fake = ctypes.c_void_p(256)
+    rc = lib.race_nc_fwd_view(fake, fake, shared_in, bad, Bz, H, T, S, D, 1e-6, 0, fake, 1 << 40, None, 0, None)
+    assert rc == 1 and "overlapping" in lib.race_last_error().decode()
+    rc = lib.race_nc_bwd_view(fake, fake, shared_in, shared_in, fake, fake, bad, Bz, H, T, S, D, 1e-6, 0, fake,
+                              1 << 40, None, 0, None)
+    assert rc == 1 and "overlapping" in lib.race_last_error().decode()

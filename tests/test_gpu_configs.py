@@ -13,17 +13,18 @@ backward, its exact suffix. Each window is normalised by itself (reference pass 
 scaling/test_kernels.py:38-51, per window), so late windows, whose gradients are orders of
 magnitude smaller than the first tokens', are held to the same relative bar.
 
-The long-context sweep (T = 2^22 and 2^24) is checked forward on windows late in the
-sequence, from the fp64 prefix state of everything before them.
+The long-context sweep (T = 2^21 .. 2^24) runs forward and backward at full size; out, dq, dk
+and dv are checked on windows across the last block boundary and at the sequence end (the oracle
+starts from the fp64 prefix state of everything before them and scans to the end), and out and dq
+across the middle block boundary (dk and dv there too at T = 2^22, over the whole suffix).
 """
 import math
 
 import pytest
 import torch
 
-from race_ref import (_stream_probs, bf16_planes, check, oracle_group_windows, oracle_layer, oracle_prefix_state,
-                      qkv_blocks)
-from oracle import oracle_c
+from race_ref import (bf16_planes, check, oracle_group_windows, oracle_layer, oracle_prefix_state,
+                      oracle_segment_windows, qkv_blocks)
 
 pytestmark = pytest.mark.gpu
 
@@ -150,36 +151,58 @@ def test_fused_t65536_whole(dev):
         print(f"T=65536 whole {name} relerr {check(name, got, r, BF16_TOL):.2e}", flush=True)
 
 
-@pytest.mark.parametrize("T", [1 << 22, 1 << 24])
-def test_cfg3_sweep_late_windows(dev, T):
-    """The long-context sweep's shapes (B=1, H=4, D=64, L=8, K=4): forward outputs of head 2 on
-    a window across the middle block boundary and on the sequence's last tokens, against the fp64
-    oracle started from the exact prefix state of all earlier tokens."""
+@pytest.mark.parametrize("T", [1 << 21, 1 << 22, 1 << 23, 1 << 24])
+def test_cfg3_sweep_fwd_bwd(dev, T):
+    """The long-context sweep (B=1, H=4, D=64, L=8, K=4, bf16 ~ N(0, 1/sqrt(D)), go ~ N(0,1)) at
+    every T it runs, forward and backward at full size, against the fp64 oracle
+    (scaling/test_kernels.py:69-104 checks gradients at every T of its sweep):
+      * the tail: out, dq, dk, dv of head 2 on a window across the last workgroup-block boundary
+        and on the sequence's last tokens; the oracle starts from the exact fp64 prefix state of
+        every earlier token and scans the tail to the end, so the suffix sums are exact;
+      * the middle: out and dq (which depend only on the prefix) on a window across the middle
+        block boundary; at T = 2^22 also dk and dv there, with the oracle scanning the whole
+        2M-token suffix."""
     from race_attention_amd import build_planes_protos, race_causal_attention
     B, H, D, L, Kb, wlen, h = 1, 4, 64, 8, 4, 256, 2
-    print(f"sweep T={T}", flush=True)
+    print(f"cfg3 sweep T={T} fwd+bwd", flush=True)
     planes_T, _ = build_planes_protos(D, Kb, L, 1, device=dev, seed=0)
-    g = torch.Generator(device=dev).manual_seed(1)
-    q, k, v = ((torch.randn(B, H, T, D, generator=g, device=dev) / math.sqrt(D)).to(torch.bfloat16)
-               for _ in range(3))
-    with torch.no_grad():
-        out = race_causal_attention(q, k, v, planes_T, L, Kb, eps=EPS)
+    q, k, v, go = _inputs(dev, B, H, H, T, D, 1.0 / math.sqrt(D), seed=1)
+    xs = [x.requires_grad_(True) for x in (q, k, v)]
+    out = race_causal_attention(*xs, planes_T, L, Kb, eps=EPS)
+    out.backward(go)
+    torch.cuda.synchronize()
+    grads = [x.grad for x in xs]
+    for x in grads:
+        assert torch.isfinite(x.float()).all()
+    q, k, v = (x.detach() for x in xs)
     CB, NB = qkv_blocks(T, B * H, L, Kb, D)
-    wins = [(NB // 2) * CB - wlen // 2, T - wlen]
     pl = bf16_planes(planes_T)
     scale = math.sqrt(D)
-    ks, vs, qs = k[0, h].cpu(), v[0, h].cpu(), q[0, h].cpu()
-    A, Bst, pos = None, None, 0
-    for w in wins:
-        a, bb = oracle_prefix_state(ks[pos:w], vs[pos:w], pl, L, Kb, scale)
-        A = a if A is None else A + a
-        Bst = bb if Bst is None else Bst + bb
-        pos = w
-        pK = _stream_probs(ks[w:w + wlen], pl, L, Kb, scale)
-        pQ = _stream_probs(qs[w:w + wlen], pl, L, Kb, scale)
-        ref = oracle_c.race_windows(pK, pQ, vs[w:w + wlen], None, EPS, [0], wlen, A, Bst)[0]
-        re = check(f"T={T} window [{w}, {w + wlen})", out[0, h, w:w + wlen], ref, BF16_TOL)
-        print(f"T={T} window [{w},{w + wlen}) relerr {re:.2e}", flush=True)
+    names = ("out", "dq", "dk", "dv")
+    got_all = [out] + grads
+
+    def compare(tag, wins, refs, which):
+        idx = torch.cat([torch.arange(w, w + wlen) for w in wins]).to(dev)
+        for name, got, ref in zip(names, got_all, refs):
+            if name in which:
+                _check_windows(f"T={T} {tag} h{h} {name}", got[0, h, idx].view(len(wins), wlen, D), ref, wins, wlen,
+                               BF16_TOL)
+
+    # tail: from just before the last block boundary to the end
+    last = (NB - 1) * CB
+    t0 = max(last - wlen, 0)
+    wins = sorted({min(max(last - wlen // 2, t0), T - 2 * wlen), T - wlen})
+    print(f"block {CB} tokens x {NB} blocks; tail [{t0}, {T}) windows {wins}", flush=True)
+    refs = oracle_segment_windows(q, k, v, go, pl, L, Kb, scale, EPS, 0, h, t0, T, wins, wlen)
+    compare("tail", wins, refs, names)
+    # middle block boundary
+    mid = (NB // 2) * CB - wlen // 2
+    if T == 1 << 22:
+        refs = oracle_segment_windows(q, k, v, go, pl, L, Kb, scale, EPS, 0, h, mid, T, [mid], wlen)
+        compare("middle (full suffix)", [mid], refs, names)
+    else:
+        refs = oracle_segment_windows(q, k, v, go, pl, L, Kb, scale, EPS, 0, h, mid, mid + wlen, [mid], wlen)
+        compare("middle", [mid], refs, ("out", "dq"))
 
 
 def test_cfg4_decode_at_baseline_shape(dev):

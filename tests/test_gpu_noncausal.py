@@ -48,12 +48,14 @@ def test_noncausal_op(dev, N, T, S, D):
     check("gV", vx.grad, vr.grad, TOL)
 
 
-@pytest.mark.parametrize("S,D,pad", [(24, 128, 0), (30, 100, 1), (64, 64, 3)])
+@pytest.mark.parametrize("S,D,pad", [(24, 128, 0), (30, 100, 1), (64, 64, 3), (100, 120, 1), (256, 64, 0)])
 def test_noncausal_view_layouts(dev, S, D, pad):
     """race_nc_fwd_view / race_nc_bwd_view (RaceNonCausalViewFn): values and upstream gradient as
     [M,B,T,H,D] slices of wider rows (odd pad: token and head strides not multiples of 4, rows
     moved element-wise), output and gV written in [M,B,T,H,D], against the fp64 oracle on the
-    same streams in [N,T,D]; S <= 32 runs the matrix-core kernels, S = 64 the FMA ones."""
+    same streams in [N,T,D]. The first three shapes run the matrix-core kernels (S <= 32, and
+    S = 64 at D <= 128 padded to 64 buckets); S = 100 at D = 120 and S = 256 run the FMA readout
+    and backward, whose rows are addressed per head through the same strided views."""
     from race_attention_amd.noncausal import RaceNonCausalViewFn
     M, B, T, H = 2, 2, 777, 3
     N = M * B * H
@@ -112,10 +114,43 @@ def test_noncausal_unaligned_buffers(dev):
     check("gV", vx.grad, vr.grad, TOL)
 
 
-@pytest.mark.parametrize("S", [64, 24])
+@pytest.mark.parametrize("S", [40, 24])
+def test_noncausal_unaligned_gradient_outputs(dev, S):
+    """race_nc_op_bwd through the C ABI with gpQ / gpK 4 bytes past 16-byte alignment (S = 40: the
+    64-bucket matrix-core backward; S = 24: the 32-bucket one with its probability-tile path): the
+    gradients are stored element-wise and equal the call with aligned outputs bitwise."""
+    from race_attention_amd import _lib
+    N, T, D, eps = 2, 1500, 64, 1e-6
+    pk, pq, v, go = (x.to(dev) for x in _probs(N, T, S, D, seed=S + 77))
+    lib = _lib.lib()
+    ws = _lib.workspace(lib.race_nc_op_workspace_bytes(N, T, S, D, 0, 1), dev)
+
+    def run(gpK, gpQ):
+        gV = torch.empty(N, T, D, device=dev)
+        _lib.check(lib.race_nc_op_bwd(_lib.ptr(pk), _lib.ptr(pq), _lib.ptr(v), _lib.ptr(go), _lib.ptr(gpK),
+                                      _lib.ptr(gpQ), _lib.ptr(gV), N, T, S, D, eps, 0, _lib.ptr(ws), ws.numel(),
+                                      _lib.stream_of(pk)), "race_nc_op_bwd")
+        return gV
+
+    def odd():
+        buf = torch.full((N * T * S + 1,), float("nan"), device=dev)
+        y = buf[1:].view(N, T, S)
+        assert y.data_ptr() % 16 == 4
+        return y
+
+    a_k, a_q = torch.empty(N, T, S, device=dev), torch.empty(N, T, S, device=dev)
+    gv_a = run(a_k, a_q)
+    o_k, o_q = odd(), odd()
+    gv_o = run(o_k, o_q)
+    torch.cuda.synchronize()
+    assert torch.equal(o_k, a_k) and torch.equal(o_q, a_q) and torch.equal(gv_o, gv_a)
+
+
+@pytest.mark.parametrize("S", [64, 24, 160])
 def test_noncausal_block_invariance(dev, S):
-    """The totals over any block split agree to fp32 rounding (S = 24: one bucket tile, with the
-    matrix-core readout; S = 64: two tiles, with the FMA readout)."""
+    """The totals over any block split agree to fp32 rounding (S = 24 and S = 64 at D = 64: one
+    bucket tile of the totals kernel, with the matrix-core readout; S = 160: three 64-bucket tiles,
+    with the FMA readout)."""
     from race_attention_amd.noncausal import race_nc_fwd
     pk, pq, v, _ = _probs(2, 3000, S, 64, seed=9)
     a = race_nc_fwd(pk.to(dev), pq.to(dev), v.to(dev), 1e-6, 0)
@@ -155,6 +190,81 @@ def test_batched_ace_noncausal_module(dev, share, M):
         r4 = orc.batched_ace_nc_ref(pack(K4), pack(V4), pack(Q4), ace.planes_T.cpu(), ace.protos_T.cpu(), L, K,
                                     share, lt.detach()).mean(0).permute(0, 2, 1, 3)
     check("race_attention", o4, r4, TOL)
+
+
+def test_batched_ace_broadcast_upstream_gradient(dev):
+    """A loss over out.sum(dim=2) hands the backward an upstream gradient expanded along T
+    (token stride 0): the module copies it to distinct rows and the gradients match fp64."""
+    from race_attention_amd.noncausal import BatchedACE
+    torch.manual_seed(0)
+    M, B, T, H, dk, L, K = 2, 2, 300, 3, 64, 4, 3
+    ace = BatchedACE(dk, K, L, M, device=dev, share_planes=True)
+    g = torch.Generator().manual_seed(3)
+    Kh, Vh, Qh = (torch.randn(M, B, T, H, dk, generator=g) for _ in range(3))
+    w = torch.randn(M, B, H, dk, generator=g)
+    lt = torch.tensor(0.0, dtype=torch.float64, requires_grad=True)
+    refs = [x.double().requires_grad_(True) for x in (Kh, Vh, Qh)]
+    ref = orc.batched_ace_nc_ref(*refs, ace.planes_T.cpu(), ace.protos_T.cpu(), L, K, True, lt)
+    (ref.sum(dim=2) * w.double()).sum().backward()
+    xs = [x.to(dev).requires_grad_(True) for x in (Kh, Vh, Qh)]
+    out = ace(*xs)
+    (out.sum(dim=2) * w.to(dev)).sum().backward()
+    for name, a, r in zip(("dK", "dV", "dQ"), xs, refs):
+        check(name, a.grad, r.grad, TOL)
+    check("dlogit_temp", ace.logit_temp.grad.reshape(1), lt.grad.reshape(1), TOL)
+
+
+def test_batched_ace_graph_replays_equal_eager(dev):
+    """The temperature stays in device memory (no host read per call), so a BatchedACE
+    forward+backward captures into a HIP graph: every replay's output and gradients, the
+    temperature's included, equal the eager call bitwise."""
+    from race_attention_amd.noncausal import BatchedACE
+    torch.manual_seed(0)
+    M, B, T, H, dk, L, K = 1, 2, 1000, 4, 64, 3, 3
+    ace = BatchedACE(dk, K, L, M, device=dev, share_planes=True)
+    with torch.no_grad():
+        ace.logit_temp.fill_(0.3)
+    g = torch.Generator(device=dev).manual_seed(21)
+
+    def draw():
+        return [torch.randn(M, B, T, H, dk, generator=g, device=dev) for _ in range(4)]
+
+    def step(kh, vh, qh, go):
+        out = ace(kh, vh, qh)
+        out.backward(go)
+        return out
+
+    leaves = [torch.zeros(M, B, T, H, dk, device=dev, requires_grad=True) for _ in range(3)]
+    go_s = torch.zeros(M, B, T, H, dk, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on a side stream, as torch's whole-step capture expects
+        for _ in range(2):
+            step(*leaves, go_s)
+            for t in leaves:
+                t.grad = None
+            ace.logit_temp.grad = None
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_s = step(*leaves, go_s)
+    torch.cuda.synchronize()
+    gt_s = ace.logit_temp.grad
+    for i in range(3):
+        x = draw()
+        with torch.no_grad():
+            for s_, t in zip(leaves + [go_s], x):
+                s_.copy_(t)
+        graph.replay()
+        got = [out_s.clone()] + [t.grad.clone() for t in leaves] + [gt_s.clone()]
+        ace.logit_temp.grad = None
+        ref_leaves = [t.clone().requires_grad_(True) for t in x[:3]]
+        ref = step(*ref_leaves, x[3])
+        torch.cuda.synchronize()
+        exp = [ref] + [t.grad for t in ref_leaves] + [ace.logit_temp.grad]
+        ace.logit_temp.grad = gt_s  # the graph's static gradient buffer
+        for name, a, b in zip(("out", "dK", "dV", "dQ", "dlogit_temp"), got, exp):
+            assert torch.equal(a, b), f"replay {i}: {name} differs from the eager call"
 
 
 def test_soft_hash_temperature_grad_multi_tile(dev):

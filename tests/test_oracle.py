@@ -227,6 +227,32 @@ def test_group_windows_and_prefix_state_equal_layer_oracle():
     assert orc.relerr(A, A_ref[0]) < 1e-12 and orc.relerr(Bst, B_ref[0]) < 1e-12
 
 
+def test_segment_windows_equal_layer_oracle():
+    """tests/race_ref.oracle_segment_windows (the long-context sweep's reference: prefix state of
+    [0, t0), then the streaming oracle over [t0, t1)) equals the whole-sequence layer oracle: out,
+    dq, dk, dv on windows of a segment that runs to the end, and out, dq on a segment that stops
+    early (dk, dv there lack the later tokens' suffix sums and are not claimed)."""
+    import sys
+    sys.path.insert(0, os.path.dirname(__file__))
+    from race_ref import oracle_layer, oracle_segment_windows
+    g = torch.Generator().manual_seed(9)
+    B, H, T, D, L, Kb, scale, eps = 1, 3, 400, 16, 2, 3, 2.5, 1e-6
+    q, k, v, go = (torch.randn(B, H, T, D, generator=g) for _ in range(4))
+    planes_T, _ = orc.build_planes_protos(D, Kb, L, seed=4)
+    ref = oracle_layer(q, k, v, planes_T, L, Kb, scale, eps, go)
+    h, wl = 2, 16
+    res = oracle_segment_windows(q, k, v, go, planes_T, L, Kb, scale, eps, 0, h, 250, T, [260, T - wl], wl)
+    for r, full in zip(res, ref):
+        for i, w in enumerate([260, T - wl]):
+            assert orc.relerr(r[i], full[0, h, w:w + wl]) < 1e-10
+    res = oracle_segment_windows(q, k, v, go, planes_T, L, Kb, scale, eps, 0, h, 100, 100 + wl, [100], wl)
+    for r, full in zip(res[:2], ref[:2]):
+        assert orc.relerr(r[0], full[0, h, 100:100 + wl]) < 1e-10
+    assert orc.relerr(res[2][0], ref[2][0, h, 100:100 + wl]) > 1e-3  # the missing suffix shows
+    out0 = oracle_segment_windows(q, k, v, None, planes_T, L, Kb, scale, eps, 0, h, 0, 40, [0], wl)
+    assert orc.relerr(out0[0], ref[0][0, h, :wl]) < 1e-12
+
+
 @pytest.mark.parametrize("NS,T,D", [(1, 1, 1), (4, 1, 8), (8, 16, 32), (16, 512, 64)])
 def test_c_prefix_mean_flat(NS, T, D):
     """kernels/cpu/test_cpu_kernels.py:49-53 sweep: C restatement vs fp64 cumsum."""
