@@ -183,14 +183,21 @@ RACE_DEV void mma_ab(f32x4 &acc, const __bf16 *A, int m0, const __bf16 *B, int n
         EngBF16::mma(acc, *reinterpret_cast<const bf16x8 *>(pa + k), *reinterpret_cast<const bf16x8 *>(pb + k));
 }
 
+// two fp32 values rounded to bf16 (round to nearest even) and packed into one dword, a in the low
+// half: one v_cvt_pk_bf16_f32 (element-wise casts of a whole vector sometimes lower to two
+// single conversions and a byte permute instead)
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+RACE_DEV uint32_t pk_bf16(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
 // store 4 accumulator rows (m0 + 4g + e) of column n as one vector: buf[n][m0+4g .. +3]
 RACE_DEV void st_vec4(__bf16 *p, const f32x4 &v)
 {
-    bf16x4 w;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-        w[e] = (__bf16)v[e];
-    *reinterpret_cast<bf16x4 *>(p) = w;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u32x2 *>(p) = u32x2{pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
 }
 
 // Operand pairs for MFMA chains whose reduction index k is a bucket or head-dim index held
@@ -200,13 +207,8 @@ RACE_DEV void st_vec4(__bf16 *p, const f32x4 &v)
 // A operand from two accumulator tiles (rows k, col m = lane%16), converted to bf16.
 RACE_DEV bf16x8 acc_pair(const f32x4 &lo, const f32x4 &hi)
 {
-    bf16x8 f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        f[e] = (__bf16)lo[e];
-        f[4 + e] = (__bf16)hi[e];
-    }
-    return f;
+    const u32x4 u = {pk_bf16(lo[0], lo[1]), pk_bf16(lo[2], lo[3]), pk_bf16(hi[0], hi[1]), pk_bf16(hi[2], hi[3])};
+    return __builtin_bit_cast(bf16x8, u);
 }
 
 // The matching operand from an LDS array stored [n][k] (k contiguous): row n0 + lane%16.
@@ -623,7 +625,7 @@ void race_fused_fwd_readout(const ScanParams P)
         }
         const float *wA = P.wsA + slot * P.S_pad + c.s0;
         for (int s = tid; s < ST; s += NTH)
-            sA0[0][s] = wA[s];
+            sA0[0][s] = wA[s] + P.eps;  // the carry holds A + eps
     }
 
     const int G = G1 ? 1 : P.G;  // G1: one query head per kv head, the head loop folds away
@@ -722,7 +724,7 @@ void race_fused_fwd_readout(const ScanParams P)
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            accA[i][e] = frcp(a[e] + P.eps);
+                            accA[i][e] = frcp(a[e]);
                     }
                     const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
                     f32x4 w;
@@ -972,7 +974,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
         }
         const float *wA = P.wsA + slot * P.S_pad + c.s0;
         for (int s = tid; s < ST; s += NTH)
-            sA0[0][s] = wA[s];
+            sA0[0][s] = wA[s] + P.eps;  // the carry holds A + eps
     }
     f32x4 accGA[TPW_A];
 #pragma unroll
@@ -1136,7 +1138,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            accI[i][e] = frcp(a[e] + P.eps);
+                            accI[i][e] = frcp(a[e]);
                     }
                     const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
 #pragma unroll
@@ -1354,7 +1356,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
         const float *wA = P.wsA + slot * P.S_pad + c.s0;
         const float *wA2 = P.ws2A + slot * P.S_pad + c.s0;
         for (int s = tid; s < ST; s += NTH) {
-            sA0[0][s] = wA[s];
+            sA0[0][s] = wA[s] + P.eps;  // the carry holds A + eps
             sGAe[0][s] = wA2[s];
         }
     }
@@ -1570,7 +1572,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                             *reinterpret_cast<f32x4 *>(&sA0[nxt][s]) = a;
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            accI[i][e] = frcp(a[e] + P.eps);
+                            accI[i][e] = frcp(a[e]);
                     }
                     const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][s]);
 #pragma unroll
@@ -1639,7 +1641,8 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
                     for (int i = 0; i < TPW_A; ++i) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float inc = row_scan16(accGA[i][e]) + carry[e];
+                            const float sc = row_scan16(accGA[i][e]);
+                            const float inc = i == 0 ? sc : sc + carry[e];  // (no "+ 0.0f" to issue)
                             gend[e] = g0[e] - inc;
                             accGA[i][e] += gend[e];
                             if (i + 1 < TPW_A)

@@ -50,24 +50,28 @@ RACE_DEV int64_t uniform_i64(int64_t x)
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// Row loads of one group of four mover waves of the wave-specialised totals kernel: one 16-byte chunk of
-// each of two C x 64 bf16 token tiles per thread, from two [B][H][T][D] tensors that each wave
-// chooses by its role. Their block row-0 pointers and row strides are made wave-uniform once, so a
-// chunk address costs a scalar row offset plus a per-lane clamp, 24-bit multiply-add and 64-bit add.
-// Rows at and beyond nv (the valid rows of the sub-chunk) re-read row nv - 1. (The backward main
-// kernel keeps the per-sub-chunk address arithmetic of tile_load: with this struct it issues ~4 %
-// fewer instructions per sub-chunk but measured 1 % slower.)
+// Row loads of one group of four mover waves of the wave-specialised backward kernels: one 16-byte
+// chunk of each of two C x 64 bf16 token tiles per thread, from two [B][H][T][D] tensors that each
+// wave chooses by its role. Their block row-0 pointers and row strides are made wave-uniform once,
+// so a sub-chunk's row-0 address is scalar arithmetic and a thread's chunk is that address plus a
+// 32-bit byte offset (the global_load form with a scalar base): a clamp and a 24-bit multiply-add
+// per load instead of 64-bit address arithmetic on every lane. Rows at and beyond nv (the valid
+// rows of the sub-chunk) re-read row nv - 1. Needs row strides below 2^24 elements (checked on
+// the host), so row * stride + column stays below 2^29 elements and its byte offset in 32 bits.
 struct MoverRows {
-    const __bf16 *pa, *pb;
-    int64_t sa, sb;
-    int row, col;  // the thread's row within the tile and element offset within the row
+    typedef const __attribute__((address_space(1))) char gchar;  // global memory, byte addressed
+    typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+    gchar *pa, *pb;
+    int64_t sa, sb;  // row strides in bytes
+    int row, col;    // the thread's row within the tile and element offset within the row
 
+    // a / b: this wave's two tensors (a per-wave choice, made wave-uniform here, after the choice)
     RACE_DEV void init(const __bf16 *a, int64_t sta, const __bf16 *b, int64_t stb, int mid, int chunks_per_row)
     {
-        pa = uniform_ptr(a);
-        pb = uniform_ptr(b);
-        sa = uniform_i64(sta);
-        sb = uniform_i64(stb);
+        pa = (gchar *)(uint64_t)uniform_i64((int64_t)reinterpret_cast<uintptr_t>(a));
+        pb = (gchar *)(uint64_t)uniform_i64((int64_t)reinterpret_cast<uintptr_t>(b));
+        sa = uniform_i64(sta) * 2;
+        sb = uniform_i64(stb) * 2;
         row = mid / chunks_per_row;
         col = (mid % chunks_per_row) * 8;
     }
@@ -76,8 +80,10 @@ struct MoverRows {
     RACE_DEV void load(u32x4 &ra, u32x4 &rb, int t_off, int nv) const
     {
         const unsigned rr = (unsigned)min(row, nv - 1);
-        ra = *reinterpret_cast<const u32x4 *>(pa + t_off * sa + (uint64_t)(__umul24(rr, (unsigned)sa) + col));
-        rb = *reinterpret_cast<const u32x4 *>(pb + t_off * sb + (uint64_t)(__umul24(rr, (unsigned)sb) + col));
+        const unsigned oa = (__umul24(rr, (unsigned)(sa >> 1)) + col) * 2u;
+        const unsigned ob = (__umul24(rr, (unsigned)(sb >> 1)) + col) * 2u;
+        ra = *reinterpret_cast<gu32x4 *>(pa + t_off * sa + (uint64_t)oa);
+        rb = *reinterpret_cast<gu32x4 *>(pb + t_off * sb + (uint64_t)ob);
     }
 };
 
@@ -170,7 +176,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     {
         const float *wA = P.wsA + slot * P.S_pad + c.s0;
         for (int s = tid; s < ST; s += NTH)
-            sA0[0][s] = wA[s];
+            sA0[0][s] = wA[s] + P.eps;  // the carry holds A + eps
     }
 
     // ---- helper waves: planes fragments of projection tile hw (k and q share the rows j; the state
@@ -217,10 +223,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
         }
     }
     MoverRows mv;
-    if (movkq)
-        mv.init(row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, row_ptr(P.q, c.b, c.hk, c.t_begin), P.q.st, mid, DP / 8);
-    else
-        mv.init(row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, row_ptr(P.go, c.b, c.hk, c.t_begin), P.go.st, mid, DP / 8);
+    mv.init(movkq ? row_ptr(P.k, c.b, c.hk, c.t_begin) : row_ptr(P.v, c.b, c.hk, c.t_begin), movkq ? P.k.st : P.v.st,
+            movkq ? row_ptr(P.q, c.b, c.hk, c.t_begin) : row_ptr(P.go, c.b, c.hk, c.t_begin), movkq ? P.q.st : P.go.st,
+            mid, DP / 8);
     // movers: rows of sub-chunk s into registers (2 loads)
     auto load_rows = [&](MoveRegs &m, int s) { mv.load(m.a[0], m.b[0], s * C, nv_of(s)); };
     auto stage_rows = [&](const MoveRegs &m, int s) {  // movers: registers into LDS (v, go by parity)
@@ -378,7 +383,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
                         *reinterpret_cast<f32x4 *>(&sA0[nxt][sb]) = a;
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        accI[tt][e] = frcp(a[e] + P.eps);
+                        accI[tt][e] = frcp(a[e]);
                     const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[cur][tok][sb]);
                     f32x4 w;
 #pragma unroll
@@ -519,7 +524,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     static_assert(CF::NPT == NWH, "one projection tile of k and of q per helper wave");
     static_assert(CF::LKP == 32, "one MFMA k step for the dk product");
     static_assert(CH::CHUNKS == NTHH && CH::PF == 1, "one 16-byte chunk of each row tile per mover thread");
-    static_assert(MTC * MTC == NWH && NWS == 2 * NWH, "Mg on state waves 0-3, Mp on waves 4-7");
+    static_assert(MTC * MTC == NWH && NWS == 2 * NWH, "Mg on state waves 0-3, Mp on the helper waves");
     constexpr int TPH = NTD * MTC / NWH;  // dk and dv tiles per helper wave
     static_assert(TPH * NWH == NTD * MTC, "dk, dv tiles split evenly over the helper waves");
 
@@ -611,16 +616,11 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     struct MoveRegs {
         u32x4 a[1], b[1];
     };
-    auto load_rows = [&](MoveRegs &m, int s) {
-        const int t0 = c.t_begin + s * C, nv = nv_of(s);
-        if (movkq) {
-            tile_load<CH>(m.a, row_ptr(P.k, c.b, c.hk, t0), P.k.st, nv, mid);
-            tile_load<CH>(m.b, row_ptr(P.q, c.b, c.hk, t0), P.q.st, nv, mid);
-        } else {
-            tile_load<CH>(m.a, row_ptr(P.v, c.b, c.hk, t0), P.v.st, nv, mid);
-            tile_load<CH>(m.b, row_ptr(P.go, c.b, c.hk, t0), P.go.st, nv, mid);
-        }
-    };
+    MoverRows mv;
+    mv.init(movkq ? row_ptr(P.k, c.b, c.hk, c.t_begin) : row_ptr(P.v, c.b, c.hk, c.t_begin), movkq ? P.k.st : P.v.st,
+            movkq ? row_ptr(P.q, c.b, c.hk, c.t_begin) : row_ptr(P.go, c.b, c.hk, c.t_begin), movkq ? P.q.st : P.go.st,
+            mid, DP / 8);
+    auto load_rows = [&](MoveRegs &m, int s) { mv.load(m.a[0], m.b[0], s * C, nv_of(s)); };
     auto stage_rows = [&](const MoveRegs &m, int s) {
         const int nv = nv_of(s), pb = s & 1;
         if (movkq) {
@@ -657,7 +657,6 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         // (bucket tiles launched one after another) the earlier tiles' fp32 sums of the dk and dv
         // rows, loaded a barrier phase before their stores
         AccRows<C, DP, NTHH> arK, arV;
-        auto hash_q = [&](int s) { hash_fwd(fp, &sQ[0][0], &sPQ[0][0], LDS, hw, s, false); };
         // soft-hash backward of k for sub-chunk s (gpK rows in sF) -> sGU
         auto bwd_k = [&](int s) {
             const int tok = htt * 16 + (lane & 15), table = hjt * 4 + (lane >> 4);
@@ -690,6 +689,19 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                     EngBF16::mma(accV[i], ld_tr(&sdS[0][0], LDX, kk, td * 16, lane),
                                  ld_k(&sPK[s & 1][0][0], LDK, tt * 16, kk, lane));
             }
+        };
+        // Mp[tau][t] = pK_tau . W_t (t >= tau) of sub-chunk s, tile hw: rows t (tile ta), cols tau
+        // (tile tb) -> sMp, for dv_fin in the next phase
+        auto mp_tile = [&](int s) {
+            const int ta = hw / MTC, tb = hw % MTC;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            mma_ab<ST, LDS, LDK>(acc, &sW[0][0], ta * 16, &sPK[s & 1][0][0], tb * 16, lane);
+            const int r0 = ta * 16 + g4, c0 = tb * 16 + (lane & 15);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (r0 + e < c0)
+                    acc[e] = 0.0f;
+            st_vec4(&sMp[c0][r0], acc);
         };
         // dv^T of sub-chunk s += go^T Mp^T -> sOv
         auto dv_fin = [&](int s) {
@@ -738,7 +750,6 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
 
         // the same barrier sequence as the state waves: 2 before the loop, 2 per sub-chunk, 2 after
         __syncthreads();  // rows of sub-chunk 0 in LDS
-        hash_q(0);
         __syncthreads();
         for (int s = 0; s < nsub; ++s) {
             // X0: dk rows of s - 2 out; dv of s - 1 -> sOv; soft-hash backward of k of s - 1
@@ -758,8 +769,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 dk_mma();
             }
             dv_part(s);
-            if (s + 1 < nsub)
-                hash_q(s + 1);
+            mp_tile(s);
             __syncthreads();
         }
         acc_v(nsub - 1);
@@ -790,6 +800,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
             }
         }
         f32x4 a0 = *reinterpret_cast<const f32x4 *>(P.wsA + slot * P.S_pad + c.s0 + sb);
+        a0 += P.eps;  // the A carry holds A + eps: the scan yields the denominator directly
         f32x4 ga0 = *reinterpret_cast<const f32x4 *>(P.ws2A + slot * P.S_pad + c.s0 + sb);
         if (wave < MTC) {
             const int t = wave * 16 + (lane & 15);
@@ -806,13 +817,15 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
             for (int kb = 0; kb < DP / 32; ++kb)
                 sProjK[wave][kb][lane] = fp[kb];
         }
-        // state waves 0-3: soft-hash of k for sub-chunk s, planes fragments read from LDS
+        // state waves 0-3: soft-hash of k and of q for sub-chunk s (projection tile `wave` of each),
+        // planes fragments read from LDS
         auto hash_k = [&](int s) {
             bf16x8 fp[DP / 32];
 #pragma unroll
             for (int kb = 0; kb < DP / 32; ++kb)
                 fp[kb] = sProjK[wave][kb][lane];
             hash_fwd(fp, &sK[0][0], &sPK[s & 1][0][0], LDK, wave, s, true);
+            hash_fwd(fp, &sQ[0][0], &sPQ[0][0], LDS, wave, s, false);
         };
         f32x4 accI[MTC], accW[MTC], accG[MTC], accPK[MTC], accGA[MTC];
         MoveRegs mA, mB;
@@ -852,7 +865,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                     }
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        accI[tt][e] = frcp(a[e] + P.eps);
+                        accI[tt][e] = frcp(a[e]);
                     const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(&sPQ[tok][sb]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -915,7 +928,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                     for (int tt = 0; tt < MTC; ++tt) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float inc = row_scan16(accGA[tt][e]) + carry[e];
+                            const float sc = row_scan16(accGA[tt][e]);
+                            const float inc = tt == 0 ? sc : sc + carry[e];  // (no "+ 0.0f" to issue)
                             gend[e] = ga0[e] - inc;
                             accGA[tt][e] += gend[e];
                             if (tt + 1 < MTC)
@@ -934,18 +948,6 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                         EngBF16::mma(accPK[tt], acc_pair(accD[2 * kd], accD[2 * kd + 1]),
                                      ld_pair(&sV[cur][0][0], LDX, tt * 16, 32 * kd, lane));
                     *reinterpret_cast<f32x4 *>(&sF[tt * 16 + (lane & 15)][sb]) = accPK[tt] + accGA[tt];
-                }
-                if (wave >= NWS - MTC * MTC) {
-                    // Mp[tau][t] = pK_tau . W_t (t >= tau): rows t (tile ta), cols tau (tile tb)
-                    const int m = wave - (NWS - MTC * MTC), ta = m / MTC, tb = m % MTC;
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    mma_ab<ST, LDS, LDK>(acc, &sW[0][0], ta * 16, &sPK[cur][0][0], tb * 16, lane);
-                    const int r0 = ta * 16 + g4, c0 = tb * 16 + (lane & 15);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (r0 + e < c0)
-                            acc[e] = 0.0f;
-                    st_vec4(&sMp[c0][r0], acc);
                 }
                 // St^T[d][s] += sum_t V[t][d] pK[t][s]
 #pragma unroll

@@ -32,6 +32,9 @@ class HybridConfig:
     race_l: int = 8
     race_k: int = 4
     race_eps: float = 1e-6
+    # logits from an fp32 product of the final hidden state and the head weights (else the head
+    # runs in the weights' dtype and its bf16-rounded logits tie often in a small random model)
+    fp32_logits: bool = False
 
 
 class RMSNorm(nn.Module):
@@ -151,7 +154,10 @@ class HybridLM(nn.Module):
         x = self.embed(idx)
         for blk in self.blocks:
             x = blk(x, cos_sin, cache)
-        logits = self.lm_head(self.norm(x)).float()
+        if self.cfg.fp32_logits:
+            logits = F.linear(self.norm(x).float(), self.lm_head.weight.float())
+        else:
+            logits = self.lm_head(self.norm(x)).float()
         if targets is None:
             return logits
         return F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1))

@@ -115,15 +115,25 @@ def test_seam_backward_runs_through_fused_kernels(dev):
     assert attn.c_q.weight.grad is not None and attn.c_q.weight.grad.abs().sum() > 0
 
 
-def _tiny_lm(dev):
+def _tiny_lm(dev, fp32_logits=False):
     from race_attention_amd.hybrid import HybridConfig, HybridLM
     cfg = HybridConfig(vocab_size=1000, n_layer=2, n_embd=256, n_head=4, n_kv_head=2, mlp_hidden=512,
-                       max_seq_len=128)
+                       max_seq_len=128, fp32_logits=fp32_logits)
     return HybridLM(cfg).to(dev).init_weights(seed=0)
 
 
 def test_hybrid_cached_generation_matches_recompute(dev):
-    model = _tiny_lm(dev)
+    """Greedy decode through the RACE state cache (one fused decode kernel per layer and token)
+    against GPT.generate's full recomputation (chat/nanochat/gpt.py:519-547: the whole forward
+    re-run for every token). The two paths compute the same function with different arithmetic
+    (the chunked bf16-operand scan against the fp32 state updated token by token, and dense layers
+    at different GEMM shapes), so their logits differ by a measured e = max |logits_c - logits_r|.
+    Wherever the recomputed logits' top-2 margin exceeds 2e, the two argmaxes are equal by
+    construction (no logit can move by more than e), so there token identity is asserted without
+    any allowance; only near-ties within 2e of each other are left undecided. The head computes
+    fp32 logits (fp32_logits) so that bf16 rounding of the logits does not manufacture ties; at
+    least 20 of the 24 greedy steps must be decided, and every decided step must agree."""
+    model = _tiny_lm(dev, fp32_logits=True)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, model.cfg.vocab_size, (2, 24), generator=g).to(dev)
     n = 12
@@ -137,18 +147,21 @@ def test_hybrid_cached_generation_matches_recompute(dev):
     logits_c = torch.stack(steps)
     scale = logits_ref.abs().max().item()
     err = (logits_c - logits_ref).abs().max().item()
-    print(f"cached vs recompute logits: max abs diff {err:.3e} (max |logit| {scale:.3e})")
     assert err <= BF16_TOL * scale
     top2 = logits_ref.topk(2, dim=-1).values
     margin = top2[..., 0] - top2[..., 1]
-    sure = margin > 4 * err
+    decided = margin > 2 * err
     agree = logits_c.argmax(-1) == logits_ref.argmax(-1)
-    print(f"greedy steps with margin > 4x error: {int(sure.sum())}/{sure.numel()}")
-    assert bool(agree[sure].all())
-    # free-running cached generation follows the same tokens while margins are safe
+    print(f"cached vs recompute logits: max abs diff {err:.3e} (max |logit| {scale:.3e}); top-2 margins "
+          f"min {margin.min().item():.3e} median {margin.median().item():.3e}; decided steps (margin > 2e) "
+          f"{int(decided.sum())}/{decided.numel()}, of which agreeing {int(agree[decided].sum())}; "
+          f"all steps agreeing {int(agree.sum())}/{agree.numel()}")
+    assert int(decided.sum()) >= 20
+    assert bool(agree[decided].all())
+    # free-running cached generation follows the recomputed tokens up to the first undecided step
     toks_c, _ = model.generate(prompt, n, use_cache=True)
     for b in range(prompt.shape[0]):
-        lim = int(torch.nonzero(~sure[:, b]).min()) if (~sure[:, b]).any() else n
+        lim = int(torch.nonzero(~decided[:, b]).min()) if (~decided[:, b]).any() else n
         assert torch.equal(toks_c[b, :lim], toks_ref[b, :lim]), f"sequence {b} diverged before step {lim}"
 
 
