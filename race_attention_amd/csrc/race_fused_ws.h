@@ -292,19 +292,19 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
             *reinterpret_cast<bf16x4 *>(&sGU[tok][table * 4]) = w;
         }
     };
-    // helpers: dq^T = P gproj^T -> sO
+    // state waves: dq^T = P gproj^T -> sO, tile `wave` of the NTD x MTC (d, token) tiles (the
+    // helpers, which set the phase length, only hash q and store dq)
+    static_assert(NTD * MTC == NWS, "one dq tile per state wave");
     auto dq_mma = [&]() {
-#pragma unroll
-        for (int i = 0; i < TPH_O; ++i) {
-            const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            EngBF16::mma(acc, sBack[hw][i][lane], *reinterpret_cast<const bf16x8 *>(&sGU[tt * 16 + (lane & 15)][(lane >> 4) * 8]));
-            const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
-            if constexpr (OUT_F32)
-                *reinterpret_cast<f32x4 *>(&sO[tok][d]) = acc;
-            else
-                st_vec4(&sO[tok][d], acc);
-        }
+        const int t = wave, td = t / MTC, tt = t % MTC;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        EngBF16::mma(acc, sBack[t % NWH][t / NWH][lane],
+                     *reinterpret_cast<const bf16x8 *>(&sGU[tt * 16 + (lane & 15)][(lane >> 4) * 8]));
+        const int d = td * 16 + ((lane >> 4) << 2), tok = tt * 16 + (lane & 15);
+        if constexpr (OUT_F32)
+            *reinterpret_cast<f32x4 *>(&sO[tok][d]) = acc;
+        else
+            st_vec4(&sO[tok][d], acc);
     };
     auto dq_store = [&](int s) {  // helpers: the staged dq rows of sub-chunk s to HBM
         store_out<OT, C, DP, LDO, NTHH>(P.dq, c.b, c.hk, c.st, c.t_begin + s * C, nv_of(s), sO, arQ, hid);
@@ -334,9 +334,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
                 hash_bwd_q(s - 1);
             }
             __syncthreads();
-            // X1: dq of s - 1; soft-hash of q of s + 1 (k: state waves 0-3)
-            if (s >= 1)
-                dq_mma();
+            // X1: soft-hash of q of s + 1 (k: state waves 0-3; dq of s - 1: state waves)
             if (s + 1 < nsub)
                 hash_fwd(&sQ[0][0], &sPQ[(s & 1) ^ 1][0][0], hw, s + 1, true);
             __syncthreads();
@@ -347,8 +345,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
         acc_load(nsub - 1);
         hash_bwd_q(nsub - 1);
         __syncthreads();
-        dq_mma();
-        __syncthreads();
+        __syncthreads();  // (dq of the last sub-chunk: state waves)
         wait_vmem_all();
         dq_store(nsub - 1);
         __syncthreads();
@@ -410,7 +407,10 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
                 }
             }
             __syncthreads();
-            // X1: gW += pK^T Mg^T, gpQ, gA, dS^T += go^T W, St += V^T pK
+            // X1: dq of s - 1 (its projection gradients came from the helpers in X0);
+            //     gW += pK^T Mg^T, gpQ, gA, dS^T += go^T W, St += V^T pK
+            if (s >= 1)
+                dq_mma();
             // pK^T fragment and W (the same bf16 pQ times the same reciprocal as in X0) read again
             // rather than kept in registers across the barrier
             const bf16x8 fPK = ld_tr(&sPK[cur][0][0], LDS, 0, wave * 16, lane);
@@ -449,6 +449,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
             body(s, mA);
         wait_vmem_all();  // (the re-read rows past the end)
         __syncthreads();
+        dq_mma();  // the last sub-chunk's dq
         __syncthreads();
         // block totals: dS^T -> ws2B [s][d] ; gA (sum over tokens) -> ws2A
         float *wB = P.ws2B + (slot * P.S_pad + c.s0) * P.DPw;
