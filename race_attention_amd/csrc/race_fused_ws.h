@@ -131,7 +131,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     __shared__ __align__(16) bf16x8 sBack[NWH][TPH_O][64];
     // tanh of the q projections, from the soft-hash forward (X1) to its backward two phases later,
     // by sub-chunk parity: [parity][token][table*4 + bit]
-    __shared__ __align__(16) float sThQ[2][C][CF::LKP];
+    // (rows of LKP + 8 floats: the 16-byte writes and reads [token][table*4] of a 16-lane pass then
+    // hit every bank once; at LKP they collide four ways)
+    __shared__ __align__(16) float sThQ[2][C][CF::LKP + 8];
 
     const Ctx c = make_ctx(P, ST);
     const float coef = -2.0f * SH_LOG2E * P.inv_scale;  // soft-hash exponent factor
@@ -518,7 +520,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     // row pitches of pK, Mg / Mp and the fp32 gpK rows. pK is read mostly as 16-byte MFMA operand
     // rows (16 rows x 32 k per read): with a pitch of ST + 16 elements (an odd multiple of 32 bytes)
     // those reads hit all 64 banks once per pass, with ST + 8 two-way (measured 1.7 % faster)
-    constexpr int LDK = ST + 16, LDM = C + 8, LDF = ST + 4;
+    // Mg and Mp rows at C + 16: their 16-byte MFMA operand reads then hit every bank once per pass
+    // (two-way at C + 8, which in turn made their fewer 8-byte stores conflict-free)
+    constexpr int LDK = ST + 16, LDM = C + 16, LDF = ST + 4;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
     static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised backward: 128-bucket tiles, D = 64, K = 4");
@@ -546,7 +550,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     __shared__ __align__(16) bf16x8 sTri[MTC][64];   // lane-ordered triangle of the A scan
     // tanh of the k projections, from the soft-hash forward to its backward two phases later, by
     // sub-chunk parity: [parity][token][table*4 + bit]
-    __shared__ __align__(16) float sThK[2][C][CF::LKP];
+    __shared__ __align__(16) float sThK[2][C][CF::LKP + 8];  // (pitch: as sThQ of the totals kernel)
     // planes fragments of state waves 0-3 for their k projection tile, lane-ordered
     __shared__ __align__(16) bf16x8 sProjK[NWH][DP / 32][64];
 
