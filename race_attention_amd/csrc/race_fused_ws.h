@@ -4,14 +4,16 @@
 // Same results as race_fused_bwd_totals (race_fused.h): dq, and the block totals of W^T go and
 // of gA. The workgroup is split by role instead of by tile set:
 //  * eight state waves, wave w owning bucket tile w with its share of the bucket state St in
-//    registers: the A scan, W = pQ/(A+eps), gW = go St^T + pK^T Mg^T, gpQ, gA and the state
-//    products (St += V^T pK, dS^T += go^T W);
+//    registers: the A scan (the carry holds A + eps), W = pQ/(A+eps), gW = go St^T + pK^T Mg^T,
+//    gpQ, gA and the state products (St += V^T pK, dS^T += go^T W); they also compute dq^T =
+//    P gproj^T (one 16 x 16 tile each), move the rows (loads two sub-chunks ahead, staging into
+//    LDS: k and q by waves 0-3, v and go by waves 4-7), and waves 0-3 soft-hash the next
+//    sub-chunk's k rows (one projection tile each);
 //  * four helper waves: the soft-hash of q one sub-chunk ahead of the state waves, the soft-hash
-//    backward of q, dq = planes gproj^T and the dq stores;
-//  * the state waves also move the rows (loads two sub-chunks ahead, staging into LDS: k and q
-//    by waves 0-3, v and go by waves 4-7), and waves 0-3 soft-hash the next sub-chunk's k rows
-//    (one projection tile each): work that fits their idle time in the second phase. (Hashing
-//    q on waves 4-7 as well measured 0.6 % slower: it leaves the helpers idle in that phase.)
+//    backward of q, and the dq stores.
+// The split was balanced by timing each phase per role: with the dq product on the helpers they
+// set the length of the second phase (~2150 of 2465 cycles against ~1400 for the state waves);
+// moved to the state waves it made the kernel 6 % faster.
 // A sub-chunk costs two barrier phases (X0, X1) and each SIMD runs three waves (two state, one
 // helper), so the helpers' soft-hash arithmetic overlaps the state waves' MFMA and LDS latency.
 //
@@ -19,12 +21,13 @@
 //   X0  state: rows of s + 1 into LDS, loads of s + 3;
 //              A scan, W -> sW, gW = St go^T, Mg -> sMg                        (sub-chunk s)
 //       help:  dq rows of s - 2 out; soft-hash backward of q -> sGU            (sub-chunk s - 1)
-//   X1  state: gW += pK^T Mg^T, gpQ -> sGP, gA, dS^T += go^T W, St += V^T pK    (sub-chunk s)
+//   X1  state: dq^T = P gproj^T -> sO                                          (sub-chunk s - 1)
+//              gW += pK^T Mg^T, gpQ -> sGP, gA, dS^T += go^T W, St += V^T pK    (sub-chunk s)
 //              soft-hash of k -> pK (waves 0-3)                                 (sub-chunk s + 1)
-//       help:  dq^T = P gproj^T -> sO (s - 1); soft-hash of q -> pQ              (sub-chunk s + 1)
+//       help:  soft-hash of q -> pQ                                             (sub-chunk s + 1)
 // Arrays that the two roles use in the same phase are double buffered by sub-chunk parity
-// (v and go rows, pK, pQ, the A carry); every other array is written and read in different
-// phases.
+// (v and go rows, pK, pQ, the A carry, the tanh of the q projections); every other array is
+// written and read in different phases.
 #pragma once
 #include "race_fused.h"
 
@@ -485,25 +488,28 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
 //
 // Same results as race_fused_bwd_main (race_fused.h): dk and dv from the suffix states. Roles:
 //  * eight state waves, wave w owning bucket tile w with its share of St^T and of the suffix
-//    state dS^T in registers (both as [d][s] accumulator tiles): the A scan, W, gW = go St^T +
-//    pK^T Mg^T, gA and its suffix scan, gpK = gAhat + V dS^T + W^T Mg (dS straight from
-//    registers), Mg, Mp and the state updates; they also move the rows (k and q by waves 0-3,
-//    v and go by waves 4-7, two sub-chunks ahead);
-//  * four helper waves: the soft-hash of q one sub-chunk ahead, the soft-hash backward of k one
-//    behind, dk = planes gproj^T, dv = dS^T pK^T + go^T Mp^T and the dk and dv stores (hashing k
-//    on the helpers as well measured 2 % slower: they then set the length of the second phase).
+//    state dS^T in registers (both as [d][s] accumulator tiles): the A scan (the carry holds
+//    A + eps), W, gW = go St^T + pK^T Mg^T, gA and its suffix scan, gpK = gAhat + V dS^T + W^T Mg
+//    (dS straight from registers), Mg and the state updates; they also move the rows (k and q by
+//    waves 0-3, v and go by waves 4-7, two sub-chunks ahead), and waves 0-3 soft-hash the next
+//    sub-chunk's k and q rows (one projection tile each, from the same planes fragments);
+//  * four helper waves: the soft-hash backward of k one sub-chunk behind, Mp = pK_tau . W_t,
+//    dk = planes gproj^T, dv = dS^T pK^T + go^T Mp^T and the dk and dv stores.
+// The split was balanced by timing each phase per role: the helpers had set the length of both
+// phases (X0 ~2600 of 2770 cycles, X1 ~3260 of 3590); the q soft-hash moved to the state waves
+// and Mp to the helpers (which had become the shorter role in X1) made the kernel 4.5 % faster.
 // Two barrier phases per sub-chunk (the generic kernel has four), three waves per SIMD.
 //
-// Pipeline of sub-chunk s (state waves on s, helpers on s - 1 and s + 1 around it):
+// Pipeline of sub-chunk s (state waves on s, helpers on s - 1 and s around it):
 //   X0  state: k, q rows of s + 1 into LDS (waves 0-3); A scan, W -> sW, gW = St go^T,
 //              dS^T -= go^T W (own bucket tile, W read back by the same wave) -> sdS, Mg -> sMg
 //       help:  dk rows of s - 2 out; dv of s - 1 += go^T Mp^T -> sOv; soft-hash backward of k of
 //              s - 1 (gpK rows in sF) -> sGU
 //   X1  state: v, go rows of s + 1 into LDS (waves 4-7); gW += pK^T Mg^T, gA, gpK = W^T Mg +
-//              dS V^T, the gA suffix scan, gpK + gAhat -> sF, Mp -> sMp, St += V^T pK;
-//              soft-hash of k of s + 1 (waves 0-3)
+//              dS V^T, the gA suffix scan, gpK + gAhat -> sF, St += V^T pK;
+//              soft-hash of k and q of s + 1 (waves 0-3)
 //       help:  dv rows of s - 1 out; dk of s - 1 -> sOk; dv of s = dS^T pK^T (registers);
-//              soft-hash of q of s + 1
+//              Mp of s -> sMp
 // Arrays both roles touch in one phase are double buffered by sub-chunk parity (v and go rows,
 // pK, the tanh of the k projections); every other array is written and read in different phases.
 template <int ST, int DP, int KB, bool OUT_F32>
@@ -526,7 +532,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
     static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised backward: 128-bucket tiles, D = 64, K = 4");
-    static_assert(CF::NPT == NWH, "one projection tile of k and of q per helper wave");
+    static_assert(CF::NPT == NWH, "one projection tile of k and of q per state wave 0-3, one soft-hash backward tile of k per helper wave");
     static_assert(CF::LKP == 32, "one MFMA k step for the dk product");
     static_assert(CH::CHUNKS == NTHH && CH::PF == 1, "one 16-byte chunk of each row tile per mover thread");
     static_assert(MTC * MTC == NWH && NWS == 2 * NWH, "Mg on state waves 0-3, Mp on the helper waves");
@@ -551,7 +557,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     // tanh of the k projections, from the soft-hash forward to its backward two phases later, by
     // sub-chunk parity: [parity][token][table*4 + bit]
     __shared__ __align__(16) float sThK[2][C][CF::LKP + 8];  // (pitch: as sThQ of the totals kernel)
-    // planes fragments of state waves 0-3 for their k projection tile, lane-ordered
+    // planes fragments of state waves 0-3 for their k and q projection tile, lane-ordered
     __shared__ __align__(16) bf16x8 sProjK[NWH][DP / 32][64];
 
     const Ctx c = make_ctx(P, ST);
@@ -639,9 +645,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
 
     if (helper) {
         // ================================================================ helper waves
-        // planes fragments: projection tile hw (k and q), and the dk tiles t = hw + NWH i
-        bf16x8 fp[DP / 32], fb[TPH];
-        load_proj(fp, hw);
+        // planes fragments of the dk tiles t = hw + NWH i
+        bf16x8 fb[TPH];
 #pragma unroll
         for (int i = 0; i < TPH; ++i) {
             const int d = ((hw + NWH * i) / MTC) * 16 + (lane & 15);
@@ -767,7 +772,7 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 bwd_k(s - 1);
             }
             __syncthreads();
-            // X1: dv rows of s - 1 out; dk of s - 1; dv of s (dS part); soft-hash of s + 1
+            // X1: dv rows of s - 1 out; dk of s - 1; dv of s (dS part); Mp of s
             if (s >= 1) {
                 acc_k(s - 1);
                 store_v(s - 1);
