@@ -95,9 +95,12 @@ struct FCfg {
     static constexpr int NTD = DP / 16;
     static constexpr int NPT = NJT * MTC;      // projection tiles per tensor
     static constexpr int LDX = DP + 8;         // bf16 rows of tokens
-    // k and q rows, read only as projection operands (16-byte MFMA reads): a pitch of DP + 16
-    // elements keeps those reads conflict-free (0.5 % per layer step over DP + 8)
-    static constexpr int LDQ = DP + 16;
+    // k and q rows, read only as projection operands (16-byte MFMA reads of 16 rows): unpadded,
+    // with the 16-byte chunks of row r stored at chunk ^ (r mod QCH) (kq_off), so both the row
+    // stores (QCH threads per row) and the operand reads hit every bank once per pass (a pitch of
+    // DP + 16 kept the reads conflict-free but made the stores conflict three ways)
+    static constexpr int LDQ = DP;
+    static constexpr int QCH = DP / 8;         // 16-byte chunks per k / q row
     static constexpr int LDC = C + 8;          // bf16 rows of length C
     static constexpr int LDS = ST + 8;         // bf16 rows of length ST
     static constexpr int LDG = ((LKP + 31) / 32) * 32 + 8;  // rows of projection grads (whole MFMA k steps)
@@ -106,6 +109,14 @@ struct FCfg {
     static_assert(KB >= 2 && KB <= 4, "fused kernels: 2 <= K <= 4");
     static_assert(ST % R == 0 && ST % 32 == 0 && DP % 32 == 0, "tile shapes");
 };
+
+// Element offset of 16-byte chunk ch of row `row` in a k / q row tile (chunks XOR-swizzled by row).
+template <class CF>
+RACE_DEV int kq_off(int row, int ch)
+{
+    static_assert((CF::QCH & (CF::QCH - 1)) == 0, "power-of-two chunks per k / q row");
+    return row * CF::LDQ + 8 * (ch ^ (row & (CF::QCH - 1)));
+}
 
 // Lane-constant operand fragments (loaded once per workgroup). Projection tiles
 // are assigned to waves as t = wave + i*NW over NT tiles (k tiles, then q tiles);
@@ -165,10 +176,10 @@ template <class CF, int DP, int NSLOT>
 RACE_DEV f32x4 proj_T(const FusedFrags<CF, DP, NSLOT> &fr, int i, const __bf16 *sX, int tt, int lane)
 {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDQ + (lane >> 4) * 8;
+    const int row = tt * 16 + (lane & 15);
 #pragma unroll
     for (int kb = 0; kb < DP / 32; ++kb)
-        EngBF16::mma(acc, fr.proj[i][kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+        EngBF16::mma(acc, fr.proj[i][kb], *reinterpret_cast<const bf16x8 *>(sX + kq_off<CF>(row, kb * 4 + (lane >> 4))));
     return acc;
 }
 
@@ -274,6 +285,20 @@ RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int 
 // zeros. The copies are finite, and every product the fused kernels form with a padding token's
 // row is multiplied by that token's zero probabilities (pK, pQ and so W are masked to zero by the
 // soft-hash), or lands in an output row that is not stored: no kernel needs the zeros.
+// k or q tile rows into LDS in the swizzled layout of kq_off (rows at and beyond nv as loaded).
+template <class CF>
+RACE_DEV void tile_store_kq(__bf16 *dst, const u32x4 (&r)[CF::PF], int tid)
+{
+    constexpr int CH = CF::CHUNKS / CF::C;
+    static_assert(CH == CF::QCH, "one k / q row per QCH chunks");
+#pragma unroll
+    for (int i = 0; i < CF::PF; ++i) {
+        const int idx = tid + i * CF::NTH;
+        if (idx < CF::CHUNKS)
+            *reinterpret_cast<u32x4 *>(dst + kq_off<CF>(idx / CH, idx % CH)) = r[i];
+    }
+}
+
 template <class CF, bool ZERO = false, int LD = CF::LDX>
 RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int tid)
 {
@@ -472,7 +497,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     const int t_last = c.t_begin + (nsub - 1) * C;  // start of the last sub-chunk
     load_rows(pkB, pvB, c.t_begin);
     wait_vmem_all();
-    tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pkB, min(C, c.t_end - c.t_begin), tid);
+    tile_store_kq<CF>(&sK[0][0], pkB, tid);
     tile_store_rows<CF>(&sV[0][0][0], pvB, min(C, c.t_end - c.t_begin), tid);
     load_rows(pkA, pvA, min(c.t_begin + C, t_last));
     __syncthreads();
@@ -527,7 +552,7 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
         // nothing reads): every prefetch set is consumed on every path, so the compiler's
         // memory-counter tracking needs no wait before the set is loaded again
         wait_vmem_older<2 * CF::PF>();
-        tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], nk, min(C, c.t_end - t0 - C), tid);
+        tile_store_kq<CF>(&sK[0][0], nk, tid);
         tile_store_rows<CF>(&sV[nxt][0][0], nvr, min(C, c.t_end - t0 - C), tid);
         __syncthreads();
     };
@@ -636,8 +661,8 @@ void race_fused_fwd_readout(const ScanParams P)
         tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, nv0, tid);
         tile_load<CF>(pq, row_ptr(P.q, c.b, c.hk * G, c.t_begin), P.q.st, nv0, tid);
         tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, nv0, tid);
-        tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pk, nv0, tid);
-        tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pq, nv0, tid);
+        tile_store_kq<CF>(&sK[0][0], pk, tid);
+        tile_store_kq<CF>(&sQ[0][0], pq, tid);
         tile_store_rows<CF>(&sV[0][0][0], pv, nv0, tid);
     }
     wait_vmem_all();
@@ -663,7 +688,7 @@ void race_fused_fwd_readout(const ScanParams P)
             if (g > 0) {  // further query heads of the group: load q synchronously
                 u32x4 tq[CF::PF];
                 tile_load<CF>(tq, row_ptr(P.q, c.b, hq, t0), P.q.st, nv, tid);
-                tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], tq, nv, tid);
+                tile_store_kq<CF>(&sQ[0][0], tq, tid);
                 __syncthreads();
             }
             // ---- P1: soft-hash of k (first head only) and q; previous output rows to HBM
@@ -791,14 +816,14 @@ void race_fused_fwd_readout(const ScanParams P)
             if (g == G - 1) {
                 if (more) {
                     const int nv1 = min(C, c.t_end - t0 - C);
-                    tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pk, nv1, tid);
+                    tile_store_kq<CF>(&sK[0][0], pk, tid);
                     tile_store_rows<CF>(&sV[nxt][0][0], pv, nv1, tid);
                     if (G == 1)
-                        tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pq, nv1, tid);
+                        tile_store_kq<CF>(&sQ[0][0], pq, tid);
                     else {
                         u32x4 tq[CF::PF];
                         tile_load<CF>(tq, row_ptr(P.q, c.b, c.hk * G, t0 + C), P.q.st, nv1, tid);
-                        tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], tq, nv1, tid);
+                        tile_store_kq<CF>(&sQ[0][0], tq, tid);
                     }
                 }
             }
@@ -1065,10 +1090,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_totals(const ScanParam
             //          | T4 of the previous step
             wait_vmem_all();
             if (g == 0) {
-                tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pf.k, nv, tid);
+                tile_store_kq<CF>(&sK[0][0], pf.k, tid);
                 tile_store_rows<CF>(&sV[0][0], pf.v, nv, tid);
             }
-            tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pf.q, nv, tid);
+            tile_store_kq<CF>(&sQ[0][0], pf.q, tid);
             tile_store_rows<CF>(&sGO[0][0], pf.g, nv, tid);
             // (tiles one launch after another) the earlier tiles' sum of the previous step's dq
             // rows, stored in P2; issued before the row prefetch so that waiting for it does not
@@ -1490,10 +1515,10 @@ __global__ __launch_bounds__(NW * 64) void race_fused_bwd_main(const ScanParams 
             // ---- H0: rows into LDS (their loads were issued a step ago) | T5 of the previous sub-chunk
             wait_vmem_all();
             if (g == 0) {
-                tile_store_rows<CF, false, CF::LDQ>(&sK[0][0], pf.k, nv, tid);
+                tile_store_kq<CF>(&sK[0][0], pf.k, tid);
                 tile_store_rows<CF>(&sV[cur][0][0], pf.v, nv, tid);
             }
-            tile_store_rows<CF, false, CF::LDQ>(&sQ[0][0], pf.q, nv, tid);
+            tile_store_kq<CF>(&sQ[0][0], pf.q, tid);
             tile_store_rows<CF>(&sGO[gb][0][0], pf.g, nv, tid);
             // (tiles one launch after another) the earlier tiles' sums of the previous sub-chunk's
             // dk and dv rows, stored in H3; issued before the row prefetch

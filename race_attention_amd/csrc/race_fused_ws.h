@@ -122,7 +122,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     __shared__ __align__(16) __bf16 sPQ[2][C][LDS];
     __shared__ __align__(16) __bf16 sW[C][LDS];
     __shared__ __align__(16) __bf16 sMg[C][LDM];     // Mg as [t][tau]
-    __shared__ __align__(16) float sGP[C][ST + 4];   // gpQ rows [t][s]
+    // gpQ rows [t][s], at a pitch of ST + 8 floats: the state waves' 16-byte stores (16 tokens x 4
+    // bucket quads per pass) hit every bank once (two-way at ST + 4)
+    __shared__ __align__(16) float sGP[C][ST + 8];
     __shared__ __align__(16) __bf16 sGU[C][LDG];     // projection gradients of q [t][j]
     __shared__ __align__(16) OT sO[C][LDO];          // dq staging
     __shared__ __align__(16) float sA0[2][ST];
@@ -236,8 +238,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     auto stage_rows = [&](const MoveRegs &m, int s) {  // movers: registers into LDS (v, go by parity)
         const int nv = nv_of(s), pb = s & 1;
         if (movkq) {
-            tile_store_rows<CH, false, CF::LDQ>(&sK[0][0], m.a, nv, mid);
-            tile_store_rows<CH, false, CF::LDQ>(&sQ[0][0], m.b, nv, mid);
+            tile_store_kq<CH>(&sK[0][0], m.a, mid);
+            tile_store_kq<CH>(&sQ[0][0], m.b, mid);
         } else {
             tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
             tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
@@ -254,10 +256,10 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
     auto hash_fwd = [&](const __bf16 *sX, __bf16 *dst, int tw, int s, bool keep_th) {
         const int jt = tw / MTC, tt = tw % MTC;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDQ + (lane >> 4) * 8;
+        const int xr = tt * 16 + (lane & 15);
 #pragma unroll
         for (int kb = 0; kb < DP / 32; ++kb)
-            EngBF16::mma(acc, sProj[tw][kb][lane], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+            EngBF16::mma(acc, sProj[tw][kb][lane], *reinterpret_cast<const bf16x8 *>(sX + kq_off<CF>(xr, kb * 4 + (lane >> 4))));
         const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
         const bool ok = tok < nv_of(s) && table < c.Lt;
         float th[4], p[R];
@@ -527,8 +529,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     // rows (16 rows x 32 k per read): with a pitch of ST + 16 elements (an odd multiple of 32 bytes)
     // those reads hit all 64 banks once per pass, with ST + 8 two-way (measured 1.7 % faster)
     // Mg and Mp rows at C + 16: their 16-byte MFMA operand reads then hit every bank once per pass
-    // (two-way at C + 8, which in turn made their fewer 8-byte stores conflict-free)
-    constexpr int LDK = ST + 16, LDM = C + 16, LDF = ST + 4;
+    // (two-way at C + 8, which in turn made their fewer 8-byte stores conflict-free); gpK rows at
+    // ST + 8 floats: the state waves' 16-byte stores conflict-free (two-way at ST + 4)
+    constexpr int LDK = ST + 16, LDM = C + 16, LDF = ST + 8;
     using OT = typename std::conditional<OUT_F32, float, __bf16>::type;
     constexpr int LDO = DP + (OUT_F32 ? 4 : 8);
     static_assert(NWS == 8 && DP == 64 && KB == 4, "wave-specialised backward: 128-bucket tiles, D = 64, K = 4");
@@ -537,7 +540,9 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     static_assert(CH::CHUNKS == NTHH && CH::PF == 1, "one 16-byte chunk of each row tile per mover thread");
     static_assert(MTC * MTC == NWH && NWS == 2 * NWH, "Mg on state waves 0-3, Mp on the helper waves");
     constexpr int TPH = NTD * MTC / NWH;  // dk and dv tiles per helper wave
-    static_assert(TPH * NWH == NTD * MTC, "dk, dv tiles split evenly over the helper waves");
+    // helper wave hw owns d tile hw of every token tile: its dS^T, go^T and planes operand
+    // fragments are shared by its tiles
+    static_assert(TPH == MTC && NWH == NTD, "one d tile of every token tile per helper wave");
 
     __shared__ __align__(16) __bf16 sK[C][CF::LDQ];
     __shared__ __align__(16) __bf16 sQ[C][CF::LDQ];
@@ -583,10 +588,10 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     auto hash_fwd = [&](const bf16x8 (&fp)[DP / 32], const __bf16 *sX, __bf16 *dst, int ldd, int tw, int s, bool keep_th) {
         const int jt = tw / MTC, tt = tw % MTC;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const __bf16 *pb = sX + (tt * 16 + (lane & 15)) * CF::LDQ + (lane >> 4) * 8;
+        const int xr = tt * 16 + (lane & 15);
 #pragma unroll
         for (int kb = 0; kb < DP / 32; ++kb)
-            EngBF16::mma(acc, fp[kb], *reinterpret_cast<const bf16x8 *>(pb + kb * 32));
+            EngBF16::mma(acc, fp[kb], *reinterpret_cast<const bf16x8 *>(sX + kq_off<CF>(xr, kb * 4 + (lane >> 4))));
         const int tok = tt * 16 + (lane & 15), table = jt * 4 + (lane >> 4);
         const bool ok = tok < nv_of(s) && table < c.Lt;
         float th[4], p[R];
@@ -594,14 +599,18 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         if (keep_th)
             *reinterpret_cast<f32x4 *>(&sThK[s & 1][tok][table * 4]) = f32x4{th[0], th[1], th[2], th[3]};
         __bf16 *row = dst + tok * ldd + table * R;
+        bf16x8 w[R / 8];
 #pragma unroll
-        for (int h = 0; h < R / 8; ++h) {
-            bf16x8 w;
+        for (int h = 0; h < R / 8; ++h)
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                w[e] = (__bf16)p[8 * h + e];
-            *reinterpret_cast<bf16x8 *>(row + 8 * h) = w;
-        }
+                w[h][e] = (__bf16)p[8 * h + e];
+        // (storing the two halves in the other order on odd tokens would make these stores
+        // conflict-free at the k pitch, but the lane select of the halves costs registers: the
+        // kernel then spills and runs 66 % slower)
+#pragma unroll
+        for (int h = 0; h < R / 8; ++h)
+            *reinterpret_cast<bf16x8 *>(row + 8 * h) = w[h];
     };
     // planes fragments of projection tile tw: A operand rows j = table*4 + bit, k = d
     auto load_proj = [&](bf16x8 (&fp)[DP / 32], int tw) {
@@ -635,8 +644,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
     auto stage_rows = [&](const MoveRegs &m, int s) {
         const int nv = nv_of(s), pb = s & 1;
         if (movkq) {
-            tile_store_rows<CH, false, CF::LDQ>(&sK[0][0], m.a, nv, mid);
-            tile_store_rows<CH, false, CF::LDQ>(&sQ[0][0], m.b, nv, mid);
+            tile_store_kq<CH>(&sK[0][0], m.a, mid);
+            tile_store_kq<CH>(&sQ[0][0], m.b, mid);
         } else {
             tile_store_rows<CH>(&sV[pb][0][0], m.a, nv, mid);
             tile_store_rows<CH>(&sGO[pb][0][0], m.b, nv, mid);
@@ -645,12 +654,10 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
 
     if (helper) {
         // ================================================================ helper waves
-        // planes fragments of the dk tiles t = hw + NWH i
-        bf16x8 fb[TPH];
-#pragma unroll
-        for (int i = 0; i < TPH; ++i) {
-            const int d = ((hw + NWH * i) / MTC) * 16 + (lane & 15);
-            bf16x8 f;
+        // planes fragment of the dk tiles (d tile hw)
+        bf16x8 fb;
+        {
+            const int d = hw * 16 + (lane & 15);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int j = (lane >> 4) * 8 + e;
@@ -658,9 +665,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                 float x = 0.0f;
                 if (bit < P.K && table < c.Lt && d < P.D)
                     x = P.planes[d * LKtot + (c.l0 + table) * P.K + bit];
-                f[e] = (__bf16)x;
+                fb[e] = (__bf16)x;
             }
-            fb[i] = f;
         }
         const int hjt = hw / MTC, htt = hw % MTC;
         f32x4 accV[TPH];
@@ -691,13 +697,14 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         // dv^T of sub-chunk s = dS^T pK^T (dS after the sub-chunk) into registers
         auto dv_part = [&](int s) {
 #pragma unroll
-            for (int i = 0; i < TPH; ++i) {
-                const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
-                accV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int tt = 0; tt < MTC; ++tt)
+                accV[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < ST; kk += 32)
-                    EngBF16::mma(accV[i], ld_tr(&sdS[0][0], LDX, kk, td * 16, lane),
-                                 ld_k(&sPK[s & 1][0][0], LDK, tt * 16, kk, lane));
+            for (int kk = 0; kk < ST; kk += 32) {
+                const bf16x8 fd = ld_tr(&sdS[0][0], LDX, kk, hw * 16, lane);
+#pragma unroll
+                for (int tt = 0; tt < MTC; ++tt)
+                    EngBF16::mma(accV[tt], fd, ld_k(&sPK[s & 1][0][0], LDK, tt * 16, kk, lane));
             }
         };
         // Mp[tau][t] = pK_tau . W_t (t >= tau) of sub-chunk s, tile hw: rows t (tile ta), cols tau
@@ -715,28 +722,26 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         };
         // dv^T of sub-chunk s += go^T Mp^T -> sOv
         auto dv_fin = [&](int s) {
+            const bf16x8 fg = ld_tr(&sGO[s & 1][0][0], LDX, 0, hw * 16, lane);
 #pragma unroll
-            for (int i = 0; i < TPH; ++i) {
-                const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
-                EngBF16::mma(accV[i], ld_tr(&sGO[s & 1][0][0], LDX, 0, td * 16, lane),
-                             ld_k(&sMp[0][0], LDM, tt * 16, 0, lane));
+            for (int tt = 0; tt < MTC; ++tt) {
+                EngBF16::mma(accV[tt], fg, ld_k(&sMp[0][0], LDM, tt * 16, 0, lane));
                 if constexpr (OUT_F32)
-                    *reinterpret_cast<f32x4 *>(&sOv[tt * 16 + (lane & 15)][td * 16 + g4]) = accV[i];
+                    *reinterpret_cast<f32x4 *>(&sOv[tt * 16 + (lane & 15)][hw * 16 + g4]) = accV[tt];
                 else
-                    st_vec4(&sOv[tt * 16 + (lane & 15)][td * 16 + g4], accV[i]);
+                    st_vec4(&sOv[tt * 16 + (lane & 15)][hw * 16 + g4], accV[tt]);
             }
         };
         // dk^T = P gproj^T -> sOk
         auto dk_mma = [&]() {
 #pragma unroll
-            for (int i = 0; i < TPH; ++i) {
-                const int t = hw + NWH * i, td = t / MTC, tt = t % MTC;
+            for (int tt = 0; tt < MTC; ++tt) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                EngBF16::mma(acc, fb[i], *reinterpret_cast<const bf16x8 *>(&sGU[tt * 16 + (lane & 15)][(lane >> 4) * 8]));
+                EngBF16::mma(acc, fb, *reinterpret_cast<const bf16x8 *>(&sGU[tt * 16 + (lane & 15)][(lane >> 4) * 8]));
                 if constexpr (OUT_F32)
-                    *reinterpret_cast<f32x4 *>(&sOk[tt * 16 + (lane & 15)][td * 16 + g4]) = acc;
+                    *reinterpret_cast<f32x4 *>(&sOk[tt * 16 + (lane & 15)][hw * 16 + g4]) = acc;
                 else
-                    st_vec4(&sOk[tt * 16 + (lane & 15)][td * 16 + g4], acc);
+                    st_vec4(&sOk[tt * 16 + (lane & 15)][hw * 16 + g4], acc);
             }
         };
         auto store_k = [&](int s) {
@@ -929,6 +934,18 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                     accPK[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
                     EngBF16::mma(accPK[tt], fW, ld_tr(&sMg[0][0], LDM, 0, tt * 16, lane));
                 }
+                // gpK^T += dS V^T (dS after the sub-chunk, from registers) and St^T[d][s] += sum_t
+                // V[t][d] pK[t][s]: neither needs gA, so their operand reads and products go ahead of
+                // the serial DPP scan below and overlap it
+#pragma unroll
+                for (int tt = 0; tt < MTC; ++tt)
+#pragma unroll
+                    for (int kd = 0; kd < DP / 32; ++kd)
+                        EngBF16::mma(accPK[tt], acc_pair(accD[2 * kd], accD[2 * kd + 1]),
+                                     ld_pair(&sV[cur][0][0], LDX, tt * 16, 32 * kd, lane));
+#pragma unroll
+                for (int i = 0; i < NTD; ++i)
+                    EngBF16::mma(accS[i], ld_tr(&sV[cur][0][0], LDX, 0, i * 16, lane), fPK);
                 // gAhat_t = gAhat_start - sum_{tau < t} gA_tau: a token tile's 16 tokens lie along the
                 // 16 lanes of a DPP row, so fp32 row scans, with token tile 0's row total carried into
                 // tile 1; the sub-chunk's end value seeds the next sub-chunk
@@ -950,19 +967,10 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
                     for (int e = 0; e < 4; ++e)
                         ga0[e] = row_bcast15(gend[e]);
                 }
-                // gpK^T += dS V^T (dS after the sub-chunk, from registers) ; + gAhat -> sF
+                // gpK^T + gAhat -> sF
 #pragma unroll
-                for (int tt = 0; tt < MTC; ++tt) {
-#pragma unroll
-                    for (int kd = 0; kd < DP / 32; ++kd)
-                        EngBF16::mma(accPK[tt], acc_pair(accD[2 * kd], accD[2 * kd + 1]),
-                                     ld_pair(&sV[cur][0][0], LDX, tt * 16, 32 * kd, lane));
+                for (int tt = 0; tt < MTC; ++tt)
                     *reinterpret_cast<f32x4 *>(&sF[tt * 16 + (lane & 15)][sb]) = accPK[tt] + accGA[tt];
-                }
-                // St^T[d][s] += sum_t V[t][d] pK[t][s]
-#pragma unroll
-                for (int i = 0; i < NTD; ++i)
-                    EngBF16::mma(accS[i], ld_tr(&sV[cur][0][0], LDX, 0, i * 16, lane), fPK);
             }
             if (movkq && s + 1 < nsub)
                 hash_k(s + 1);
