@@ -281,10 +281,6 @@ RACE_DEV void tile_load(u32x4 (&r)[CF::PF], const __bf16 *base, int64_t st, int 
     }
 }
 
-// Tile rows into LDS, rows at and beyond nv as loaded (copies of row nv - 1) or, with ZERO, as
-// zeros. The copies are finite, and every product the fused kernels form with a padding token's
-// row is multiplied by that token's zero probabilities (pK, pQ and so W are masked to zero by the
-// soft-hash), or lands in an output row that is not stored: no kernel needs the zeros.
 // k or q tile rows into LDS in the swizzled layout of kq_off (rows at and beyond nv as loaded).
 template <class CF>
 RACE_DEV void tile_store_kq(__bf16 *dst, const u32x4 (&r)[CF::PF], int tid)
@@ -299,6 +295,10 @@ RACE_DEV void tile_store_kq(__bf16 *dst, const u32x4 (&r)[CF::PF], int tid)
     }
 }
 
+// Tile rows into LDS, rows at and beyond nv as loaded (copies of row nv - 1) or, with ZERO, as
+// zeros. The copies are finite, and every product the fused kernels form with a padding token's
+// row is multiplied by that token's zero probabilities (pK, pQ and so W are masked to zero by the
+// soft-hash), or lands in an output row that is not stored: no kernel needs the zeros.
 template <class CF, bool ZERO = false, int LD = CF::LDX>
 RACE_DEV void tile_store_rows(__bf16 *dst, const u32x4 (&r)[CF::PF], int nv, int tid)
 {
@@ -584,6 +584,70 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     }
 }
 
+// Wave-uniform copy of a pointer or 64-bit integer that holds the same value in every lane (a
+// per-wave choice between kernel arguments), so that the address arithmetic on it runs on the
+// scalar unit.
+template <class T>
+RACE_DEV T *uniform_ptr(T *p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T *>(((uint64_t)hi << 32) | lo);
+}
+
+RACE_DEV int64_t uniform_i64(int64_t x)
+{
+    const uint64_t v = (uint64_t)x;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Row loads of a group of four waves (the movers of the wave-specialised backward kernels, the
+// forward readout's workgroup): one 16-byte chunk of each of two C x 64 bf16 token tiles per
+// thread, from two [B][H][T][D] tensors (which may be a per-wave choice). Their block row-0 pointers and row strides are made wave-uniform once,
+// so a sub-chunk's row-0 address is scalar arithmetic and a thread's chunk is that address plus a
+// 32-bit byte offset (the global_load form with a scalar base): a clamp and a 24-bit multiply-add
+// per load instead of 64-bit address arithmetic on every lane. Rows at and beyond nv (the valid
+// rows of the sub-chunk) re-read row nv - 1. Needs row strides below 2^24 elements (checked on
+// the host), so row * stride + column stays below 2^29 elements and its byte offset in 32 bits.
+struct MoverRows {
+    typedef const __attribute__((address_space(1))) char gchar;  // global memory, byte addressed
+    typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+    gchar *pa, *pb;
+    int64_t sa, sb;  // row strides in bytes
+    int row, col;    // the thread's row within the tile and element offset within the row
+
+    // a / b: this wave's two tensors (a per-wave choice, made wave-uniform here, after the choice)
+    RACE_DEV void init(const __bf16 *a, int64_t sta, const __bf16 *b, int64_t stb, int mid, int chunks_per_row)
+    {
+        pa = (gchar *)(uint64_t)uniform_i64((int64_t)reinterpret_cast<uintptr_t>(a));
+        pb = (gchar *)(uint64_t)uniform_i64((int64_t)reinterpret_cast<uintptr_t>(b));
+        sa = uniform_i64(sta) * 2;
+        sb = uniform_i64(stb) * 2;
+        row = mid / chunks_per_row;
+        col = (mid % chunks_per_row) * 8;
+    }
+
+    // rows t_off .. t_off + C - 1 of the block (t_off = sub-chunk index * C)
+    RACE_DEV void load(u32x4 &ra, u32x4 &rb, int t_off, int nv) const
+    {
+        const unsigned rr = (unsigned)min(row, nv - 1);
+        const unsigned oa = (__umul24(rr, (unsigned)(sa >> 1)) + col) * 2u;
+        const unsigned ob = (__umul24(rr, (unsigned)(sb >> 1)) + col) * 2u;
+        ra = *reinterpret_cast<gu32x4 *>(pa + t_off * sa + (uint64_t)oa);
+        rb = *reinterpret_cast<gu32x4 *>(pb + t_off * sb + (uint64_t)ob);
+    }
+    // the first tensor's chunk only
+    RACE_DEV void load_a(u32x4 &ra, int t_off, int nv) const
+    {
+        const unsigned rr = (unsigned)min(row, nv - 1);
+        const unsigned oa = (__umul24(rr, (unsigned)(sa >> 1)) + col) * 2u;
+        ra = *reinterpret_cast<gu32x4 *>(pa + t_off * sa + (uint64_t)oa);
+    }
+};
+
 // ============================================================================ forward readout
 template <int ST, int DP, int KB, int NW, bool OUT_F32, bool G1>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(FCfg<ST, DP, KB, NW>::RO_WAVES)))
@@ -656,6 +720,15 @@ void race_fused_fwd_readout(const ScanParams P)
     const int G = G1 ? 1 : P.G;  // G1: one query head per kv head, the head loop folds away
     const int nsub = (c.t_end - c.t_begin + C - 1) / C;
     u32x4 pk[CF::PF], pq[CF::PF], pv[CF::PF];
+    // one 16-byte chunk per thread (D = 64 on four waves): the prefetch of the next rows forms its
+    // addresses from wave-uniform block row-0 pointers plus a 32-bit lane offset (MoverRows)
+    constexpr bool SB = CF::CHUNKS == NTH && DP == 64;
+    MoverRows mvKV, mvQ;
+    if constexpr (SB) {
+        mvKV.init(row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, row_ptr(P.v, c.b, c.hk, c.t_begin), P.v.st, tid, DP / 8);
+        mvQ.init(row_ptr(P.q, c.b, c.hk * G, c.t_begin), P.q.st, row_ptr(P.q, c.b, c.hk * G, c.t_begin), P.q.st, tid,
+                 DP / 8);
+    }
     {
         const int nv0 = min(C, c.t_end - c.t_begin);
         tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, c.t_begin), P.k.st, nv0, tid);
@@ -678,10 +751,16 @@ void race_fused_fwd_readout(const ScanParams P)
         const bool more = sc + 1 < nsub;
         if (more) {
             const int t1 = t0 + C, nv1 = min(C, c.t_end - t1);
-            tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, nv1, tid);
-            tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, t1), P.v.st, nv1, tid);
-            if (G == 1)
-                tile_load<CF>(pq, row_ptr(P.q, c.b, c.hk, t1), P.q.st, nv1, tid);
+            if constexpr (SB) {
+                mvKV.load(pk[0], pv[0], t1 - c.t_begin, nv1);
+                if (G == 1)
+                    mvQ.load_a(pq[0], t1 - c.t_begin, nv1);
+            } else {
+                tile_load<CF>(pk, row_ptr(P.k, c.b, c.hk, t1), P.k.st, nv1, tid);
+                tile_load<CF>(pv, row_ptr(P.v, c.b, c.hk, t1), P.v.st, nv1, tid);
+                if (G == 1)
+                    tile_load<CF>(pq, row_ptr(P.q, c.b, c.hk, t1), P.q.st, nv1, tid);
+            }
         }
         for (int g = 0; g < G; ++g) {
             const int hq = c.hk * G + g;

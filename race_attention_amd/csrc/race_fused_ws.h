@@ -33,63 +33,6 @@
 
 namespace race {
 
-// Wave-uniform copy of a pointer or 64-bit integer that holds the same value in every lane (a
-// per-wave choice between kernel arguments), so that the address arithmetic on it runs on the
-// scalar unit.
-template <class T>
-RACE_DEV T *uniform_ptr(T *p)
-{
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<T *>(((uint64_t)hi << 32) | lo);
-}
-
-RACE_DEV int64_t uniform_i64(int64_t x)
-{
-    const uint64_t v = (uint64_t)x;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
-// Row loads of one group of four mover waves of the wave-specialised backward kernels: one 16-byte
-// chunk of each of two C x 64 bf16 token tiles per thread, from two [B][H][T][D] tensors that each
-// wave chooses by its role. Their block row-0 pointers and row strides are made wave-uniform once,
-// so a sub-chunk's row-0 address is scalar arithmetic and a thread's chunk is that address plus a
-// 32-bit byte offset (the global_load form with a scalar base): a clamp and a 24-bit multiply-add
-// per load instead of 64-bit address arithmetic on every lane. Rows at and beyond nv (the valid
-// rows of the sub-chunk) re-read row nv - 1. Needs row strides below 2^24 elements (checked on
-// the host), so row * stride + column stays below 2^29 elements and its byte offset in 32 bits.
-struct MoverRows {
-    typedef const __attribute__((address_space(1))) char gchar;  // global memory, byte addressed
-    typedef const __attribute__((address_space(1))) u32x4 gu32x4;
-    gchar *pa, *pb;
-    int64_t sa, sb;  // row strides in bytes
-    int row, col;    // the thread's row within the tile and element offset within the row
-
-    // a / b: this wave's two tensors (a per-wave choice, made wave-uniform here, after the choice)
-    RACE_DEV void init(const __bf16 *a, int64_t sta, const __bf16 *b, int64_t stb, int mid, int chunks_per_row)
-    {
-        pa = (gchar *)(uint64_t)uniform_i64((int64_t)reinterpret_cast<uintptr_t>(a));
-        pb = (gchar *)(uint64_t)uniform_i64((int64_t)reinterpret_cast<uintptr_t>(b));
-        sa = uniform_i64(sta) * 2;
-        sb = uniform_i64(stb) * 2;
-        row = mid / chunks_per_row;
-        col = (mid % chunks_per_row) * 8;
-    }
-
-    // rows t_off .. t_off + C - 1 of the block (t_off = sub-chunk index * C)
-    RACE_DEV void load(u32x4 &ra, u32x4 &rb, int t_off, int nv) const
-    {
-        const unsigned rr = (unsigned)min(row, nv - 1);
-        const unsigned oa = (__umul24(rr, (unsigned)(sa >> 1)) + col) * 2u;
-        const unsigned ob = (__umul24(rr, (unsigned)(sb >> 1)) + col) * 2u;
-        ra = *reinterpret_cast<gu32x4 *>(pa + t_off * sa + (uint64_t)oa);
-        rb = *reinterpret_cast<gu32x4 *>(pb + t_off * sb + (uint64_t)ob);
-    }
-};
-
 template <int ST, int DP, int KB, bool OUT_F32>
 __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams P)
 {
