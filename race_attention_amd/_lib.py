@@ -114,6 +114,10 @@ PROF_KERNELS = ["qkv_fwd_totals", "qkv_fwd_readout", "qkv_bwd_totals", "qkv_bwd_
 _LIB = None
 
 
+# RACE_ABI_VERSION of include/race_attention.h that SIGNATURES declares
+ABI_VERSION = 2
+
+
 def load_library(path=LIB_PATH):
     """Load librace_amd.so and declare every C-ABI signature (no GPU call)."""
     global _LIB
@@ -128,6 +132,9 @@ def load_library(path=LIB_PATH):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.race_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path} implements C-ABI version {lib.race_abi_version()}, these bindings "
+                           f"declare version {ABI_VERSION}: rebuild the library")
     if path == LIB_PATH:
         _LIB = lib
     return lib

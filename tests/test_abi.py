@@ -18,6 +18,11 @@ def declared_functions():
     return sorted(set(re.findall(r"\b(race_\w+)\s*\(", text)))
 
 
+def test_binding_declares_the_header_abi_version():
+    m = re.search(r"#define RACE_ABI_VERSION (\d+)", open(HEADER).read())
+    assert m and int(m.group(1)) == _lib.ABI_VERSION
+
+
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for must in ("race_op_fwd", "race_op_bwd", "race_qkv_fwd", "race_qkv_bwd", "race_decode_step",
@@ -34,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_sizes():
     lib = _lib.load_library()
-    assert lib.race_abi_version() == 2
+    assert lib.race_abi_version() == 2 == _lib.ABI_VERSION
     sh = _lib.QKVShape(1, 4, 4, 1 << 20, 64, 8, 4, 8.0, 1e-6, 0)
     state = lib.race_qkv_state_bytes(sh)
     # per-block states (A and St, fp32, one slot per block plus the final state), not [T,S]
