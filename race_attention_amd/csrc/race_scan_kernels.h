@@ -176,11 +176,13 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_totals(const ScanParams P)
                 mma_tile<E, C>(accS[i], &sPKt[0][0], LDC, &sVt[0][0], LDC, (t / CF::NTD) * 16,
                                (t % CF::NTD) * 16, c.lane);
         }
+        if (!P.linear) {  // (grid-uniform) linear attention has no normaliser A
 #pragma unroll
-        for (int i = 0; i < TPW_A1; ++i) {
-            const int tn = c.wave + i * NW;
-            if (tn < CF::NTS)
-                mma_tile_gen<E, C>(accA[i], PredAll(), 1.0f, &sPKt[0][0], LDC, 0, tn * 16, c.lane);
+            for (int i = 0; i < TPW_A1; ++i) {
+                const int tn = c.wave + i * NW;
+                if (tn < CF::NTS)
+                    mma_tile_gen<E, C>(accA[i], PredAll(), 1.0f, &sPKt[0][0], LDC, 0, tn * 16, c.lane);
+            }
         }
         __syncthreads();
     }
@@ -307,7 +309,7 @@ __global__ __launch_bounds__(NW * 64) void race_fwd_readout(const ScanParams P)
         for (int i = 0; i < CF::TPW_CS; ++i) {
             const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
             carry[i] = 0.0f;
-            if (tn < CF::NTS) {
+            if (tn < CF::NTS && !P.linear) {  // (linear attention: no normaliser)
                 const float a0 = sA0[tn * 16 + (c.lane & 15)];
                 accA[i] = f32x4{a0, a0, a0, a0};
                 mma_tile_gen<E, C>(accA[i], PredTrilIncl(), 1.0f, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
@@ -522,14 +524,16 @@ void race_bwd_totals(const ScanParams P)
             const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
             carry[i] = 0.0f;
             accA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (tn < CF::NTS) {
+            if (tn < CF::NTS && P.linear) {
+                accA[i] = f32x4{1.f, 1.f, 1.f, 1.f};  // linear attention: W = pQ
+            } else if (tn < CF::NTS) {
                 const float a0 = sA0[tn * 16 + (c.lane & 15)];
                 accA[i] = f32x4{a0, a0, a0, a0};
                 mma_tile_gen<E, C>(accA[i], PredTrilIncl(), 1.0f, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
                 carry[i] = accA[i][3];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    accA[i][e] = P.linear ? 1.0f : frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
+                    accA[i][e] = frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
             }
         }
         __syncthreads();
@@ -863,14 +867,16 @@ void race_bwd_main(const ScanParams P)
             accA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
             accGA[i] = f32x4{0.f, 0.f, 0.f, 0.f};
             accPK[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (tn < CF::NTS) {
+            if (tn < CF::NTS && P.linear) {
+                accA[i] = f32x4{1.f, 1.f, 1.f, 1.f};  // linear attention: W = pQ
+            } else if (tn < CF::NTS) {
                 const float a0 = sA0[tn * 16 + (c.lane & 15)];
                 accA[i] = f32x4{a0, a0, a0, a0};
                 mma_tile_gen<E, C>(accA[i], PredTrilIncl(), 1.0f, &sPKt[0][0], LDC, tm * 16, tn * 16, c.lane);
                 carry[i] = accA[i][3];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    accA[i][e] = P.linear ? 1.0f : frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
+                    accA[i][e] = frcp(accA[i][e] + P.eps);  // now 1/(A+eps)
             }
         }
 #pragma unroll
@@ -1007,22 +1013,24 @@ void race_bwd_main(const ScanParams P)
                 st_cm(&sdSt[0][0], LDS_, m0, n0, c.lane, accDS[i]);
             }
         }
+        if (!P.linear) {  // (grid-uniform) linear attention has no gA
 #pragma unroll
-        for (int j = 0; j < CF::TPW_CS / MTC; ++j) {
-            const float tot = col_total<MTC>(accGA, j);
-            const int tn = c.wave + j * NW;
-            if (tn < CF::NTS && c.lane < 16)
-                sGAe[tn * 16 + c.lane] -= (double)tot;
-        }
+            for (int j = 0; j < CF::TPW_CS / MTC; ++j) {
+                const float tot = col_total<MTC>(accGA, j);
+                const int tn = c.wave + j * NW;
+                if (tn < CF::NTS && c.lane < 16)
+                    sGAe[tn * 16 + c.lane] -= (double)tot;
+            }
 #pragma unroll
-        for (int i = 0; i < CF::TPW_CS; ++i) {
-            const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
-            if (tn < CF::NTS)
-                st_rm(&sF[0][0], LDF, tm * 16, tn * 16, c.lane, accGA[i]);
+            for (int i = 0; i < CF::TPW_CS; ++i) {
+                const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
+                if (tn < CF::NTS)
+                    st_rm(&sF[0][0], LDF, tm * 16, tn * 16, c.lane, accGA[i]);
+            }
         }
         __syncthreads();
         // gAhat_t = gAhat_end + sum_{tau>=t, tau in this sub-chunk} gA_tau
-        for (int s = c.tid; s < ST; s += NTH) {
+        for (int s = c.tid; s < ST && !P.linear; s += NTH) {
             float run = (float)sGAe[s];
             for (int t = C - 1; t >= 0; --t) {
                 run += sF[t][s];
@@ -1049,9 +1057,11 @@ void race_bwd_main(const ScanParams P)
             const int tm = i % MTC, tn = c.wave + (i / MTC) * NW;
             if (tn < CF::NTS) {
                 const int r = acc_row(tm * 16, c.lane), col = acc_col(tn * 16, c.lane);
+                if (!P.linear) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    accPK[i][e] += sF[r + e][col];
+                    for (int e = 0; e < 4; ++e)
+                        accPK[i][e] += sF[r + e][col];
+                }
                 if constexpr (CF::QKV)
                     st_rm(&sF[0][0], LDF, tm * 16, tn * 16, c.lane, accPK[i]);
                 else
