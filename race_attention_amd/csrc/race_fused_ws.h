@@ -449,8 +449,8 @@ __global__ __launch_bounds__(768) void race_fused_bwd_totals_ws(const ScanParams
 // Pipeline of sub-chunk s (state waves on s, helpers on s - 1 and s around it):
 //   X0  state: k, q rows of s + 1 into LDS (waves 0-3); A scan, W -> sW, gW = St go^T,
 //              dS^T -= go^T W (own bucket tile, W read back by the same wave) -> sdS, Mg -> sMg
-//       help:  dk rows of s - 2 out; dv of s - 1 += go^T Mp^T -> sOv; soft-hash backward of k of
-//              s - 1 (gpK rows in sF) -> sGU
+//       help:  soft-hash backward of k of s - 1 (gpK rows in sF) -> sGU; dv of s - 1 += go^T Mp^T
+//              -> sOv; dk rows of s - 2 out
 //   X1  state: v, go rows of s + 1 into LDS (waves 4-7); gW += pK^T Mg^T, gA, gpK = W^T Mg +
 //              dS V^T, the gA suffix scan, gpK + gAhat -> sF, St += V^T pK;
 //              soft-hash of k and q of s + 1 (waves 0-3)
@@ -711,15 +711,15 @@ __global__ __launch_bounds__(768) void race_fused_bwd_main_ws(const ScanParams P
         __syncthreads();  // rows of sub-chunk 0 in LDS
         __syncthreads();
         for (int s = 0; s < nsub; ++s) {
-            // X0: dk rows of s - 2 out; dv of s - 1 -> sOv; soft-hash backward of k of s - 1
-            if (s >= 1)
+            // X0: soft-hash backward of k of s - 1; dv of s - 1 -> sOv; dk rows of s - 2 out (the stores
+            // last: first, they delay the phase's products by 2.5 %)
+            if (s >= 1) {
                 acc_v(s - 1);
+                bwd_k(s - 1);
+                dv_fin(s - 1);
+            }
             if (s >= 2)
                 store_k(s - 2);
-            if (s >= 1) {
-                dv_fin(s - 1);
-                bwd_k(s - 1);
-            }
             __syncthreads();
             // X1: dv rows of s - 1 out; dk of s - 1; dv of s (dS part); Mp of s
             if (s >= 1) {
