@@ -839,18 +839,9 @@ void race_fused_fwd_readout(const ScanParams P)
                 }
             }
             __syncthreads();
-            // ---- P3: out^T = St^T W^T (state operand from registers) ; Pm^T = triu-masked pK W^T
-            //          -> sPm ; St += pK^T V (last head)
-            f32x4 accO[TPW_O];
-#pragma unroll
-            for (int i = 0; i < TPW_O; ++i) {
-                const int j = i / MTC, tt = i % MTC;
-                accO[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < ST / 32; ++ks)
-                    EngBF16::mma(accO[i], acc_pair(accS[(2 * ks) * NDW + j], accS[(2 * ks + 1) * NDW + j]),
-                                 ld_pair(&sW[0][0], LDS, tt * 16, 32 * ks, lane));
-            }
+            // ---- P3: Pm^T = triu-masked pK W^T -> sPm (first: its LDS stores then drain behind the
+            //          products, 1.5 % faster) ; out^T = St^T W^T (state operand from registers) ;
+            //          St += pK^T V (last head)
 #pragma unroll
             for (int i = 0; i < TPW_M; ++i) {
                 const int t = wave + i * NW;
@@ -865,6 +856,16 @@ void race_fused_fwd_readout(const ScanParams P)
                             acc[e] = 0.0f;
                     st_vec4(&sPm[tok][tau], acc);
                 }
+            }
+            f32x4 accO[TPW_O];
+#pragma unroll
+            for (int i = 0; i < TPW_O; ++i) {
+                const int j = i / MTC, tt = i % MTC;
+                accO[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < ST / 32; ++ks)
+                    EngBF16::mma(accO[i], acc_pair(accS[(2 * ks) * NDW + j], accS[(2 * ks + 1) * NDW + j]),
+                                 ld_pair(&sW[0][0], LDS, tt * 16, 32 * ks, lane));
             }
             if (g == G - 1) {
 #pragma unroll
