@@ -33,8 +33,8 @@ static hipError_t launch_fv(ScanKernel k, const ScanParams &P, dim3 grid, hipStr
         hipLaunchKernelGGL((race_fused_fwd_readout<ST, DP, KB, NW, false, G1>), grid, block, 0, s, P);
     else if (k == K_BWD_TOTALS && G1 && ST == 128 && DP == 64 && KB == 4 && !P.dq.f32) {
         // wave-specialised variant, bf16 dq: eight state waves and four helper waves (race_fused_ws.h),
-        // with fp32 staging when bucket tiles are launched one after another (cfg2: 1 % faster than
-        // the 8-wave kernel there)
+        // also with fp32 staging of a later bucket tile (cfg2: 1 % faster than the 8-wave kernel
+        // there); for the first tile's fp32 partial output the 8-wave kernel measured 1.5 % faster
         if constexpr (G1 && ST == 128 && DP == 64 && KB == 4) {
             if (P.dq.stage_f32)
                 hipLaunchKernelGGL((race_fused_bwd_totals_ws<ST, DP, KB, true>), grid, dim3(768), 0, s, P);
