@@ -298,9 +298,10 @@ def bench_sweep(torch, args, build_planes_protos, race_causal_attention):
             q.grad = k.grad = v.grad = None
             race_causal_attention(q, k, v, planes_T, L, K).backward(go)
 
-        step()
+        for _ in range(3):  # (the first T also warms the device's clocks)
+            step()
         torch.cuda.synchronize()
-        reps = 3
+        reps = 5
         t0 = time.perf_counter()
         for _ in range(reps):
             step()
