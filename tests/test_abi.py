@@ -255,3 +255,21 @@ def test_noncausal_view_rejects_overlapping_outputs(out_strides):
     rc = lib.race_nc_bwd_view(fake, fake, shared_in, shared_in, fake, fake, bad, Bz, H, T, S, D, 1e-6, 0, fake,
                               1 << 40, None, 0, None)
     assert rc == 1 and "overlapping" in lib.race_last_error().decode()
+
+
+def test_integration_bindings_match_the_library_signatures():
+    """The ctypes stubs that INTEGRATION.md shows a maintainer of the reference declare the same
+    argument types as the package's own binding (which the header test above pins)."""
+    import ctypes
+    text = open(os.path.join(os.path.dirname(HEADER), "..", "INTEGRATION.md")).read()
+    alias = {"vp": ctypes.c_void_p, "c_void_p": ctypes.c_void_p, "i64": ctypes.c_int64,
+             "c_int64": ctypes.c_int64, "f32": ctypes.c_float, "c_float": ctypes.c_float,
+             "c_int": ctypes.c_int, "c_size_t": ctypes.c_size_t, "Tensor4": _lib.Tensor4}
+    found = re.findall(r"\b_?lib\.(race_\w+)\.argtypes = \[([^\]]*)\]", text, flags=re.S)
+    assert len(found) >= 4
+    for name, args in found:
+        got = [alias[a.strip().replace("ctypes.", "")] for a in args.split(",") if a.strip()]
+        assert got == list(_lib.SIGNATURES[name][1]), name
+    for name, res in re.findall(r"\b_?lib\.(race_\w+)\.restype = ([\w.]+)", text):
+        assert alias.get(res.replace("ctypes.", ""), getattr(ctypes, res.replace("ctypes.", ""), None)) \
+            == _lib.SIGNATURES[name][0], name
