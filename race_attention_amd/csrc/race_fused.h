@@ -584,18 +584,9 @@ __global__ __launch_bounds__(NW * 64) void race_fused_fwd_totals(const ScanParam
     }
 }
 
-// Wave-uniform copy of a pointer or 64-bit integer that holds the same value in every lane (a
+// Wave-uniform copy of a 64-bit integer (or address) that holds the same value in every lane (a
 // per-wave choice between kernel arguments), so that the address arithmetic on it runs on the
 // scalar unit.
-template <class T>
-RACE_DEV T *uniform_ptr(T *p)
-{
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<T *>(((uint64_t)hi << 32) | lo);
-}
-
 RACE_DEV int64_t uniform_i64(int64_t x)
 {
     const uint64_t v = (uint64_t)x;
@@ -606,9 +597,9 @@ RACE_DEV int64_t uniform_i64(int64_t x)
 
 // Row loads of a group of four waves (the movers of the wave-specialised backward kernels, the
 // forward readout's workgroup): one 16-byte chunk of each of two C x 64 bf16 token tiles per
-// thread, from two [B][H][T][D] tensors (which may be a per-wave choice). Their block row-0 pointers and row strides are made wave-uniform once,
-// so a sub-chunk's row-0 address is scalar arithmetic and a thread's chunk is that address plus a
-// 32-bit byte offset (the global_load form with a scalar base): a clamp and a 24-bit multiply-add
+// thread, from two [B][H][T][D] tensors (which may be a per-wave choice). Their block row-0
+// pointers and row strides are made wave-uniform once, so a sub-chunk's row-0 address is scalar
+// arithmetic and a thread's chunk is that address plus a 32-bit byte offset (the global_load form with a scalar base): a clamp and a 24-bit multiply-add
 // per load instead of 64-bit address arithmetic on every lane. Rows at and beyond nv (the valid
 // rows of the sub-chunk) re-read row nv - 1. Needs row strides below 2^24 elements (checked on
 // the host), so row * stride + column stays below 2^29 elements and its byte offset in 32 bits.
